@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path on one MI355X.
+
+Headline (``value``): W4A16 GEMV, M=1, K=4096, N=14336, group 128 (BASELINE
+configs[2]) in GB/s of algorithmic bytes, with every input resident in HBM and
+the weight sets rotated so that the 256 MB Infinity Cache cannot serve them.
+The other BASELINE configurations (W4A16 M=8/32/128, W8A16, dense 512^3,
+FlashAttention fwd, KDA) are measured in the same run and reported under
+``workloads``.
+
+A "step" is one call of the hot-path op on one batch of synthetic input.
+Timing: W untimed warm-up steps, then K steps bracketed by synchronisation,
+timed with HIP events recorded on the stream the kernels are launched on.
+The K steps are captured into one HIP graph and replayed (how a decode loop
+issues them); the same K steps enqueued eagerly from Python are reported as
+``eager_us_per_call``.
+
+The CPU baseline times the CPU oracle (a numpy restatement of the reference's
+arithmetic) on a bounded sample of the same workload on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME ...]
+                       [--no-cpu] [--list]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "triton-metal_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "W4A16 GEMM GB/s & %HBM roofline (M=1..128); FA-fwd TFLOP/s & %MFMA peak"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_PEAK_TFLOPS = 2516.6      # MI355X dense fp16/bf16 MFMA, TFLOP/s
+ROTATE_BYTES = 600 << 20       # > 256 MB Infinity Cache
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# workloads: each returns dict(launches, bytes, flops, bound, config, dtype)
+# ---------------------------------------------------------------------------
+def _nsets(per_set_bytes):
+    return max(2, min(64, -(-ROTATE_BYTES // max(1, per_set_bytes))))
+
+
+def w4a16(dev, M, K=4096, N=14336, G=128):
+    import torch
+    import triton_metal_amd as tm
+    ng = K // G
+    per = N * K // 2 + 2 * N * ng * 2
+    R = _nsets(per)
+    g = torch.Generator(device=dev).manual_seed(2)
+    Ws = [torch.randint(0, 256, (N, K // 2), device=dev, dtype=torch.uint8, generator=g)
+          for _ in range(R)]
+    Ss = [(torch.rand(N, ng, device=dev, generator=g) * 0.019 + 0.001).half() for _ in range(R)]
+    Zs = [torch.randint(0, 16, (N, ng), device=dev, generator=g).half() for _ in range(R)]
+    x = torch.randn(M, K, device=dev, generator=g).half()
+    y = torch.empty(M, N, device=dev, dtype=torch.float16)
+    launches = [tm.plan_int4_matmul(x, Ws[j], y, Ss[j], Zs[j], M, N, K, G) for j in range(R)]
+
+    nbytes = N * K // 2 + 2 * N * ng + 2 * N * ng + 2 * M * K + 2 * M * N
+    flops = 2 * M * N * K
+    bound = "hbm" if M <= 32 else "mfma"
+    return dict(launches=launches, keep=(Ws, Ss, Zs, x, y), bytes=nbytes, flops=flops,
+                bound=bound, dtype="fp16",
+                config={"workload": f"w4a16_m{M}", "M": M, "K": K, "N": N, "group_size": G,
+                        "weight_sets_rotated": R})
+
+
+def w8a16(dev, M, K=4096, N=11008):
+    import torch
+    import triton_metal_amd as tm
+    per = N * K + 2 * N
+    R = _nsets(per)
+    g = torch.Generator(device=dev).manual_seed(3)
+    Ws = [torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8, generator=g)
+          for _ in range(R)]
+    Ss = [(torch.rand(N, device=dev, generator=g) * 0.019 + 0.001).half() for _ in range(R)]
+    x = torch.randn(M, K, device=dev, generator=g).half()
+    y = torch.empty(M, N, device=dev, dtype=torch.float16)
+    launches = [tm.plan_int8_matmul(x, Ws[j], y, Ss[j], None, M, N, K) for j in range(R)]
+
+    nbytes = N * K + 2 * N + 2 * M * K + 2 * M * N
+    flops = 2 * M * N * K
+    bound = "hbm" if M <= 32 else "mfma"
+    return dict(launches=launches, keep=(Ws, Ss, x, y), bytes=nbytes, flops=flops,
+                bound=bound, dtype="fp16",
+                config={"workload": f"w8a16_m{M}", "M": M, "K": K, "N": N,
+                        "weight_sets_rotated": R})
+
+
+def dense(dev, M=512, N=512, K=512):
+    import torch
+    import triton_metal_amd as tm
+    g = torch.Generator(device=dev).manual_seed(1)
+    A = torch.randn(M, K, device=dev, generator=g).half()
+    B = torch.randn(K, N, device=dev, generator=g).half()
+    C = torch.empty(M, N, device=dev, dtype=torch.float16)
+    launches = [tm.plan_matmul(A, B, C, M, N, K)]
+    return dict(launches=launches, keep=(A, B, C), bytes=2 * (M * K + K * N + M * N),
+                flops=2 * M * N * K, bound="mfma", dtype="fp16", config={"workload": f"dense_{M}x{N}x{K}", "M": M, "N": N, "K": K})
+
+
+WORKLOADS = {
+    "w4a16_m1": lambda d: w4a16(d, 1),
+    "w4a16_m8": lambda d: w4a16(d, 8),
+    "w4a16_m32": lambda d: w4a16(d, 32),
+    "w4a16_m128": lambda d: w4a16(d, 128),
+    "w8a16_m1": lambda d: w8a16(d, 1),
+    "w8a16_m16": lambda d: w8a16(d, 16),
+    "w8a16_m128": lambda d: w8a16(d, 128),
+    "dense_512": lambda d: dense(d),
+    "dense_4096": lambda d: dense(d, 4096, 4096, 4096),
+}
+HEADLINE = "w4a16_m1"
+
+
+def time_workload(w, steps, warmup, graph=True):
+    """Average ms per step: eagerly enqueued, and replayed from one HIP graph
+    holding the K steps (the launch pattern of a captured decode loop)."""
+    import torch
+    L = w["launches"]
+    R = len(L)
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        L[i % R]()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        L[(warmup + i) % R]()
+    end.record(stream)
+    torch.cuda.synchronize()
+    eager_ms = start.elapsed_time(end) / steps
+    if not graph:
+        return eager_ms, eager_ms
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=cap):
+        sp = torch.cuda.current_stream().cuda_stream
+        for i in range(steps):
+            L[i % R](sp)
+    g.replay()
+    torch.cuda.synchronize()
+    start.record(stream)
+    g.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    graph_ms = start.elapsed_time(end) / steps
+    del g
+    return graph_ms, eager_ms
+
+
+def summarize(w, ms, eager_ms):
+    s = ms * 1e-3
+    gbs = w["bytes"] / s / 1e9
+    tfl = w["flops"] / s / 1e12
+    if w["bound"] == "hbm":
+        roof = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(gbs / HBM_PEAK_GBS, 4))
+    else:
+        roof = dict(bound="mfma", achieved=round(tfl, 2), peak=MFMA_PEAK_TFLOPS, unit="TFLOP/s",
+                    frac=round(tfl / MFMA_PEAK_TFLOPS, 4))
+    return dict(us_per_call=round(ms * 1e3, 3), eager_us_per_call=round(eager_ms * 1e3, 3),
+                GBps=round(gbs, 1), TFLOPs=round(tfl, 3), roofline=roof, config=w["config"])
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle on a bounded sample of the headline workload
+# ---------------------------------------------------------------------------
+def cpu_baseline(target_s=12.0):
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    import oracle
+    cores = len(os.sched_getaffinity(0))
+    K, G, M = 4096, 128, 1
+    N = 14336 // 4  # sample: a quarter of the output columns per call
+    rng = np.random.default_rng(0)
+    packed = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    s = (rng.random((N, K // G)) * 0.019 + 0.001).astype(np.float16).astype(np.float32)
+    z = rng.integers(0, 16, (N, K // G)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
+    nbytes = N * K // 2 + 4 * N * (K // G) + 2 * M * K + 2 * M * N
+    with threadpool_limits(cores):
+        oracle.int4_matmul(x, packed, s, z, M, N, K, G)  # warm-up
+        times = []
+        t_end = time.perf_counter() + target_s
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            oracle.int4_matmul(x, packed, s, z, M, N, K, G)
+            times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=cores, kind="port",
+                sample=f"oracle.int4_matmul (numpy unpack + fp32 dequant + fp64 matmul), "
+                       f"M=1 K=4096 N={N} (1/4 of the columns), {len(times)} reps, median "
+                       f"{med * 1e3:.1f} ms; elementwise numpy single-threaded, BLAS "
+                       f"{cores} threads")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", nargs="*", default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--list", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eagerly enqueued calls only (no HIP graph)")
+    args = ap.parse_args()
+    if args.list:
+        print("\n".join(WORKLOADS))
+        return 0
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(every kernel here runs on one GPU's share; see DESIGN.md for sharding)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    names = args.only or list(WORKLOADS)
+    if HEADLINE not in names:
+        names = [HEADLINE] + names
+    results = {}
+    for name in names:
+        log(f"[bench] {name}: setup")
+        w = WORKLOADS[name](dev)
+        ms, eager_ms = time_workload(w, args.steps, args.warmup, graph=not args.eager)
+        results[name] = summarize(w, ms, eager_ms)
+        log(f"[bench] {name}: {results[name]['us_per_call']} us/call "
+            f"{results[name]['GBps']} GB/s {results[name]['TFLOPs']} TFLOP/s")
+        del w
+        torch.cuda.empty_cache()
+        if name == HEADLINE:
+            head_ms = ms
+
+    head = results[HEADLINE]
+    line = {
+        "metric": METRIC,
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head_ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "timing": "eager" if args.eager else "K steps replayed from one HIP graph; "
+                  "eager_us_per_call is the same loop enqueued from Python",
+        "config": head["config"],
+        "roofline": dict(head["roofline"], traffic=None),
+        "workloads": {k: v for k, v in results.items() if k != HEADLINE},
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

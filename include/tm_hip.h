@@ -1,0 +1,132 @@
+/*
+ * tm_hip.h -- C ABI of the MI355X (gfx950) kernel library libtm_hip.so.
+ *
+ * Plain C: pointers, sizes and ints only.  Every function returns 0 on
+ * success; a positive value is the hipError_t that the HIP runtime returned,
+ * a negative value is one of the TM_ERR_* codes below.  tm_last_error() gives
+ * a thread-local message for the last failure on the calling thread.
+ *
+ * All typed entry points are asynchronous on `stream` (a hipStream_t passed as
+ * void*, NULL = the null stream) and launch on the calling thread's current
+ * HIP device.  Every buffer is allocated and owned by the caller; the library
+ * owns only the code objects it loads.
+ *
+ * The library binds to the HIP runtime already loaded in the process (for
+ * example PyTorch's), and loads the system libamdhip64 only when none is.
+ */
+#ifndef TM_HIP_H
+#define TM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+/* ---- error codes --------------------------------------------------------- */
+#define TM_OK 0
+#define TM_ERR_INVALID_ARG (-1)   /* bad shape, dtype, pointer or size */
+#define TM_ERR_UNSUPPORTED (-2)   /* valid request this build cannot serve */
+#define TM_ERR_NO_RUNTIME (-3)    /* no usable HIP runtime / no GPU */
+#define TM_ERR_NOT_FOUND (-4)     /* kernel name not present in a module */
+#define TM_ERR_LOAD (-5)          /* code object rejected by the runtime */
+
+/* ---- dtype codes ----------------------------------------------------------- */
+#define TM_DT_NONE (-1) /* absent optional tensor (e.g. zero-points) */
+#define TM_DT_F32 0
+#define TM_DT_F16 1
+#define TM_DT_BF16 2
+#define TM_DT_U8 3
+
+/* ---- library / device ------------------------------------------------------ */
+/* Resolve the HIP runtime.  Called implicitly by every entry point. */
+int tm_init(void);
+/* Message for the last failure on this thread ("" if none). */
+const char* tm_last_error(void);
+/* Library version string. */
+const char* tm_version(void);
+/* Device properties: gcn arch name (e.g. "gfx950:sramecc+:xnack-"), CU count,
+ * max shared memory per block, L2 bytes.  Any out pointer may be NULL.
+ * Replaces triton_metal/backend/device_detect.py:239 get_device_info(). */
+int tm_device_info(int device, char* arch, size_t arch_len, int* cu_count,
+                   int* max_shared_per_block, int* l2_bytes);
+/* Number of built-in kernels and the name of kernel i (for introspection). */
+int tm_num_builtin_modules(void);
+const char* tm_builtin_module_name(int i);
+
+/* ---- generic code-object loader / launcher --------------------------------
+ * Replaces MetalUtils.load_binary (triton_metal/backend/driver.py:114-162),
+ * which returns (library, pipeline_state, n_regs, n_spills, n_max_threads),
+ * and MetalUtils.launch (driver.py:164-227).  Unlike the Metal path the launch
+ * does not wait: call tm_synchronize to block. */
+typedef struct tm_module_opaque* tm_module_t;
+typedef struct tm_function_opaque* tm_function_t;
+
+/* Load a gfx950 code object (hsaco bytes) on the current device. */
+int tm_module_load(const void* image, size_t nbytes, tm_module_t* out);
+int tm_module_unload(tm_module_t module);
+/* Look up `name`; the out values mirror load_binary's n_regs, n_spills
+ * (private segment bytes per lane) and n_max_threads.  NULL outs ignored. */
+int tm_module_get_function(tm_module_t module, const char* name, tm_function_t* out,
+                           int* n_regs, int* n_spills, int* max_threads, int* shared_bytes);
+/* Launch with kernel arguments as an array of pointers to each argument
+ * (hipModuleLaunchKernel's kernelParams convention). */
+int tm_launch(tm_function_t fn, unsigned grid_x, unsigned grid_y, unsigned grid_z,
+              unsigned block_x, unsigned block_y, unsigned block_z, unsigned shared_bytes,
+              void* stream, void** args);
+int tm_synchronize(void* stream);
+
+/* ---- weight-only quantized matmul --------------------------------------------
+ * Buffer order follows the reference template ABI
+ *   input, weight, output, scales, zeros, M, N, K
+ * of make_int8_matmul_kernel (triton_metal/codegen/_msl_templates.py:2652-2661)
+ * and make_int4_matmul_kernel (_msl_templates.py:2704-2713, group size a
+ * template parameter there, an argument here).
+ *
+ *   output[m, n] = sum_k input[m, k] * (q(n, k) - zeros[g]) * scales[g]
+ *
+ * int8: weight int8 [N, K]; scales/zeros [N] (per output channel).
+ * int4: weight bytes [N, K/2] (even k in the low nibble; equivalently uint32
+ *       [N, K/8] with nibble i of word j = k 8j+i); scales/zeros
+ *       [N, ceil(K/group_size)].
+ * input/output: [M, K] / [M, N] row-major in act_dtype (F32, F16 or BF16).
+ * scales: F32/F16/BF16.  zeros: TM_DT_NONE (zero), F32/F16/BF16 or U8.
+ * Accumulation is fp32.  fp16/bf16 activations with scales in the activation
+ * dtype run on MFMA kernels; other combinations on an fp32 kernel. */
+int tm_int8_matmul(const void* input, const void* weight, void* output, const void* scales,
+                   const void* zeros, int M, int N, int K, int act_dtype, int scale_dtype,
+                   int zero_dtype, void* stream);
+int tm_int4_matmul(const void* input, const void* weight, void* output, const void* scales,
+                   const void* zeros, int M, int N, int K, int group_size, int act_dtype,
+                   int scale_dtype, int zero_dtype, void* stream);
+/* Dequantised weight tile out[n, k] = round_out((float(q) - z) * s), the
+ * per-element arithmetic of _msl_templates.py:2671 (int8) / 2738-2739 (int4).
+ * qbits 4 or 8; out_dtype F32/F16/BF16. */
+int tm_wq_dequant(const void* weight, const void* scales, const void* zeros, void* out, int N,
+                  int K, int group_size, int qbits, int scale_dtype, int zero_dtype,
+                  int out_dtype, void* stream);
+
+/* ---- dense matmul -----------------------------------------------------------
+ * C[M, N] = A[M, K] @ B[K, N], row-major with leading dimensions lda/ldb/ldc
+ * (elements).  Replaces make_matmul_kernel (_msl_templates.py:447-585; buffer
+ * order A, B, C, M, N, K) and make_simdgroup_matmul_kernel (3501-3667; fp16
+ * in, fp32 out).  in_dtype F16/BF16 (MFMA) or F32; out_dtype F32/F16/BF16. */
+int tm_matmul(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb,
+              int ldc, int in_dtype, int out_dtype, void* stream);
+/* output[M, N] = input[M, K] @ weight[N, K]^T (+ bias[N]); bias may be NULL.
+ * Replaces make_fused_linear_kernel (_msl_templates.py:4013-4135; buffer order
+ * input, weight, C, [bias], M, N, K). */
+int tm_linear(const void* input, const void* weight, const void* bias, void* output, int M,
+              int N, int K, int in_dtype, int out_dtype, void* stream);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+#ifdef __cplusplus
+}
+#endif
+#endif /* TM_HIP_H */

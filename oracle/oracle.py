@@ -1,0 +1,232 @@
+"""CPU oracle for the hot path -- TEST INFRASTRUCTURE ONLY.
+
+This module restates, in numpy, the arithmetic of the reference kernels the
+library replaces.  It exists to check the HIP kernels: only tests/,
+__graft_entry__.smoke() and bench.py's CPU-baseline leg may import it, and
+never as the thing measured or shipped.  The product path (triton_metal_amd)
+must not import it.
+
+Every function cites the reference file:line it follows (paths relative to the
+reference tree bledden/triton-metal).  How each function is pinned (golden
+vectors / known-answer tests / closed forms) is listed in PINNING below; the
+tests in tests/test_oracle_*.py carry out those checks.
+
+KDA has no counterpart in the reference (no linear attention anywhere in
+bledden/triton-metal), so kda_recurrent / kda_chunked restate the published
+gated delta rule of Kimi Delta Attention; they are pinned only by closed forms
+and by agreeing with each other.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+PINNING = {
+    "unpack_int4": "hand-built nibble words (order), ported KATs seeds 7070/44",
+    "pack_int4": "round trip with unpack_int4; packing of tests/test_emitter.py:3027-3032",
+    "dequant_int4": "closed form per-group scales (group index), z=q -> 0, KATs 7070/44",
+    "dequant_int8": "closed form, KATs 8888/66",
+    "int4_matmul": "KATs 7070/44 (expected values of the reference tests), brute force",
+    "int8_matmul": "KATs 8888/66, brute force",
+    "matmul": "KATs 42/789/101/202/303/404/505/707/808, I@B=B, brute-force triple loop",
+    "flash_attention": "KATs 555/666/1234/123, torch SDPA (CPU, fp64), logsumexp, "
+                       "uniform-score and causal-row-0 closed forms",
+    "kda_recurrent": "closed forms (beta=0, T=1, orthonormal retrieval, memoryless); "
+                     "agreement with kda_chunked (parity unpinned by the reference)",
+    "kda_chunked": "agreement with kda_recurrent; same closed forms (parity unpinned by "
+                   "the reference)",
+}
+
+
+# ---------------------------------------------------------------------------
+# int4 / int8 weight-only quantisation
+# ---------------------------------------------------------------------------
+def unpack_int4(packed: np.ndarray, K: int) -> np.ndarray:
+    """[N, K/2] bytes -> [N, K] nibbles, even k in the low nibble.
+
+    _msl_templates.py:2724-2732: ``byte = weight[col*(K/2) + k/2]``;
+    ``w4 = k%2==0 ? byte & 0xF : (byte >> 4) & 0xF``."""
+    b = np.ascontiguousarray(packed).view(np.uint8).reshape(-1, K // 2)
+    out = np.empty((b.shape[0], K), dtype=np.uint8)
+    out[:, 0::2] = b & 0x0F
+    out[:, 1::2] = (b >> 4) & 0x0F
+    return out
+
+
+def pack_int4(q: np.ndarray) -> np.ndarray:
+    """[N, K] values 0..15 -> [N, K/2] bytes, ``lo | (hi << 4)``.
+
+    tests/test_emitter.py:3027-3032 and 6198-6204."""
+    q = np.asarray(q, dtype=np.uint8)
+    return (q[:, 0::2] & 0x0F) | ((q[:, 1::2] & 0x0F) << 4)
+
+
+def dequant_int4(packed, scales, zeros, K: int, group_size: int) -> np.ndarray:
+    """w[n, k] = (float(q) - z[n, k/G]) * s[n, k/G] in fp32.
+
+    _msl_templates.py:2734-2739 (``group_idx = k / GROUP_SIZE``;
+    ``n_groups = ceil(K / G)``; ``w = (float(w4) - z) * s``)."""
+    q = unpack_int4(packed, K).astype(np.float32)
+    N = q.shape[0]
+    ng = (K + group_size - 1) // group_size
+    s = np.asarray(scales, dtype=np.float32).reshape(N, ng)
+    z = (np.zeros((N, ng), np.float32) if zeros is None
+         else np.asarray(zeros, dtype=np.float32).reshape(N, ng))
+    g = np.arange(K) // group_size
+    return ((q - z[:, g]) * s[:, g]).astype(np.float32)
+
+
+def dequant_int8(weight, scales, zeros) -> np.ndarray:
+    """w[n, k] = (float(W[n, k]) - z[n]) * s[n] in fp32 (_msl_templates.py:2671)."""
+    w = np.asarray(weight).view(np.int8).astype(np.float32)
+    N = w.shape[0]
+    s = np.asarray(scales, dtype=np.float32).reshape(N, 1)
+    z = np.zeros((N, 1), np.float32) if zeros is None else np.asarray(
+        zeros, dtype=np.float32).reshape(N, 1)
+    return ((w - z) * s).astype(np.float32)
+
+
+def int4_matmul(x, packed, scales, zeros, M, N, K, group_size) -> np.ndarray:
+    """out[M, N] = x @ dequant_int4(...)^T, accumulated in float64.
+
+    make_int4_matmul_kernel, _msl_templates.py:2704-2744 (the reference
+    accumulates in fp32 per output; fp64 here is the tighter answer both are
+    checked against)."""
+    w = dequant_int4(packed, scales, zeros, K, group_size).astype(np.float64)
+    return np.asarray(x, dtype=np.float64).reshape(M, K) @ w.T
+
+
+def int8_matmul(x, weight, scales, zeros, M, N, K) -> np.ndarray:
+    """out[M, N] = x @ dequant_int8(...)^T (_msl_templates.py:2652-2678)."""
+    w = dequant_int8(np.asarray(weight).reshape(N, K), scales, zeros).astype(np.float64)
+    return np.asarray(x, dtype=np.float64).reshape(M, K) @ w.T
+
+
+# ---------------------------------------------------------------------------
+# dense matmul
+# ---------------------------------------------------------------------------
+def matmul(A, B) -> np.ndarray:
+    """C = A @ B with A [M, K], B [K, N] row-major, float64 accumulation.
+
+    make_matmul_kernel _msl_templates.py:512-585 (``acc += tileA[row][k] *
+    tileB[k][col]``); make_simdgroup_matmul_kernel 3501-3667 (same product)."""
+    return np.asarray(A, dtype=np.float64) @ np.asarray(B, dtype=np.float64)
+
+
+def linear(x, W, bias=None) -> np.ndarray:
+    """out = x @ W^T (+ bias) (make_fused_linear_kernel, _msl_templates.py:4013-4135)."""
+    out = np.asarray(x, dtype=np.float64) @ np.asarray(W, dtype=np.float64).T
+    if bias is not None:
+        out = out + np.asarray(bias, dtype=np.float64)[None, :]
+    return out
+
+
+# ---------------------------------------------------------------------------
+# flash attention forward
+# ---------------------------------------------------------------------------
+def flash_attention(Q, K, V, scale: float, causal: bool):
+    """Attention over [..., S, D] heads in float64; returns (O, LSE).
+
+    make_flash_attention_kernel _msl_templates.py:1568-1767: scores
+    ``S = Q.K^T * scale``; a score is -inf when ``kv_pos >= seq_len`` or, if
+    causal, ``kv_pos > q_pos`` (1610-1619); softmax by row; ``O /= l`` only when
+    ``l > 0`` (1747-1754), so a fully masked row yields O = 0.  LSE (natural
+    log, no reference counterpart) = logsumexp of the masked scores, -inf for a
+    fully masked row."""
+    q = np.asarray(Q, dtype=np.float64)
+    k = np.asarray(K, dtype=np.float64)
+    v = np.asarray(V, dtype=np.float64)
+    s = np.einsum("...qd,...kd->...qk", q, k) * scale
+    Sq, Sk = s.shape[-2], s.shape[-1]
+    if causal:
+        mask = np.arange(Sk)[None, :] > np.arange(Sq)[:, None]
+        s = np.where(mask, -np.inf, s)
+    m = np.max(s, axis=-1, keepdims=True)
+    m_safe = np.where(np.isfinite(m), m, 0.0)
+    p = np.exp(s - m_safe)
+    l = np.sum(p, axis=-1, keepdims=True)
+    o = np.einsum("...qk,...kd->...qd", p, v)
+    o = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
+    with np.errstate(divide="ignore"):
+        lse = np.where(l[..., 0] > 0, m_safe[..., 0] + np.log(l[..., 0]), -np.inf)
+    return o, lse
+
+
+# ---------------------------------------------------------------------------
+# KDA (Kimi Delta Attention) chunked gated delta rule -- no reference code
+# ---------------------------------------------------------------------------
+def kda_recurrent(q, k, v, g, beta, scale=None, initial_state=None):
+    """Token-by-token gated delta rule with per-key-channel decay, float64.
+
+    Layout [B, T, H, D] (q, k: Dk; v: Dv), g [B, T, H, Dk] (log decay),
+    beta [B, T, H].  Per head, S in R^{Dk x Dv}:
+        S <- diag(exp(g_t)) S
+        S <- S + beta_t k_t (v_t - S^T k_t)^T
+        o_t = S^T (q_t * scale)
+    Returns (o [B, T, H, Dv], S_T [B, H, Dk, Dv])."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    g = np.asarray(g, np.float64)
+    beta = np.asarray(beta, np.float64)
+    B, T, H, Dk = q.shape
+    Dv = v.shape[-1]
+    if scale is None:
+        scale = Dk ** -0.5
+    S = (np.zeros((B, H, Dk, Dv)) if initial_state is None
+         else np.array(initial_state, np.float64).reshape(B, H, Dk, Dv))
+    o = np.zeros((B, T, H, Dv))
+    for t in range(T):
+        S = S * np.exp(g[:, t])[..., None]
+        kt = k[:, t]
+        u = beta[:, t][..., None] * (v[:, t] - np.einsum("bhkv,bhk->bhv", S, kt))
+        S = S + np.einsum("bhk,bhv->bhkv", kt, u)
+        o[:, t] = np.einsum("bhkv,bhk->bhv", S, q[:, t] * scale)
+    return o, S
+
+
+def kda_chunked(q, k, v, g, beta, scale=None, initial_state=None, chunk_size=64):
+    """Chunk-parallel form of kda_recurrent (independent restatement), float64.
+
+    Within a chunk with inclusive cumulative log decay G_t (per channel) and
+    pairwise decays D[t, s, c] = exp(G_tc - G_sc) for s <= t (never > 1):
+        A[t, s]   = beta_t sum_c k_tc k_sc D[t, s, c]   (s < t),  T = (I + A)^-1
+        Aqk[t, s] = sum_c q_tc k_sc D[t, s, c] * scale  (s <= t)
+        U  = T diag(beta) (V - (k * exp(G)) S0)
+        O  = (q * scale * exp(G)) S0 + Aqk U
+        S1 = diag(exp(G_C)) S0 + (k * exp(G_C - G))^T U
+    The pairwise form never multiplies exp(G) by exp(-G), so it stays finite
+    for any decay."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    g = np.asarray(g, np.float64)
+    beta = np.asarray(beta, np.float64)
+    B, T, H, Dk = q.shape
+    Dv = v.shape[-1]
+    if scale is None:
+        scale = Dk ** -0.5
+    S = (np.zeros((B, H, Dk, Dv)) if initial_state is None
+         else np.array(initial_state, np.float64).reshape(B, H, Dk, Dv))
+    o = np.zeros((B, T, H, Dv))
+    for b in range(B):
+        for h in range(H):
+            St = S[b, h].copy()
+            for c0 in range(0, T, chunk_size):
+                c1 = min(T, c0 + chunk_size)
+                kc, vc, qc = k[b, c0:c1, h], v[b, c0:c1, h], q[b, c0:c1, h] * scale
+                bc = beta[b, c0:c1, h]
+                G = np.cumsum(g[b, c0:c1, h], axis=0)
+                n = c1 - c0
+                incl = np.tril(np.ones((n, n), bool))
+                expo = np.where(incl[:, :, None], G[:, None, :] - G[None, :, :], -np.inf)
+                Dts = np.exp(expo)                                   # [t, s, c]
+                A = np.where(np.tril(incl, -1),
+                             bc[:, None] * np.einsum("tc,sc,tsc->ts", kc, kc, Dts), 0.0)
+                Aqk = np.einsum("tc,sc,tsc->ts", qc, kc, Dts)
+                Tm = np.linalg.inv(np.eye(n) + A)
+                eG = np.exp(G)
+                U = Tm @ (bc[:, None] * (vc - (kc * eG) @ St))
+                o[b, c0:c1, h] = (qc * eG) @ St + Aqk @ U
+                St = eG[-1][:, None] * St + (kc * np.exp(G[-1][None, :] - G)).T @ U
+            S[b, h] = St
+    return o, S

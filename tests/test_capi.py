@@ -1,0 +1,75 @@
+"""The C ABI library loads and exports what include/tm_hip.h declares (CPU only).
+
+No compute is launched: only symbol presence, metadata calls and argument
+validation that fails before any HIP call.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+LIB = ROOT / "triton-metal_amd" / "triton_metal_amd" / "libtm_hip.so"
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(tm_\w+)\s*\(", text, flags=re.M))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for n in ["tm_init", "tm_last_error", "tm_module_load", "tm_launch", "tm_int4_matmul",
+              "tm_int8_matmul", "tm_matmul", "tm_linear", "tm_wq_dequant"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    assert LIB.exists(), "libtm_hip.so not built (run __graft_entry__.build())"
+    lib = ctypes.CDLL(str(LIB))
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_header():
+    import triton_metal_amd._lib as L
+    assert set(declared_functions()) <= set(L.SIGNATURES)
+
+
+def test_metadata_calls_without_gpu():
+    import triton_metal_amd._lib as L
+    lib = L.lib()
+    assert b"gfx950" in lib.tm_version()
+    assert lib.tm_num_builtin_modules() >= 2
+    names = {lib.tm_builtin_module_name(i).decode() for i in range(lib.tm_num_builtin_modules())}
+    assert {"wq_gemm", "gemm"} <= names
+    assert lib.tm_builtin_module_name(99) is None
+
+
+def test_argument_validation_before_any_hip_call():
+    import triton_metal_amd._lib as L
+    lib = L.lib()
+    p = ctypes.c_void_p(16)
+    # odd K for int4
+    rc = lib.tm_int4_matmul(p, p, p, p, None, 1, 16, 7, 128, L.TM_DT_F16, L.TM_DT_F16,
+                            L.TM_DT_NONE, None)
+    assert rc == L.TM_ERR_INVALID_ARG and "even" in L.last_error()
+    # bad dtype
+    rc = lib.tm_int8_matmul(p, p, p, p, None, 1, 16, 64, 7, L.TM_DT_F16, L.TM_DT_NONE, None)
+    assert rc == L.TM_ERR_INVALID_ARG
+    # zeros dtype given but NULL pointer
+    rc = lib.tm_int8_matmul(p, p, p, p, None, 1, 16, 64, L.TM_DT_F16, L.TM_DT_F16,
+                            L.TM_DT_F16, None)
+    assert rc == L.TM_ERR_INVALID_ARG and "zeros" in L.last_error()
+    # leading dimension too small
+    rc = lib.tm_matmul(p, p, p, 4, 4, 4, 2, 4, 4, L.TM_DT_F16, L.TM_DT_F16, None)
+    assert rc == L.TM_ERR_INVALID_ARG
+    # empty problems are a no-op success
+    assert lib.tm_matmul(p, p, p, 0, 4, 4, 4, 4, 4, L.TM_DT_F16, L.TM_DT_F16, None) == 0
+    with pytest.raises(RuntimeError):
+        L.check(L.TM_ERR_INVALID_ARG, "probe")

@@ -1,0 +1,118 @@
+"""Dense matmul / fused linear parity on the GPU against the oracle.
+
+fp16/bf16 outputs within atol 2e-2 / rtol 1e-2 of the oracle's fp64 product
+of the same (rounded) inputs; the reference's known-answer tests with the
+reference's own tolerances.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import triton_metal_amd as tm
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 2e-2, 1e-2
+
+MATMUL_KATS = ["matmul_seed789", "matmul_seed101r", "matmul_seed202", "matmul_seed42",
+               "matmul_seed101g", "simdgroup_seed88", "simdgroup_seed303", "simdgroup_seed404",
+               "simdgroup_seed505", "simdgroup_f16_seed707", "simdgroup_f16_seed808"]
+
+
+@pytest.mark.parametrize("name", MATMUL_KATS)
+@pytest.mark.parametrize("out_dtype", ["same", "f32"])
+def test_matmul_reference_kat(kats, dev, name, out_dtype):
+    m, a = kats[name]
+    M, N, K = m["M"], m["N"], m["K"]
+    dt = torch.float16 if m["in_dtype"] == "fp16" else torch.float32
+    A = torch.tensor(a["A"], dtype=dt, device=dev).reshape(M, K)
+    B = torch.tensor(a["B"], dtype=dt, device=dev).reshape(K, N)
+    C = torch.empty(M, N, dtype=dt if out_dtype == "same" else torch.float32, device=dev)
+    kern = (tm.make_simdgroup_matmul_kernel(m["in_dtype"]) if name.startswith("simdgroup")
+            else tm.make_matmul_kernel())
+    kern(A, B, C, M, N, K)
+    got = C.float().cpu().numpy().ravel()
+    sel = np.zeros((M, N), bool)
+    sel[::m["spot"], ::m["spot"]] = True
+    err = np.abs(got - a["expected"])[sel.ravel()].max()
+    assert err < m["tol"]
+    # the same inputs through the MFMA path (fp16) stay inside the reference tolerance too
+    if dt == torch.float32:
+        A16, B16 = A.half(), B.half()
+        C16 = torch.empty(M, N, dtype=torch.float32, device=dev)
+        tm.matmul(A16, B16, C16, M, N, K)
+        ref = oracle.matmul(A16.float().cpu().numpy(), B16.float().cpu().numpy())
+        np.testing.assert_allclose(C16.cpu().numpy(), ref, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("name", ["linear_seed1111", "linear_seed2222"])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_fused_linear_reference_kat(kats, dev, name, dt):
+    m, a = kats[name]
+    M, N, K = m["M"], m["N"], m["K"]
+    x = torch.tensor(a["input"], dtype=dt, device=dev).reshape(M, K)
+    W = torch.tensor(a["weight"], dtype=dt, device=dev).reshape(N, K)
+    C = torch.empty(M, N, dtype=dt, device=dev)
+    if m["has_bias"]:
+        b = torch.tensor(a["bias"], dtype=dt, device=dev)
+        tm.make_fused_linear_kernel(True)(x, W, C, b, M, N, K)
+    else:
+        tm.make_fused_linear_kernel(False)(x, W, C, M, N, K)
+    err = np.abs(C.float().cpu().numpy().ravel() - a["expected"]).max()
+    assert err < (m["tol"] if dt == torch.float32 else max(m["tol"], 5e-2))
+
+
+def test_identity_fp16(dev):
+    # tests/test_emitter.py:4849 test_matmul_fp16_identity
+    A = torch.eye(16, dtype=torch.float16, device=dev)
+    B = torch.arange(1, 17, dtype=torch.float16, device=dev).repeat(16, 1).contiguous()
+    C = torch.empty(16, 16, dtype=torch.float16, device=dev)
+    tm.matmul(A, B, C, 16, 16, 16)
+    assert torch.equal(C, B)
+
+
+def _rand(shape, seed, dt):
+    return torch.randn(*shape, generator=torch.Generator().manual_seed(seed)).to(dt)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (256, 384, 1024), (100, 72, 40),
+                                   (1, 64, 64), (33, 8, 520), (2048, 2048, 256)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_matmul_shapes(dev, M, N, K, dt):
+    A, B = _rand((M, K), 1, dt), _rand((K, N), 2, dt)
+    C = torch.empty(M, N, dtype=dt, device=dev)
+    tm.matmul(A.to(dev), B.to(dev), C, M, N, K)
+    ref = oracle.matmul(A.float().numpy(), B.float().numpy())
+    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=ATOL * np.sqrt(K / 64),
+                               rtol=RTOL)
+
+
+def test_matmul_c1_fp16_fp32_out(dev):
+    M = N = K = 512
+    A, B = _rand((M, K), 3, torch.float16), _rand((K, N), 4, torch.float16)
+    C = torch.empty(M, N, dtype=torch.float32, device=dev)
+    tm.matmul(A.to(dev), B.to(dev), C, M, N, K)
+    ref = oracle.matmul(A.float().numpy(), B.float().numpy())
+    np.testing.assert_allclose(C.cpu().numpy(), ref, atol=1e-3, rtol=1e-4)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 128, 256), (1000, 520, 64), (7, 24, 48)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_linear_shapes(dev, M, N, K, bias):
+    x, W = _rand((M, K), 5, torch.float16), _rand((N, K), 6, torch.float16)
+    b = _rand((N,), 7, torch.float16) if bias else None
+    C = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.fused_linear(x.to(dev), W.to(dev), C, None if b is None else b.to(dev), M, N, K)
+    ref = oracle.linear(x.float().numpy(), W.float().numpy(),
+                        None if b is None else b.float().numpy())
+    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=ATOL * np.sqrt(K / 64),
+                               rtol=RTOL)
+
+
+def test_fp32_general_path(dev):
+    M, N, K = 13, 17, 19
+    A, B = _rand((M, K), 8, torch.float32), _rand((K, N), 9, torch.float32)
+    C = torch.empty(M, N, dtype=torch.float32, device=dev)
+    tm.matmul(A.to(dev), B.to(dev), C, M, N, K)
+    np.testing.assert_allclose(C.cpu().numpy(), oracle.matmul(A.numpy(), B.numpy()),
+                               atol=1e-5, rtol=1e-5)

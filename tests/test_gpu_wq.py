@@ -1,0 +1,217 @@
+"""W8A16 / W4A16 parity on the GPU against the oracle.
+
+Tolerances: fp16/bf16 outputs within atol 2e-2 / rtol 1e-2 of the oracle's
+fp32-dequant, fp64-accumulated result; dequantised weights bit-exact.
+The reference's own known-answer tests run with the reference's tolerances.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import triton_metal_amd as tm
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def make_int4_problem(M, N, K, G, seed, act=torch.float16, zeros="f16"):
+    g = _gen(seed)
+    x = torch.randn(M, K, generator=g).to(act)
+    q = torch.randint(0, 16, (N, K), generator=g, dtype=torch.uint8)
+    packed = torch.from_numpy(oracle.pack_int4(q.numpy()))
+    ng = (K + G - 1) // G
+    s = (torch.rand(N, ng, generator=g) * 0.019 + 0.001).to(act)
+    zi = torch.randint(0, 16, (N, ng), generator=g)
+    z = None if zeros is None else (zi.to(torch.uint8) if zeros == "u8" else zi.to(act))
+    return x, q, packed, s, z
+
+
+def make_int8_problem(M, N, K, seed, act=torch.float16, zeros=None):
+    g = _gen(seed)
+    x = torch.randn(M, K, generator=g).to(act)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s = (torch.rand(N, generator=g) * 0.019 + 0.001).to(act)
+    z = None if zeros is None else torch.randint(-3, 4, (N,), generator=g).to(act)
+    return x, w, s, z
+
+
+def np32(t):
+    return None if t is None else t.float().numpy()
+
+
+def check_close(got, ref, atol=ATOL, rtol=RTOL):
+    got = got.float().cpu().numpy().astype(np.float64)
+    np.testing.assert_allclose(got, ref, atol=atol, rtol=rtol)
+
+
+# --- reference known-answer tests ---------------------------------------------
+@pytest.mark.parametrize("name", ["int4_seed7070", "int4_seed44"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_int4_reference_kat(kats, dev, name, dtype):
+    m, a = kats[name]
+    M, N, K, G = m["M"], m["N"], m["K"], m["G"]
+    x = torch.tensor(a["input"], dtype=dtype, device=dev).reshape(M, K)
+    w = torch.tensor(a["packed"].astype(np.uint8), device=dev).reshape(N, K // 2)
+    s = torch.tensor(a["scales"], dtype=dtype, device=dev)
+    z = torch.tensor(a["zeros"], dtype=dtype, device=dev)
+    out = torch.empty(M, N, dtype=dtype, device=dev)
+    tm.make_int4_matmul_kernel(group_size=G)(x, w, out, s, z, M, N, K)
+    torch.cuda.synchronize()
+    err = np.abs(out.float().cpu().numpy().ravel() - a["expected"]).max()
+    assert err < m["tol"]
+    if dtype == torch.float32:
+        assert err < 1e-4
+
+
+@pytest.mark.parametrize("name", ["int8_seed8888", "int8_seed66"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_int8_reference_kat(kats, dev, name, dtype):
+    m, a = kats[name]
+    M, N, K = m["M"], m["N"], m["K"]
+    x = torch.tensor(a["input"], dtype=dtype, device=dev).reshape(M, K)
+    w = torch.tensor(a["weight"].astype(np.int8), device=dev).reshape(N, K)
+    s = torch.tensor(a["scales"], dtype=dtype, device=dev)
+    z = torch.tensor(a["zeros"], dtype=dtype, device=dev)
+    out = torch.empty(M, N, dtype=dtype, device=dev)
+    tm.make_int8_matmul_kernel()(x, w, out, s, z, M, N, K)
+    torch.cuda.synchronize()
+    err = np.abs(out.float().cpu().numpy().ravel() - a["expected"]).max()
+    assert err < m["tol"]
+    if dtype == torch.float32:
+        assert err < 1e-4
+
+
+# --- dequantised weights are bit-exact ------------------------------------------
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int4_dequant_tile_bit_exact(dev, act):
+    N, K, G = 96, 512, 128
+    _, q, packed, s, z = make_int4_problem(1, N, K, G, seed=11, act=act)
+    ref = torch.from_numpy(oracle.dequant_int4(packed.numpy(), np32(s), np32(z), K, G)).to(act)
+    got = tm.wq_dequant(packed.to(dev), s.to(dev), z.to(dev), N, K, 4, G, out_dtype=act)
+    assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("kind", ["skinny", "tiled"])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int4_in_register_dequant_bit_exact(dev, kind, act):
+    """One-hot activation rows make each output equal one dequantised weight,
+    so the GEMM's in-register dequantisation is compared bit for bit."""
+    N, K, G = 64, 512, 128
+    M = 8 if kind == "skinny" else 64
+    _, q, packed, s, z = make_int4_problem(M, N, K, G, seed=12, act=act)
+    ks = torch.randperm(K, generator=_gen(3))[:M]
+    x = torch.zeros(M, K, dtype=act)
+    x[torch.arange(M), ks] = 1.0
+    ref = torch.from_numpy(oracle.dequant_int4(packed.numpy(), np32(s), np32(z), K, G)).to(act)
+    out = torch.empty(M, N, dtype=act, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev), z.to(dev), M, N, K, G)
+    assert torch.equal(out.cpu().view(torch.int16), ref[:, ks].T.contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("kind", ["skinny", "tiled"])
+def test_int8_in_register_dequant_bit_exact(dev, kind):
+    N, K = 64, 512
+    M = 8 if kind == "skinny" else 64
+    _, w, s, _ = make_int8_problem(M, N, K, seed=13)
+    ks = torch.randperm(K, generator=_gen(4))[:M]
+    x = torch.zeros(M, K, dtype=torch.float16)
+    x[torch.arange(M), ks] = 1.0
+    ref = torch.from_numpy(oracle.dequant_int8(w.numpy(), np32(s), None)).half()
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None, M, N, K)
+    assert torch.equal(out.cpu().view(torch.int16), ref[:, ks].T.contiguous().view(torch.int16))
+
+
+# --- benchmark configurations (a column subset is checked against the oracle) ----
+def _cols(N, n=384, seed=0):
+    return np.sort(np.random.default_rng(seed).choice(N, n, replace=False))
+
+
+@pytest.mark.parametrize("M", [1, 8, 32, 128])
+def test_w4a16_config_c3(dev, M):
+    N, K, G = 14336, 4096, 128
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=100 + M)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev), z.to(dev), M, N, K, G)
+    cols = _cols(N)
+    ref = oracle.int4_matmul(np32(x), packed.numpy()[cols], np32(s)[cols], np32(z)[cols],
+                             M, len(cols), K, G)
+    check_close(out.cpu()[:, cols], ref)
+
+
+@pytest.mark.parametrize("M", [1, 16, 128])
+def test_w8a16_config_c2(dev, M):
+    N, K = 11008, 4096
+    x, w, s, _ = make_int8_problem(M, N, K, seed=200 + M)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None, M, N, K)
+    cols = _cols(N)
+    ref = oracle.int8_matmul(np32(x), w.numpy()[cols], np32(s)[cols], None, M, len(cols), K)
+    check_close(out.cpu()[:, cols], ref)
+
+
+# --- edge cases -------------------------------------------------------------------
+@pytest.mark.parametrize("M,N,K,G", [(3, 48, 512, 128), (5, 64, 1024, 64), (9, 64, 512, 32),
+                                     (17, 128, 768, 128), (65, 64, 256, 128), (1, 40, 512, 128),
+                                     (2, 64, 200, 40), (4, 24, 64, 16)])
+@pytest.mark.parametrize("zeros", ["f16", "u8", None])
+def test_int4_shapes_and_zero_types(dev, M, N, K, G, zeros):
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 7 + N, zeros=zeros)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
+                   None if z is None else z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    check_close(out.cpu(), ref)
+
+
+def test_int4_fractional_zero_points(dev):
+    """Non-integer zero-points take the fp32 formula path lane by lane."""
+    M, N, K, G = 4, 64, 1024, 128
+    x, q, packed, s, _ = make_int4_problem(M, N, K, G, seed=21)
+    z = (torch.rand(N, K // G, generator=_gen(22)) * 8).half()
+    z[::2] = z[::2].round()  # mix integral and fractional rows
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev), z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    check_close(out.cpu(), ref)
+    deq = tm.wq_dequant(packed.to(dev), s.to(dev), z.to(dev), N, K, 4, G)
+    refd = torch.from_numpy(oracle.dequant_int4(packed.numpy(), np32(s), np32(z), K, G)).half()
+    assert torch.equal(deq.cpu().view(torch.int16), refd.view(torch.int16))
+
+
+@pytest.mark.parametrize("M", [1, 7, 33])
+def test_int4_bf16_activations(dev, M):
+    N, K, G = 128, 1024, 128
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=31, act=torch.bfloat16)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev), z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    check_close(out.cpu(), ref, atol=3e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (16, 128, 512), (3, 40, 100), (70, 64, 256)])
+@pytest.mark.parametrize("zeros", [False, True])
+def test_int8_shapes(dev, M, N, K, zeros):
+    x, w, s, z = make_int8_problem(M, N, K, seed=M + N + K, zeros=zeros or None)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None if z is None else z.to(dev),
+                   M, N, K)
+    ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
+    check_close(out.cpu(), ref)
+
+
+def test_empty_and_errors(dev):
+    x = torch.zeros(0, 512, dtype=torch.float16, device=dev)
+    w = torch.zeros(64, 256, dtype=torch.uint8, device=dev)
+    s = torch.ones(64, 4, dtype=torch.float16, device=dev)
+    out = torch.empty(0, 64, dtype=torch.float16, device=dev)
+    tm.int4_matmul(x, w, out, s, None, 0, 64, 512, 128)  # no-op
+    with pytest.raises(TypeError):
+        tm.int4_matmul(x.float(), w, out, s, None, 0, 64, 512, 128)
+    with pytest.raises(ValueError):
+        tm.int4_matmul(x.cpu(), w, out, s, None, 0, 64, 512, 128)

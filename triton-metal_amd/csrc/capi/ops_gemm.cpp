@@ -1,0 +1,168 @@
+// Typed entry points for the matmul family: W8A16 / W4A16 weight-only
+// matmul, the dequantised weight tile, dense matmul and fused linear.
+// Each validates its arguments, picks a kernel variant from the shape and
+// dtypes and launches it asynchronously on the caller's stream.
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+
+#include "runtime.h"
+
+using namespace tmhip;
+
+namespace {
+
+const char* dt_name(int dt) {
+  switch (dt) {
+    case TM_DT_F32: return "f32";
+    case TM_DT_F16: return "f16";
+    case TM_DT_BF16: return "bf16";
+    case TM_DT_U8: return "u8";
+    case TM_DT_NONE: return "none";
+    default: return "?";
+  }
+}
+
+// Kernel registry keyed by name (names are compile-time constants of the
+// instantiations in the .hip sources).
+Kernel& kernel(const std::string& name) {
+  static std::mutex mu;
+  static std::map<std::string, Kernel*> table;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = table.find(name);
+  if (it != table.end()) return *it->second;
+  char* stored = strdup(name.c_str());
+  Kernel* k = new Kernel(stored);
+  table[name] = k;
+  return *k;
+}
+
+int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, const void* Z,
+              int M, int N, int K, int G, int adt, int sdt, int zdt, void* stream) {
+  const char* op = qbits == 4 ? "tm_int4_matmul" : "tm_int8_matmul";
+  if (M < 0 || N < 0 || K < 0) return fail(TM_ERR_INVALID_ARG, "%s: negative size", op);
+  if (M == 0 || N == 0) return 0;
+  if (!X || !W || !Y || !S) return fail(TM_ERR_INVALID_ARG, "%s: null buffer", op);
+  if (qbits == 4 && (K % 2 != 0))
+    return fail(TM_ERR_INVALID_ARG, "%s: K=%d must be even (two nibbles per byte)", op, K);
+  if (qbits == 4 && G <= 0) return fail(TM_ERR_INVALID_ARG, "%s: group_size=%d", op, G);
+  if (!is_float(adt) || !is_float(sdt))
+    return fail(TM_ERR_INVALID_ARG, "%s: act dtype %s / scale dtype %s", op, dt_name(adt),
+                dt_name(sdt));
+  if (!(zdt == TM_DT_NONE || is_float(zdt) || zdt == TM_DT_U8))
+    return fail(TM_ERR_INVALID_ARG, "%s: zero dtype %d", op, zdt);
+  if (zdt != TM_DT_NONE && !Z) return fail(TM_ERR_INVALID_ARG, "%s: zeros is NULL", op);
+  if (!api()) return TM_ERR_NO_RUNTIME;
+  clear_error();
+
+  const int CK = qbits == 4 ? 128 : 64;
+  bool fast = is_half(adt) && (qbits == 8 || G % 128 == 0) && N % 16 == 0 && K > 0 &&
+              aligned16(X) && aligned16(W);
+  const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
+  size_t lds = (size_t)M * (K + 8) * 2 + (size_t)M * (K / 128) * 4;
+  if (fast && M <= 8 && K % (4 * CK) == 0 && lds <= (size_t)max_dynamic_lds()) {
+    char name[64];
+    snprintf(name, sizeof name, "wq_skinny_q%d_%s", qbits, act);
+    return launch(kernel(name), dim3(N / 16), dim3(256), (unsigned)lds, stream, X, W, Y, S, Z, M,
+                  N, K, G, sdt, zdt);
+  }
+  if (fast && K % 256 == 0 && N % 64 == 0) {
+    char name[64];
+    snprintf(name, sizeof name, "wq_tiled_q%d_%s", qbits, act);
+    int tiles = ((M + 63) / 64) * (N / 64);
+    int grid = (tiles + 7) / 8 * 8;
+    return launch(kernel(name), dim3(grid), dim3(256), 0, stream, X, W, Y, S, Z, M, N, K, G, sdt,
+                  zdt);
+  }
+  int Gg = qbits == 4 ? G : 1;
+  return launch(kernel("wq_general"), dim3((N + 3) / 4), dim3(256), 0, stream, X,
+                (const uint8_t*)W, Y, S, Z, M, N, K, Gg, qbits, adt, sdt, zdt);
+}
+
+int dense(const void* A, const void* B, void* C, const void* bias, int M, int N, int K, int lda,
+          int ldb, int ldc, bool bt, int idt, int odt, void* stream) {
+  const char* op = bt ? "tm_linear" : "tm_matmul";
+  if (M < 0 || N < 0 || K < 0) return fail(TM_ERR_INVALID_ARG, "%s: negative size", op);
+  if (M == 0 || N == 0) return 0;
+  if (!A || !B || !C) return fail(TM_ERR_INVALID_ARG, "%s: null buffer", op);
+  if (!is_float(idt) || !is_float(odt))
+    return fail(TM_ERR_INVALID_ARG, "%s: dtypes %s -> %s", op, dt_name(idt), dt_name(odt));
+  if (lda < K || ldc < N || (bt ? ldb < K : ldb < N))
+    return fail(TM_ERR_INVALID_ARG, "%s: leading dimension too small", op);
+  if (!api()) return TM_ERR_NO_RUNTIME;
+  clear_error();
+  bool mfma = is_half(idt) && (odt == idt || odt == TM_DT_F32) && K % 8 == 0 && lda % 8 == 0 &&
+              ldb % 8 == 0 && aligned16(A) && aligned16(B) && (bt || N % 8 == 0);
+  if (mfma) {
+    const char* tile;
+    long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+    long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    int bm;
+    if (t128 >= 256) { tile = "t128"; bm = 128; }
+    else if (t64 >= 192) { tile = "t64"; bm = 64; }
+    else { tile = "t32"; bm = 32; }
+    char name[96];
+    snprintf(name, sizeof name, "gemm_%s_%s_%s_%s%s", tile, bt ? "nt" : "nn",
+             idt == TM_DT_BF16 ? "bf16" : "f16", odt == TM_DT_F32 ? "f32" : "same",
+             (bt && bias) ? "_bias" : "");
+    int grid = ((M + bm - 1) / bm) * ((N + bm - 1) / bm);
+    return launch(kernel(name), dim3(grid), dim3(256), 0, stream, A, B, C, bias, M, N, K, lda,
+                  ldb, ldc);
+  }
+  size_t total = (size_t)M * N;
+  return launch(kernel("gemm_general"), dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                stream, A, B, C, bias, M, N, K, lda, ldb, ldc, bt ? 1 : 0, idt, odt);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tm_int8_matmul(const void* input, const void* weight, void* output, const void* scales,
+                   const void* zeros, int M, int N, int K, int act_dtype, int scale_dtype,
+                   int zero_dtype, void* stream) {
+  return wq_matmul(8, input, weight, output, scales, zeros, M, N, K, 1, act_dtype, scale_dtype,
+                   zero_dtype, stream);
+}
+
+int tm_int4_matmul(const void* input, const void* weight, void* output, const void* scales,
+                   const void* zeros, int M, int N, int K, int group_size, int act_dtype,
+                   int scale_dtype, int zero_dtype, void* stream) {
+  return wq_matmul(4, input, weight, output, scales, zeros, M, N, K, group_size, act_dtype,
+                   scale_dtype, zero_dtype, stream);
+}
+
+int tm_wq_dequant(const void* weight, const void* scales, const void* zeros, void* out, int N,
+                  int K, int group_size, int qbits, int scale_dtype, int zero_dtype,
+                  int out_dtype, void* stream) {
+  if (!weight || !scales || !out) return fail(TM_ERR_INVALID_ARG, "tm_wq_dequant: null buffer");
+  if (qbits != 4 && qbits != 8) return fail(TM_ERR_INVALID_ARG, "tm_wq_dequant: qbits=%d", qbits);
+  if (N < 0 || K < 0 || (qbits == 4 && (K % 2 || group_size <= 0)))
+    return fail(TM_ERR_INVALID_ARG, "tm_wq_dequant: N=%d K=%d G=%d", N, K, group_size);
+  if (!is_float(scale_dtype) || !is_float(out_dtype) ||
+      !(zero_dtype == TM_DT_NONE || is_float(zero_dtype) || zero_dtype == TM_DT_U8))
+    return fail(TM_ERR_INVALID_ARG, "tm_wq_dequant: dtype");
+  if (zero_dtype != TM_DT_NONE && !zeros)
+    return fail(TM_ERR_INVALID_ARG, "tm_wq_dequant: zeros is NULL");
+  size_t total = (size_t)N * K;
+  if (total == 0) return 0;
+  if (!api()) return TM_ERR_NO_RUNTIME;
+  clear_error();
+  int G = qbits == 4 ? group_size : 1;
+  return launch(kernel("wq_dequant"), dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                stream, (const uint8_t*)weight, scales, zeros, out, N, K, G, qbits, scale_dtype,
+                zero_dtype, out_dtype);
+}
+
+int tm_matmul(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb,
+              int ldc, int in_dtype, int out_dtype, void* stream) {
+  return dense(A, B, C, nullptr, M, N, K, lda, ldb, ldc, false, in_dtype, out_dtype, stream);
+}
+
+int tm_linear(const void* input, const void* weight, const void* bias, void* output, int M,
+              int N, int K, int in_dtype, int out_dtype, void* stream) {
+  return dense(input, weight, output, bias, M, N, K, K, K, N, true, in_dtype, out_dtype, stream);
+}
+
+}  // extern "C"

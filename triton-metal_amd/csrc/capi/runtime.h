@@ -1,0 +1,83 @@
+// Host-side runtime of libtm_hip.so: HIP entry points resolved from the HIP
+// runtime already present in the process, per-device code-object cache,
+// thread-local error state and a typed launch helper.
+#pragma once
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+#include "tm_hip.h"
+
+namespace tmhip {
+
+// HIP runtime entry points (resolved with dlsym; the library never links
+// libamdhip64 so that it shares the caller's runtime instead of loading a
+// second copy).
+struct HipApi {
+  hipError_t (*GetDevice)(int*);
+  hipError_t (*GetDeviceCount)(int*);
+  hipError_t (*DeviceGetAttribute)(int*, hipDeviceAttribute_t, int);
+  hipError_t (*GetDeviceProperties)(hipDeviceProp_t*, int);
+  hipError_t (*ModuleLoadData)(hipModule_t*, const void*);
+  hipError_t (*ModuleUnload)(hipModule_t);
+  hipError_t (*ModuleGetFunction)(hipFunction_t*, hipModule_t, const char*);
+  hipError_t (*FuncGetAttribute)(int*, hipFunction_attribute, hipFunction_t);
+  hipError_t (*ModuleLaunchKernel)(hipFunction_t, unsigned, unsigned, unsigned, unsigned,
+                                   unsigned, unsigned, unsigned, hipStream_t, void**, void**);
+  hipError_t (*StreamSynchronize)(hipStream_t);
+  const char* (*GetErrorString)(hipError_t);
+  hipError_t (*GetLastError)(void);
+};
+
+// Returns nullptr (and sets the error) when no runtime can be resolved.
+const HipApi* api();
+
+// Error helpers: set the thread-local message and return `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char* what);
+void clear_error();
+
+constexpr int kMaxDevices = 64;
+
+// A kernel in one of the embedded code objects, resolved lazily per device.
+class Kernel {
+ public:
+  explicit Kernel(const char* name) : name_(name) {
+    for (auto& f : fn_) f.store(nullptr, std::memory_order_relaxed);
+  }
+  // Resolve for the current device; returns 0 or an error code.
+  int get(hipFunction_t* out);
+  const char* name() const { return name_; }
+
+ private:
+  const char* name_;
+  std::atomic<hipFunction_t> fn_[kMaxDevices];
+};
+
+int current_device(int* dev);
+// Largest dynamic LDS allocation per workgroup on the current device (bytes).
+int max_dynamic_lds();
+
+// Launch helper: args are passed by value and forwarded as kernelParams.
+template <class... Args>
+int launch(Kernel& k, dim3 grid, dim3 block, unsigned shared, void* stream, Args... args) {
+  hipFunction_t f = nullptr;
+  int rc = k.get(&f);
+  if (rc) return rc;
+  void* params[] = {(void*)&args..., nullptr};
+  hipError_t e = api()->ModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                           shared, (hipStream_t)stream, params, nullptr);
+  if (e != hipSuccess) return hip_fail(e, k.name());
+  return 0;
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline bool is_half(int dt) { return dt == TM_DT_F16 || dt == TM_DT_BF16; }
+inline bool is_float(int dt) { return dt == TM_DT_F32 || dt == TM_DT_F16 || dt == TM_DT_BF16; }
+
+}  // namespace tmhip

@@ -1,0 +1,112 @@
+// Shared device-side helpers for the gfx950 (CDNA4) kernels of this library.
+//
+// Everything here is written for 64-lane wavefronts and the gfx950 MFMA
+// shapes v_mfma_f32_16x16x32_{f16,bf16} and v_mfma_f32_32x32x16_{f16,bf16}.
+//
+// MFMA operand layouts used throughout (lane l of a 64-lane wave):
+//   16x16x32:  A: row l%16, k = 8*(l/16)+e (e<8)     B: col l%16, same k
+//              D: col l%16, row 4*(l/16)+e (e<4)
+//   32x32x16:  A: row l%32, k = 8*(l/32)+e (e<8)     B: col l%32, same k
+//              D: col l%32, row 8*(e/4)+4*(l/32)+(e%4) (e<16)
+// A GEMM only needs A and B to agree on the k <-> (lane, element) mapping, so
+// kernels are free to feed any fixed permutation of k to both operands.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half_t;
+typedef __bf16 bf16_t;
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 b8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 b4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+#define TM_DEV __device__ __forceinline__
+
+// dtype codes shared with the C-ABI (include/tm_hip.h).
+enum { TM_DT_F32 = 0, TM_DT_F16 = 1, TM_DT_BF16 = 2 };
+
+// ---- scalar conversions -----------------------------------------------------
+TM_DEV float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// fp32 -> bf16, round to nearest even (NaN kept quiet).
+TM_DEV uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+TM_DEV uint16_t f32_to_f16_bits(float f) {
+  half_t h = (half_t)f;  // v_cvt_f16_f32, round to nearest even
+  return __builtin_bit_cast(uint16_t, h);
+}
+TM_DEV float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(half_t, b); }
+
+// Two fp32 -> packed bf16x2 (RNE).
+TM_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+TM_DEV uint32_t pack_f16x2(float lo, float hi) {
+  return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+}
+
+template <int DT> TM_DEV float load_as_f32(const void* p, size_t i) {
+  if constexpr (DT == TM_DT_F32) return ((const float*)p)[i];
+  else if constexpr (DT == TM_DT_F16) return (float)((const half_t*)p)[i];
+  else return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+template <int DT> TM_DEV void store_from_f32(void* p, size_t i, float v) {
+  if constexpr (DT == TM_DT_F32) ((float*)p)[i] = v;
+  else if constexpr (DT == TM_DT_F16) ((uint16_t*)p)[i] = f32_to_f16_bits(v);
+  else ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
+}
+
+// ---- MFMA wrappers ------------------------------------------------------------
+// The 8 x 16-bit operand of a 16x16x32 / 32x32x16 MFMA travels as 4 dwords.
+TM_DEV f4_t mfma16x16x32(u4_t a, u4_t b, f4_t c, bool bf16) {
+  if (bf16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a),
+                                                   __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
+                                                __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+template <bool BF16> TM_DEV f4_t mfma16(u4_t a, u4_t b, f4_t c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a),
+                                                   __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
+                                                  __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+template <bool BF16> TM_DEV f16_t mfma32(u4_t a, u4_t b, f16_t c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(b8_t, a),
+                                                   __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8_t, a),
+                                                  __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+
+// ---- packed 16-bit helpers ---------------------------------------------------
+// Byte permute: result byte i = byte sel_i of the 8-byte value {hi:lo}.
+TM_DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+TM_DEV h2_t as_h2(uint32_t u) { return __builtin_bit_cast(h2_t, u); }
+TM_DEV uint32_t h2_bits(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Buffer-free 16-byte global load that the compiler keeps as one dwordx4.
+TM_DEV u4_t ldg128(const void* p) { return *(const u4_t*)p; }
+TM_DEV u2_t ldg64(const void* p) { return *(const u2_t*)p; }
+
+// Wave-wide reductions (64 lanes).
+TM_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}

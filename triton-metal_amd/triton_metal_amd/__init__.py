@@ -1,0 +1,32 @@
+"""MI355X (gfx950) native kernels for triton-metal's hot path.
+
+Dense fp16/bf16 matmul (the tl.dot path), W8A16 and W4A16 weight-only
+matmul, FlashAttention forward and KDA chunked forward, as hand-written HIP
+kernels behind the C ABI of libtm_hip.so (include/tm_hip.h).
+"""
+from . import errors
+from .errors import HipLaunchError, KernelLoadError, NativeLibraryMissing, NoDeviceError
+from .ops import (
+    Kernel,
+    Launch,
+    plan_int4_matmul,
+    plan_int8_matmul,
+    plan_matmul,
+    fused_linear,
+    int4_matmul,
+    int8_matmul,
+    make_fused_linear_kernel,
+    make_int4_matmul_kernel,
+    make_int8_matmul_kernel,
+    make_matmul_kernel,
+    make_simdgroup_matmul_kernel,
+    matmul,
+    wq_dequant,
+)
+
+__all__ = [
+    "errors", "HipLaunchError", "KernelLoadError", "NativeLibraryMissing", "NoDeviceError",
+    "Kernel", "Launch", "plan_int4_matmul", "plan_int8_matmul", "plan_matmul", "fused_linear", "int4_matmul", "int8_matmul", "make_fused_linear_kernel",
+    "make_int4_matmul_kernel", "make_int8_matmul_kernel", "make_matmul_kernel",
+    "make_simdgroup_matmul_kernel", "matmul", "wq_dequant",
+]

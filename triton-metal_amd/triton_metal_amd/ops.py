@@ -1,0 +1,288 @@
+"""Operator surface: the reference's hot-path kernels as calls on torch tensors.
+
+Each ``make_*_kernel`` factory mirrors the reference generator of the same
+name in triton_metal/codegen/_msl_templates.py and returns a callable that
+takes the buffers in the reference template's buffer order (tensors for
+buffers, Python ints/floats for the ``constant`` scalars).  Where the
+reference generator returns MSL text to be compiled and dispatched by a
+Metal runner, the callable here launches the gfx950 kernel directly on the
+current HIP stream of the tensors' device.
+
+All tensors must live on one CUDA (HIP) device.  The native library is the
+only execution path: if it is missing or the device is unusable an error is
+raised; nothing falls back to the CPU.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._lib import TM_DT_BF16, TM_DT_F16, TM_DT_F32, TM_DT_NONE, TM_DT_U8
+
+_FLOAT_DT = {torch.float32: TM_DT_F32, torch.float16: TM_DT_F16, torch.bfloat16: TM_DT_BF16}
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _dt(t: torch.Tensor, what: str) -> int:
+    try:
+        return _FLOAT_DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"{what}: unsupported dtype {t.dtype}") from None
+
+
+def _zdt(z) -> int:
+    if z is None:
+        return TM_DT_NONE
+    if z.dtype == torch.uint8:
+        return TM_DT_U8
+    return _dt(z, "zeros")
+
+
+def _device_of(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"expected a tensor, got {type(t).__name__}")
+        if t.device.type != "cuda":
+            raise ValueError(f"tensor on {t.device}; the kernels run on a HIP device")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise ValueError("no tensor arguments")
+    return dev
+
+
+def _need_contig(t, what):
+    if t is not None and not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+
+
+def _numel_at_least(t, n, what):
+    if t.numel() < n:
+        raise ValueError(f"{what} holds {t.numel()} elements, needs {n}")
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+class Launch:
+    """One validated call of a C-ABI entry point with its arguments bound.
+
+    Calling it launches asynchronously on the stream bound at creation (the
+    current stream of the tensors' device then) or on ``stream`` if given.
+    The device must be the current HIP device when called."""
+
+    __slots__ = ("_f", "_args", "_what", "dev", "stream")
+
+    def __init__(self, f, args, what, dev, stream=None):
+        self._f = f
+        self._args = args
+        self._what = what
+        self.dev = dev
+        self.stream = _stream(dev) if stream is None else stream
+
+    def __call__(self, stream=None):
+        rc = self._f(*self._args, self.stream if stream is None else stream)
+        if rc:
+            _lib.check(rc, self._what, kernel_name=self._what)
+
+
+def _run(launch: Launch):
+    """Launch now, making the tensors' device current if it is not."""
+    if launch.dev.index == torch.cuda.current_device():
+        launch()
+    else:
+        with torch.cuda.device(launch.dev):
+            launch()
+
+
+class Kernel:
+    """A launched-by-call kernel with the reference template's buffer order."""
+
+    def __init__(self, name, fn, params):
+        self.name = name
+        self._fn = fn
+        self.params = params
+
+    def __call__(self, *args, **kwargs):
+        return self._fn(*args, **kwargs)
+
+    def __repr__(self):
+        return f"Kernel({self.name}, {self.params})"
+
+
+# ---------------------------------------------------------------------------
+# weight-only quantized matmul (A7, A8)
+# ---------------------------------------------------------------------------
+def plan_int8_matmul(input, weight, output, scales, zeros, M, N, K, stream=None) -> Launch:
+    """Validate and bind an int8_matmul call (see int8_matmul)."""
+    dev = _device_of(input, weight, output, scales, zeros)
+    for t, w in ((input, "input"), (weight, "weight"), (output, "output"), (scales, "scales"),
+                 (zeros, "zeros")):
+        _need_contig(t, w)
+    if weight.dtype not in (torch.int8, torch.uint8):
+        raise TypeError(f"weight must be int8, got {weight.dtype}")
+    adt = _dt(input, "input")
+    if output.dtype != input.dtype:
+        raise TypeError("output dtype must equal input dtype")
+    _numel_at_least(input, M * K, "input")
+    _numel_at_least(weight, N * K, "weight")
+    _numel_at_least(output, M * N, "output")
+    _numel_at_least(scales, N, "scales")
+    if zeros is not None:
+        _numel_at_least(zeros, N, "zeros")
+    args = (_ptr(input), _ptr(weight), _ptr(output), _ptr(scales), _ptr(zeros), M, N, K, adt,
+            _dt(scales, "scales"), _zdt(zeros))
+    return Launch(_lib.lib().tm_int8_matmul, args, "int8_matmul", dev, stream)
+
+
+def int8_matmul(input, weight, output, scales, zeros, M, N, K):
+    """output[M,N] = input[M,K] @ ((weight[N,K] - zeros[N]) * scales[N])^T.
+
+    Buffer order of make_int8_matmul_kernel (_msl_templates.py:2652-2661).
+    ``zeros`` may be None (symmetric quantisation)."""
+    _run(plan_int8_matmul(input, weight, output, scales, zeros, M, N, K))
+    return output
+
+
+def plan_int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size=128,
+                     stream=None) -> Launch:
+    """Validate and bind an int4_matmul call (see int4_matmul)."""
+    dev = _device_of(input, weight, output, scales, zeros)
+    for t, w in ((input, "input"), (weight, "weight"), (output, "output"), (scales, "scales"),
+                 (zeros, "zeros")):
+        _need_contig(t, w)
+    if weight.dtype not in (torch.uint8, torch.int8, torch.int32, torch.uint32):
+        raise TypeError(f"weight must hold packed bytes (uint8/int32), got {weight.dtype}")
+    if K % 2:
+        raise ValueError("K must be even")
+    adt = _dt(input, "input")
+    if output.dtype != input.dtype:
+        raise TypeError("output dtype must equal input dtype")
+    ng = (K + group_size - 1) // group_size
+    _numel_at_least(input, M * K, "input")
+    if weight.numel() * weight.element_size() < N * K // 2:
+        raise ValueError("weight holds fewer than N*K/2 bytes")
+    _numel_at_least(output, M * N, "output")
+    _numel_at_least(scales, N * ng, "scales")
+    if zeros is not None:
+        _numel_at_least(zeros, N * ng, "zeros")
+    args = (_ptr(input), _ptr(weight), _ptr(output), _ptr(scales), _ptr(zeros), M, N, K,
+            group_size, adt, _dt(scales, "scales"), _zdt(zeros))
+    return Launch(_lib.lib().tm_int4_matmul, args, "int4_matmul", dev, stream)
+
+
+def int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size=128):
+    """output[M,N] = input[M,K] @ dequant(weight)^T with per-group scale/zero.
+
+    Buffer order of make_int4_matmul_kernel (_msl_templates.py:2704-2713).
+    ``weight`` holds [N, K/2] bytes (even k in the low nibble) as uint8, or
+    the same bytes as int32/uint32 [N, K/8]; scales/zeros are
+    [N, ceil(K/group_size)]; ``zeros`` may be None."""
+    _run(plan_int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size))
+    return output
+
+
+def wq_dequant(weight, scales, zeros, N, K, qbits, group_size=128, out_dtype=torch.float16,
+               out=None):
+    """Dequantised weight tile [N, K] = round((float(q) - z) * s) in out_dtype."""
+    dev = _device_of(weight, scales, zeros)
+    if out is None:
+        out = torch.empty(N, K, dtype=out_dtype, device=dev)
+    _need_contig(out, "out")
+    args = (_ptr(weight), _ptr(scales), _ptr(zeros), _ptr(out), N, K, group_size, qbits,
+            _dt(scales, "scales"), _zdt(zeros), _dt(out, "out"))
+    _run(Launch(_lib.lib().tm_wq_dequant, args, "wq_dequant", dev))
+    return out
+
+
+def make_int8_matmul_kernel():
+    return Kernel("int8_matmul", int8_matmul, {})
+
+
+def make_int4_matmul_kernel(group_size=128):
+    def run(input, weight, output, scales, zeros, M, N, K):
+        return int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size=group_size)
+    return Kernel("int4_matmul", run, {"group_size": group_size})
+
+
+# ---------------------------------------------------------------------------
+# dense matmul (A1, A4, fused linear)
+# ---------------------------------------------------------------------------
+def plan_matmul(A, B, C, M, N, K, stream=None) -> Launch:
+    """Validate and bind a matmul call (see matmul)."""
+    dev = _device_of(A, B, C)
+    for t, w in ((A, "A"), (B, "B"), (C, "C")):
+        _need_contig(t, w)
+    if A.dtype != B.dtype:
+        raise TypeError("A and B must share a dtype")
+    _numel_at_least(A, M * K, "A")
+    _numel_at_least(B, K * N, "B")
+    _numel_at_least(C, M * N, "C")
+    args = (_ptr(A), _ptr(B), _ptr(C), M, N, K, K, N, N, _dt(A, "A"), _dt(C, "C"))
+    return Launch(_lib.lib().tm_matmul, args, "matmul_kernel", dev, stream)
+
+
+def matmul(A, B, C, M, N, K):
+    """C[M,N] = A[M,K] @ B[K,N] (row-major, contiguous), fp32 accumulation.
+
+    Buffer order of make_matmul_kernel (_msl_templates.py:447-585).  The
+    output dtype is C's (fp32 output from fp16 inputs gives the
+    make_simdgroup_matmul_kernel(dtype="fp16") contract)."""
+    _run(plan_matmul(A, B, C, M, N, K))
+    return C
+
+
+def fused_linear(input, weight, C, bias, M, N, K):
+    """C[M,N] = input[M,K] @ weight[N,K]^T (+ bias[N]).
+
+    Buffer order of make_fused_linear_kernel (_msl_templates.py:4013-4135)
+    with ``bias`` None for has_bias=False."""
+    dev = _device_of(input, weight, C, bias)
+    for t, w in ((input, "input"), (weight, "weight"), (C, "C"), (bias, "bias")):
+        _need_contig(t, w)
+    if input.dtype != weight.dtype or (bias is not None and bias.dtype != input.dtype):
+        raise TypeError("input, weight and bias must share a dtype")
+    _numel_at_least(input, M * K, "input")
+    _numel_at_least(weight, N * K, "weight")
+    _numel_at_least(C, M * N, "C")
+    if bias is not None:
+        _numel_at_least(bias, N, "bias")
+    args = (_ptr(input), _ptr(weight), _ptr(bias), _ptr(C), M, N, K, _dt(input, "input"),
+            _dt(C, "C"))
+    _run(Launch(_lib.lib().tm_linear, args, "fused_linear", dev))
+    return C
+
+
+def make_matmul_kernel(block_m=32, block_n=32, block_k=32, dtype="fp32"):
+    """Tile sizes are chosen by the library; the arguments are kept for the
+    reference signature (_msl_templates.py:447)."""
+    return Kernel("matmul_kernel", matmul, {"dtype": dtype})
+
+
+def make_simdgroup_matmul_kernel(dtype="fp32"):
+    if dtype not in ("fp32", "f32", "fp16", "f16"):
+        raise ValueError(f"simdgroup_matmul supports fp32 and fp16, got {dtype}")
+    return Kernel("simdgroup_matmul", matmul, {"dtype": dtype})
+
+
+def make_fused_linear_kernel(has_bias=True):
+    if has_bias:
+        return Kernel("fused_linear", fused_linear, {"has_bias": True})
+
+    def run(input, weight, C, M, N, K):
+        return fused_linear(input, weight, C, None, M, N, K)
+    return Kernel("fused_linear", run, {"has_bias": False})
