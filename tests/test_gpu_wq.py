@@ -96,13 +96,14 @@ def test_int4_dequant_tile_bit_exact(dev, act):
     assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("kind", ["skinny", "tiled"])
+@pytest.mark.parametrize("kind", ["skinny", "gemv", "gemv8k", "tiled"])
 @pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
 def test_int4_in_register_dequant_bit_exact(dev, kind, act):
     """One-hot activation rows make each output equal one dequantised weight,
     so the GEMM's in-register dequantisation is compared bit for bit."""
-    N, K, G = 64, 512, 128
-    M = 8 if kind == "skinny" else 64
+    N, G = 64, 128
+    K = {"skinny": 512, "gemv": 4096, "gemv8k": 8192, "tiled": 512}[kind]
+    M = 64 if kind == "tiled" else 8
     _, q, packed, s, z = make_int4_problem(M, N, K, G, seed=12, act=act)
     ks = torch.randperm(K, generator=_gen(3))[:M]
     x = torch.zeros(M, K, dtype=act)
@@ -130,6 +131,18 @@ def test_int8_in_register_dequant_bit_exact(dev, kind):
 # --- benchmark configurations (a column subset is checked against the oracle) ----
 def _cols(N, n=384, seed=0):
     return np.sort(np.random.default_rng(seed).choice(N, n, replace=False))
+
+
+@pytest.mark.parametrize("M,K,zeros", [(2, 8192, "f16"), (3, 4096, "u8"), (5, 4096, None),
+                                       (1, 8192, None)])
+def test_int4_gemv_shapes(dev, M, K, zeros):
+    N, G = 1024, 128
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 31 + K, zeros=zeros)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
+                   None if z is None else z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    check_close(out.cpu(), ref)
 
 
 @pytest.mark.parametrize("M", [1, 8, 32, 128])

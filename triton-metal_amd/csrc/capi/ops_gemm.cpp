@@ -57,23 +57,37 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
   clear_error();
 
   const int CK = qbits == 4 ? 128 : 64;
-  bool fast = is_half(adt) && (qbits == 8 || G % 128 == 0) && N % 16 == 0 && K > 0 &&
-              aligned16(X) && aligned16(W);
+  bool fast = is_half(adt) && sdt == adt &&
+              (zdt == TM_DT_NONE || zdt == sdt || zdt == TM_DT_U8) &&
+              (qbits == 8 || G % 128 == 0) && N % 16 == 0 && K > 0 && aligned16(X) &&
+              aligned16(W);
   const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
+  const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
+  // exact-shape int4 GEMV: K = NW * PF * 128, G = 128
+  if (fast && qbits == 4 && M <= 8 && G == 128 && (K == 4096 || K == 8192)) {
+    size_t glds = (size_t)M * (K + 8) * 2 + (size_t)(K / 128) * 8 * 4;
+    if (glds <= (size_t)max_dynamic_lds()) {
+      const int pf = K == 4096 ? 4 : 8;
+      char name[64];
+      snprintf(name, sizeof name, "wq_gemv4_%s_z%c_w8p%d", act, zc, pf);
+      return launch(kernel(name), dim3(N / 16), dim3(512), (unsigned)glds, stream, X, W, Y, S,
+                    Z, M, N, K);
+    }
+  }
   size_t lds = (size_t)M * (K + 8) * 2 + (size_t)M * (K / 128) * 4;
   if (fast && M <= 8 && K % (4 * CK) == 0 && lds <= (size_t)max_dynamic_lds()) {
     char name[64];
-    snprintf(name, sizeof name, "wq_skinny_q%d_%s", qbits, act);
+    const bool vs = qbits == 4 && G == 128 && K % 4096 == 0;
+    snprintf(name, sizeof name, "wq_skinny_q%d_%s_z%c%s", qbits, act, zc, vs ? "_v" : "");
     return launch(kernel(name), dim3(N / 16), dim3(256), (unsigned)lds, stream, X, W, Y, S, Z, M,
-                  N, K, G, sdt, zdt);
+                  N, K, G);
   }
   if (fast && K % 256 == 0 && N % 64 == 0) {
     char name[64];
-    snprintf(name, sizeof name, "wq_tiled_q%d_%s", qbits, act);
+    snprintf(name, sizeof name, "wq_tiled_q%d_%s_z%c", qbits, act, zc);
     int tiles = ((M + 63) / 64) * (N / 64);
     int grid = (tiles + 7) / 8 * 8;
-    return launch(kernel(name), dim3(grid), dim3(256), 0, stream, X, W, Y, S, Z, M, N, K, G, sdt,
-                  zdt);
+    return launch(kernel(name), dim3(grid), dim3(256), 0, stream, X, W, Y, S, Z, M, N, K, G);
   }
   int Gg = qbits == 4 ? G : 1;
   return launch(kernel("wq_general"), dim3((N + 3) / 4), dim3(256), 0, stream, X,

@@ -104,6 +104,27 @@ TM_DEV uint32_t h2_bits(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
 TM_DEV u4_t ldg128(const void* p) { return *(const u4_t*)p; }
 TM_DEV u2_t ldg64(const void* p) { return *(const u2_t*)p; }
 
+// A 32-bit constant the compiler must keep in a VGPR (it cannot see its value).
+// With the masks of an (a & m) | o held this way, instruction selection emits a
+// single v_and_or_b32 (a VOP3 form that cannot encode literals on gfx9)
+// instead of separate v_and / v_or with literals.  Only a v_mov is hidden in
+// the asm; every instruction that consumes the value is compiler-generated, so
+// hazard tracking (e.g. VALU -> MFMA operand) stays with the compiler.
+TM_DEV uint32_t vgpr_const(uint32_t c) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
+  return r;
+}
+
+// Sum over each row of 16 lanes with DPP (all 16 lanes receive the sum).
+TM_DEV float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
 // Wave-wide reductions (64 lanes).
 TM_DEV float wave_sum(float v) {
 #pragma unroll

@@ -48,17 +48,46 @@ TM_DEV float ld_scalar(const void* p, size_t i, int dt) {
   }
 }
 
+// Scalar of a compile-time dtype (ZDT < 0: absent, reads as 0).
+template <int DT> TM_DEV float ld_typed(const void* p, size_t i) {
+  if constexpr (DT < 0) return 0.0f;
+  else if constexpr (DT == TM_DT_F32) return ((const float*)p)[i];
+  else if constexpr (DT == TM_DT_F16) return (float)((const half_t*)p)[i];
+  else if constexpr (DT == TM_DT_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+  else return (float)((const uint8_t*)p)[i];
+}
+
+// Raw storage type of a scale / zero-point dtype, loaded without conversion so
+// the load can stay in flight until the value is used.
+template <int DT> struct Raw { using T = uint16_t; };
+template <> struct Raw<TM_DT_F32> { using T = float; };
+template <> struct Raw<3> { using T = uint8_t; };
+template <> struct Raw<-1> { using T = uint8_t; };
+template <int DT> TM_DEV typename Raw<DT>::T ld_raw(const void* p, size_t i) {
+  if constexpr (DT < 0) return 0;
+  else return ((const typename Raw<DT>::T*)p)[i];
+}
+template <int DT> TM_DEV float raw_to_f32(typename Raw<DT>::T v) {
+  if constexpr (DT < 0) return 0.0f;
+  else if constexpr (DT == TM_DT_F32) return v;
+  else if constexpr (DT == TM_DT_F16) return (float)__builtin_bit_cast(half_t, v);
+  else if constexpr (DT == TM_DT_BF16) return bf16_bits_to_f32(v);
+  else return (float)v;
+}
+
 // int4: one word (8 nibbles) -> one 8 x 16-bit MFMA operand of OFF + q in
 // element order [n0, n4, n1, n5, n2, n6, n3, n7].
-template <bool BF16> TM_DEV u4_t w4_operand(uint32_t w) {
-  constexpr uint32_t MAGIC = BF16 ? 0x43004300u : 0x64006400u;  // 128.0 / 1024.0
+// `mask` = 0x000F000F and `magic` = the OFF exponent pattern, both held in
+// VGPRs (vgpr_const) so each half-pair costs one v_and_or_b32.
+TM_DEV u4_t w4_operand(uint32_t w, uint32_t mask, uint32_t magic) {
   u4_t r;
-  r.x = (w & 0x000F000Fu) | MAGIC;
-  r.y = ((w >> 4) & 0x000F000Fu) | MAGIC;
-  r.z = ((w >> 8) & 0x000F000Fu) | MAGIC;
-  r.w = ((w >> 12) & 0x000F000Fu) | MAGIC;
+  r.x = (w & mask) | magic;
+  r.y = ((w >> 4) & mask) | magic;
+  r.z = ((w >> 8) & mask) | magic;
+  r.w = ((w >> 12) & mask) | magic;
   return r;
 }
+template <bool BF16> constexpr uint32_t w4_magic() { return BF16 ? 0x43004300u : 0x64006400u; }
 template <bool BF16> constexpr float w4_offset() { return BF16 ? 128.0f : 1024.0f; }
 
 // int8: two words (8 signed bytes) -> exact q in natural element order.
@@ -114,13 +143,7 @@ template <bool BF16> TM_DEV float sum8(u4_t v) {
 }
 
 // Sum over aligned groups of 16 lanes.
-TM_DEV float sum16(float v) {
-  v += __shfl_xor(v, 8, 64);
-  v += __shfl_xor(v, 4, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 1, 64);
-  return v;
-}
+TM_DEV float sum16(float v) { return row16_sum(v); }
 
 TM_DEV void store_out(uint16_t* Y, size_t i, float v, bool bf16) {
   Y[i] = bf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
@@ -134,13 +157,13 @@ TM_DEV void store_out(uint16_t* Y, size_t i, float v, bool bf16) {
 // (int4) or 64 (int8); int4: G % 128 == 0; LDS: M * (K + 8) * 2 bytes of X
 // plus M * K / 128 * 4 bytes of chunk sums (dynamic).
 // ----------------------------------------------------------------------------
-template <int QB, bool BF16>
+template <int QB, bool BF16, int SDT, int ZDT, bool VS>
 __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
                                                const uint8_t* __restrict__ W,
                                                uint16_t* __restrict__ Y,
                                                const void* __restrict__ S,
                                                const void* __restrict__ Z, int M, int N, int K,
-                                               int G, int sdt, int zdt) {
+                                               int G) {
   extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8], then float xsum[M][K/128]
   __shared__ f4_t red[3][64];
   constexpr int CK = (QB == 4) ? 128 : 64;
@@ -152,6 +175,7 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
 
   const int n = n0 + (lane & 15), q = lane >> 4;
   const int m = min(lane & 15, M - 1);
+  const uint32_t vmask = vgpr_const(0x000F000Fu), vmagic = vgpr_const(w4_magic<BF16>());
   int rows[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) rows[e] = min(4 * q + e, M - 1);
@@ -162,61 +186,130 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
   const size_t ngroups = (QB == 4) ? (size_t)((K + G - 1) / G) : 1;
   const uint16_t* xrow = xs + m * ldx;
 
-  // Weight (and int4 scale / zero-point) loads of a batch of PF chunks;
-  // the first batch is issued before X is staged so its latency overlaps.
+  // Load order: the first X pieces, then the first batch of weights (and
+  // int4 scales / zero-points), so that staging X only waits for the X loads
+  // and overlaps the weight loads' HBM latency.  Loads are unconditional
+  // (indices clamped) so each batch issues without branches.
   constexpr int PF = 8;
   const int nsteps = kw / CK;
+  const int ppr = K >> 3;        // 16-byte X pieces per row (a multiple of 64)
+  constexpr int XU = 4;          // X pieces per thread per staging round
+
+  // X piece p of row r: k = 8p .. 8p+7.  Staging walks (row, piece) without
+  // divisions: round u of thread t covers piece t + 256u of each row.
+  auto x_load = [&](int r, int p0, u4_t* v) {
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const int p = min(p0 + tid + 256 * u, ppr - 1);
+      v[u] = ldg128(X + (size_t)r * K + (size_t)p * 8);
+    }
+  };
+  auto x_store = [&](int r, int p0, const u4_t* v) {
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const int p = p0 + tid + 256 * u;  // uniform per 16-lane row since ppr % 16 == 0
+      if (p < ppr) {
+        const float sm = sum16(sum8<BF16>(v[u]));
+        if ((p & 15) == 0) xsum[r * nch + (p >> 4)] = sm;
+        u4_t w = v[u];
+        if constexpr (QB == 4) w = perm_x8(w);
+        *(u4_t*)(xs + r * ldx + p * 8) = w;
+      }
+    }
+  };
+
   u4_t wv[PF];
-  float scv[PF], zbv[PF];
+  // int4 scales / zero-points of the batch: VS = one vector load of 8
+  // consecutive groups (G == 128, batch aligned to 8 groups), else per chunk.
+  typename Raw<SDT>::T sraw[PF];
+  typename Raw<ZDT>::T zraw[PF];
   auto load_batch = [&](int s0) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
-      if (s0 + i < nsteps) {
-        int kc = kbeg + (s0 + i) * CK;
-        size_t boff = (QB == 4) ? (size_t)(kc >> 1) + 16 * q : (size_t)kc + 16 * q;
-        wv[i] = ldg128(wrow + boff);
-        if constexpr (QB == 4) {
+      const int kc = kbeg + min(s0 + i, nsteps - 1) * CK;
+      const size_t boff = (QB == 4) ? (size_t)(kc >> 1) + 16 * q : (size_t)kc + 16 * q;
+      wv[i] = ldg128(wrow + boff);
+    }
+    if constexpr (QB == 4) {
+      if constexpr (VS) {
+        const size_t g0 = (size_t)n * ngroups + ((kbeg + s0 * CK) >> 7);
+        static_assert(sizeof(typename Raw<SDT>::T) == 2, "vector scales need 16-bit scales");
+        const u4_t sv = ldg128((const uint16_t*)S + g0);
+        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+        for (int i = 0; i < PF; ++i) sraw[i] = (uint16_t)(sw[i >> 1] >> (16 * (i & 1)));
+        if constexpr (ZDT == 3) {
+          const u2_t zv = ldg64((const uint8_t*)Z + g0);
+#pragma unroll
+          for (int i = 0; i < PF; ++i) zraw[i] = (uint8_t)((i < 4 ? zv.x : zv.y) >> (8 * (i & 3)));
+        } else if constexpr (ZDT >= 0) {
+          const u4_t zv = ldg128((const uint16_t*)Z + g0);
+          const uint32_t zw[4] = {zv.x, zv.y, zv.z, zv.w};
+#pragma unroll
+          for (int i = 0; i < PF; ++i) zraw[i] = (uint16_t)(zw[i >> 1] >> (16 * (i & 1)));
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+          const int kc = kbeg + min(s0 + i, nsteps - 1) * CK;
           const size_t gi = (size_t)n * ngroups + kc / G;
-          scv[i] = ld_scalar(S, gi, sdt);
-          zbv[i] = w4_offset<BF16>() + ld_scalar(Z, gi, zdt);
+          sraw[i] = ld_raw<SDT>(S, gi);
+          zraw[i] = ld_raw<ZDT>(Z, gi);
         }
       }
     }
   };
-  load_batch(0);
 
-  // Stage X (16-byte pieces) and the per-128-k-chunk row sums.
-  const int pieces = M * (K >> 3);
-  for (int c = tid; c < pieces; c += 256) {
-    int r = c / (K >> 3), kc = (c - r * (K >> 3)) << 3;
-    u4_t v = ldg128(X + (size_t)r * K + kc);
-    float s = sum16(sum8<BF16>(v));
-    if ((c & 15) == 0) xsum[r * nch + (kc >> 7)] = s;
-    if constexpr (QB == 4) v = perm_x8(v);
-    *(u4_t*)(xs + r * ldx + kc) = v;
+  {
+    u4_t xv[XU];
+    x_load(0, 0, xv);
+    load_batch(0);
+    x_store(0, 0, xv);
   }
+  for (int r = 0; r < M; ++r)
+    for (int p0 = (r == 0 ? 256 * XU : 0); p0 < ppr; p0 += 256 * XU) {
+      u4_t xv[XU];
+      x_load(r, p0, xv);
+      x_store(r, p0, xv);
+    }
   __syncthreads();
 
   f4_t y = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < nsteps; s0 += PF) {
     if (s0 > 0) load_batch(s0);
+    if constexpr (QB == 4) {
+      // one accumulator per chunk, four chunks at a time: consecutive MFMAs
+      // are independent
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      if (s0 + i < nsteps) {
-        int kc = kbeg + (s0 + i) * CK;
-        if constexpr (QB == 4) {
-          const int kl = kc + 32 * q;
-          f4_t a = {0.f, 0.f, 0.f, 0.f};
-          uint32_t ws[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+      for (int h = 0; h < PF; h += 4) {
+        f4_t a[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            a = mfma16<BF16>(*(const u4_t*)(xrow + kl + 8 * j), w4_operand<BF16>(ws[j]), a);
-          const int ch = kc >> 7;
+        for (int i = 0; i < 4; ++i) a[i] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            y[e] += scv[i] * (a[e] - zbv[i] * xsum[rows[e] * nch + ch]);
-        } else {
-          const int kl = kc + 16 * q;
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kl = kbeg + min(s0 + h + i, nsteps - 1) * CK + 32 * q;
+            const u4_t w = wv[h + i];
+            const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+            a[i] = mfma16<BF16>(*(const u4_t*)(xrow + kl + 8 * j), w4_operand(wj, vmask, vmagic), a[i]);
+          }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (s0 + h + i < nsteps) {
+            const int ch = (kbeg + (s0 + h + i) * CK) >> 7;
+            const float sc = raw_to_f32<SDT>(sraw[h + i]);
+            const float zb = w4_offset<BF16>() + raw_to_f32<ZDT>(zraw[h + i]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] += sc * (a[i][e] - zb * xsum[rows[e] * nch + ch]);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PF; ++i) {
+        if (s0 + i < nsteps) {
+          const int kl = kbeg + (s0 + i) * CK + 16 * q;
           y = mfma16<BF16>(*(const u4_t*)(xrow + kl), w8_operand<BF16>(wv[i].x, wv[i].y), y);
           y = mfma16<BF16>(*(const u4_t*)(xrow + kl + 8), w8_operand<BF16>(wv[i].z, wv[i].w), y);
         }
@@ -229,12 +322,12 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
   if (wave == 0) {
     y += red[0][lane] + red[1][lane] + red[2][lane];
     if constexpr (QB == 8) {
-      const float sc = ld_scalar(S, (size_t)n, sdt);
-      const float z = ld_scalar(Z, (size_t)n, zdt);
+      const float sc = ld_typed<SDT>(S, (size_t)n);
+      const float z = ld_typed<ZDT>(Z, (size_t)n);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float xt = 0.0f;
-        if (zdt >= 0)
+        if constexpr (ZDT >= 0)
           for (int c = 0; c < nch; ++c) xt += xsum[rows[e] * nch + c];
         y[e] = sc * (y[e] - z * xt);
       }
@@ -242,6 +335,124 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       int row = 4 * q + e;
+      if (row < M) store_out(Y, (size_t)row * N + n, y[e], BF16);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// GEMV kernel for int4, M <= 8, the exact shape K = NW * PF * 128 with
+// group size 128 (the common W4A16 decode case).  grid.x = N / 16,
+// block = NW waves; wave w owns k = w*PF*128 .. +PF*128 of the workgroup's
+// 16 columns.  Everything is unrolled at compile time: PF 16-byte weight
+// loads per lane, one vector load of the PF scales (and zero-points) per
+// lane, PF independent MFMA chains.  Dynamic LDS: M * (K + 8) * 2 bytes of X
+// plus (K / 128) * 8 * 4 bytes of chunk sums laid out [chunk][row 0..7].
+// ----------------------------------------------------------------------------
+template <bool BF16, int ZDT, int NW, int PF>
+__device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
+                                              const uint8_t* __restrict__ W,
+                                              uint16_t* __restrict__ Y,
+                                              const uint16_t* __restrict__ S,
+                                              const void* __restrict__ Z, int M, int N, int K) {
+  constexpr int NT = NW * 64;
+  constexpr int SDT = BF16 ? TM_DT_BF16 : TM_DT_F16;
+  extern __shared__ __align__(16) uint16_t xs[];
+  __shared__ f4_t red[NW - 1][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ldx = K + 8;
+  const int nch = K >> 7;
+  float* xsum = (float*)(xs + (size_t)M * ldx);  // [nch][8]
+  const int n = blockIdx.x * 16 + (lane & 15), q = lane >> 4;
+  const int m = min(lane & 15, M - 1);
+  const int kbeg = wave * (PF * 128);
+  const uint32_t vmask = vgpr_const(0x000F000Fu), vmagic = vgpr_const(w4_magic<BF16>());
+
+  // 1. first X row pieces (PF / 4 per thread), 2. weights + scales, 3. stage
+  constexpr int XP = PF / 4;  // pieces per thread per row: K / 8 / NT
+  u4_t xv[XP];
+#pragma unroll
+  for (int u = 0; u < XP; ++u) xv[u] = ldg128(X + (size_t)(tid + NT * u) * 8);
+
+  const uint8_t* wrow = W + (size_t)n * (K >> 1) + (kbeg >> 1) + 16 * q;
+  u4_t wv[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) wv[i] = ldg128(wrow + 64 * i);
+  const size_t g0 = (size_t)n * nch + (kbeg >> 7);
+  uint32_t sw[PF / 2], zw[PF / 2];
+  if constexpr (PF == 4) {
+    const u2_t v = ldg64(S + g0);
+    sw[0] = v.x; sw[1] = v.y;
+  } else {
+    const u4_t v = ldg128(S + g0);
+    sw[0] = v.x; sw[1] = v.y; sw[2] = v.z; sw[3] = v.w;
+  }
+  uint32_t zb8[(PF + 3) / 4];
+  if constexpr (ZDT == 3) {
+    if constexpr (PF == 4) zb8[0] = *(const uint32_t*)((const uint8_t*)Z + g0);
+    else { const u2_t v = ldg64((const uint8_t*)Z + g0); zb8[0] = v.x; zb8[1] = v.y; }
+  } else if constexpr (ZDT >= 0) {
+    if constexpr (PF == 4) {
+      const u2_t v = ldg64((const uint16_t*)Z + g0);
+      zw[0] = v.x; zw[1] = v.y;
+    } else {
+      const u4_t v = ldg128((const uint16_t*)Z + g0);
+      zw[0] = v.x; zw[1] = v.y; zw[2] = v.z; zw[3] = v.w;
+    }
+  }
+
+  auto stage = [&](int r, const u4_t* v) {
+#pragma unroll
+    for (int u = 0; u < XP; ++u) {
+      const int p = tid + NT * u;
+      const float sm = sum16(sum8<BF16>(v[u]));
+      if ((p & 15) == 0) xsum[(p >> 4) * 8 + r] = sm;
+      *(u4_t*)(xs + r * ldx + p * 8) = perm_x8(v[u]);
+    }
+  };
+  stage(0, xv);
+  for (int r = 1; r < M; ++r) {
+#pragma unroll
+    for (int u = 0; u < XP; ++u) xv[u] = ldg128(X + (size_t)r * K + (size_t)(tid + NT * u) * 8);
+    stage(r, xv);
+  }
+  __syncthreads();
+
+  const uint16_t* xa = xs + m * ldx + kbeg + 32 * q;
+  f4_t a[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) a[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const u4_t w = wv[i];
+      const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+      a[i] = mfma16<BF16>(*(const u4_t*)(xa + 128 * i + 8 * j), w4_operand(wj, vmask, vmagic),
+                          a[i]);
+    }
+  f4_t y = {0.f, 0.f, 0.f, 0.f};
+  const float* xsr = xsum + (kbeg >> 7) * 8 + 4 * (q & 1);
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    const uint16_t sr = (uint16_t)(sw[i >> 1] >> (16 * (i & 1)));
+    const float sc = raw_to_f32<SDT>(sr);
+    float zb = w4_offset<BF16>();
+    if constexpr (ZDT == 3) zb += (float)((zb8[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+    else if constexpr (ZDT >= 0) zb += raw_to_f32<ZDT>((uint16_t)(zw[i >> 1] >> (16 * (i & 1))));
+    const f4_t xv4 = *(const f4_t*)(xsr + 8 * i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] += sc * (a[i][e] - zb * xv4[e]);
+  }
+
+  if (wave > 0) red[wave - 1][lane] = y;
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 0; w < NW - 1; ++w) y += red[w][lane];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = 4 * q + e;
       if (row < M) store_out(Y, (size_t)row * N + n, y[e], BF16);
     }
   }
@@ -256,13 +467,13 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
 // Grid: tiles enumerated so that the row blocks sharing one column block land
 // on the same XCD (blockIdx % 8 picks the XCD).
 // ----------------------------------------------------------------------------
-template <int QB, bool BF16>
+template <int QB, bool BF16, int SDT, int ZDT>
 __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
                                               const uint8_t* __restrict__ W,
                                               uint16_t* __restrict__ Y,
                                               const void* __restrict__ S,
                                               const void* __restrict__ Z, int M, int N, int K,
-                                              int G, int sdt, int zdt) {
+                                              int G) {
   constexpr int BM = 64, KS = 256, LDX = KS + 8;
   __shared__ __align__(16) uint16_t xs[2][BM * LDX];
   __shared__ __align__(16) float xsm[2][2][BM];  // [buf][chunk][row]
@@ -277,6 +488,7 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
   const int m0 = mb * BM, n0 = nbk * 64;
 
   const int n = n0 + wave * 16 + (lane & 15), q = lane >> 4;
+  const uint32_t vmask = vgpr_const(0x000F000Fu), vmagic = vgpr_const(w4_magic<BF16>());
   const size_t rowbytes = (QB == 4) ? (size_t)(K >> 1) : (size_t)K;
   const uint8_t* wrow = W + (size_t)n * rowbytes;
   const int ngroups = (QB == 4) ? (K + G - 1) / G : 1;
@@ -287,15 +499,16 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
   // the MFMAs of step s; the X pieces go to the other LDS buffer afterwards.
   constexpr int NL = (QB == 4) ? 2 : 4;  // 16-byte weight loads per lane per step
   u4_t xr[8], wv[NL], wn[NL];
-  float scv[NL], zbv[NL], scn[NL], zbn[NL];
+  typename Raw<SDT>::T scv[NL], scn[NL];
+  typename Raw<ZDT>::T zbv[NL], zbn[NL];
   auto load_x = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       int c = tid + 256 * i;
       int r = c >> 5, kc = (c & 31) << 3;
-      int gr = m0 + r;
-      xr[i] = u4_t{0u, 0u, 0u, 0u};
-      if (gr < M) xr[i] = ldg128(X + (size_t)gr * K + k0 + kc);
+      const int gr = m0 + r;
+      xr[i] = ldg128(X + (size_t)min(gr, M - 1) * K + k0 + kc);
+      if (gr >= M) xr[i] = u4_t{0u, 0u, 0u, 0u};
     }
   };
   auto store_x = [&](int buf) {
@@ -310,7 +523,7 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
       *(u4_t*)(&xs[buf][r * LDX + kc]) = v;
     }
   };
-  auto load_w = [&](int k0, u4_t* dst, float* sc, float* zb) {
+  auto load_w = [&](int k0, u4_t* dst, typename Raw<SDT>::T* sc, typename Raw<ZDT>::T* zb) {
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       int kc = k0 + i * (QB == 4 ? 128 : 64);
@@ -318,8 +531,8 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
       dst[i] = ldg128(wrow + boff);
       if constexpr (QB == 4) {
         const size_t gi = (size_t)n * ngroups + kc / G;
-        sc[i] = ld_scalar(S, gi, sdt);
-        zb[i] = w4_offset<BF16>() + ld_scalar(Z, gi, zdt);
+        sc[i] = ld_raw<SDT>(S, gi);
+        zb[i] = ld_raw<ZDT>(Z, gi);
       }
     }
   };
@@ -354,17 +567,19 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
         uint32_t ws[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          u4_t b = w4_operand<BF16>(ws[j]);
+          u4_t b = w4_operand(ws[j], vmask, vmagic);
 #pragma unroll
           for (int t = 0; t < 4; ++t)
             a[t] = mfma16<BF16>(*(const u4_t*)(xb + (t * 16 + (lane & 15)) * LDX + kl + 8 * j),
                                 b, a[t]);
         }
+        const float sc = raw_to_f32<SDT>(scv[i]);
+        const float zb = w4_offset<BF16>() + raw_to_f32<ZDT>(zbv[i]);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const f4_t xv = *(const f4_t*)(&xsm[buf][i][t * 16 + 4 * q]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[t][e] += scv[i] * (a[t][e] - zbv[i] * xv[e]);
+          for (int e = 0; e < 4; ++e) y[t][e] += sc * (a[t][e] - zb * xv[e]);
         }
       } else {
         const int kl = i * 64 + 16 * q;
@@ -378,13 +593,11 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
         }
       }
     }
-    if constexpr (QB == 8) {
-      if (zdt >= 0) {
+    if constexpr (QB == 8 && ZDT >= 0) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          xtot[t] += *(const f4_t*)(&xsm[buf][0][t * 16 + 4 * q]) +
-                     *(const f4_t*)(&xsm[buf][1][t * 16 + 4 * q]);
-      }
+      for (int t = 0; t < 4; ++t)
+        xtot[t] += *(const f4_t*)(&xsm[buf][0][t * 16 + 4 * q]) +
+                   *(const f4_t*)(&xsm[buf][1][t * 16 + 4 * q]);
     }
     if (more) store_x(buf ^ 1);
     __syncthreads();
@@ -400,8 +613,8 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
 
   float sc = 1.0f, z = 0.0f;
   if constexpr (QB == 8) {
-    sc = ld_scalar(S, (size_t)n, sdt);
-    z = ld_scalar(Z, (size_t)n, zdt);
+    sc = ld_typed<SDT>(S, (size_t)n);
+    z = ld_typed<ZDT>(Z, (size_t)n);
   }
 #pragma unroll
   for (int t = 0; t < 4; ++t)
@@ -479,20 +692,51 @@ extern "C" __global__ __launch_bounds__(256) void wq_dequant(
 }
 
 // ----------------------------------------------------------------------------
-// Named instantiations: wq_{skinny,tiled}_q{4,8}_{f16,bf16}
+// Named instantiations: wq_{skinny,tiled}_q{4,8}_{f16,bf16}_z{n,s,u}
+// Scales have the activation dtype; zero-points: n = none, s = scale dtype,
+// u = uint8.
 // ----------------------------------------------------------------------------
-#define TM_WQ_INST(KIND, QB, BF, ACT)                                                           \
-  extern "C" __global__ __launch_bounds__(256) void wq_##KIND##_q##QB##_##ACT(                   \
-      const uint16_t* X, const uint8_t* W, uint16_t* Y, const void* S, const void* Z, int M,     \
-      int N, int K, int G, int sdt, int zdt) {                                                   \
-    wq_##KIND##_body<QB, BF>(X, W, Y, S, Z, M, N, K, G, sdt, zdt);                               \
+#define TM_WQ_ATTR_skinny __attribute__((amdgpu_waves_per_eu(4)))
+#define TM_WQ_ATTR_tiled
+#define TM_WQ_INST(KIND, QB, BF, ACT, ZS, ZDT, SUF, ...)                                        \
+  extern "C" __global__ __launch_bounds__(256) TM_WQ_ATTR_##KIND void                           \
+      wq_##KIND##_q##QB##_##ACT##_z##ZS##SUF(const uint16_t* X, const uint8_t* W, uint16_t* Y,   \
+                                             const void* S, const void* Z, int M, int N, int K,  \
+                                             int G) {                                             \
+    wq_##KIND##_body<QB, BF, (BF ? TM_DT_BF16 : TM_DT_F16), ZDT __VA_ARGS__>(X, W, Y, S, Z, M,   \
+                                                                              N, K, G);           \
   }
+// skinny: _v = vector scale loads (G == 128, K % 4096 == 0)
+#define TM_WQ_Z(KIND, QB, BF, ACT, SUF, ...)                                          \
+  TM_WQ_INST(KIND, QB, BF, ACT, n, -1, SUF, __VA_ARGS__)                              \
+  TM_WQ_INST(KIND, QB, BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), SUF, __VA_ARGS__)   \
+  TM_WQ_INST(KIND, QB, BF, ACT, u, 3, SUF, __VA_ARGS__)
 
-TM_WQ_INST(skinny, 4, false, f16)
-TM_WQ_INST(skinny, 4, true, bf16)
-TM_WQ_INST(skinny, 8, false, f16)
-TM_WQ_INST(skinny, 8, true, bf16)
-TM_WQ_INST(tiled, 4, false, f16)
-TM_WQ_INST(tiled, 4, true, bf16)
-TM_WQ_INST(tiled, 8, false, f16)
-TM_WQ_INST(tiled, 8, true, bf16)
+TM_WQ_Z(skinny, 4, false, f16, , , false)
+TM_WQ_Z(skinny, 4, true, bf16, , , false)
+TM_WQ_Z(skinny, 4, false, f16, _v, , true)
+TM_WQ_Z(skinny, 4, true, bf16, _v, , true)
+TM_WQ_Z(skinny, 8, false, f16, , , false)
+TM_WQ_Z(skinny, 8, true, bf16, , , false)
+TM_WQ_Z(tiled, 4, false, f16, , )
+TM_WQ_Z(tiled, 4, true, bf16, , )
+TM_WQ_Z(tiled, 8, false, f16, , )
+TM_WQ_Z(tiled, 8, true, bf16, , )
+
+// GEMV (int4, exact K = NW * PF * 128, G = 128): wq_gemv4_<act>_z<zs>_w<NW>p<PF>
+#define TM_GEMV4(BF, ACT, ZS, ZDT, NW, PF)                                                     \
+  extern "C" __global__ __launch_bounds__(NW * 64) void wq_gemv4_##ACT##_z##ZS##_w##NW##p##PF(  \
+      const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S, const void* Z, int M, \
+      int N, int K) {                                                                           \
+    wq_gemv4_body<BF, ZDT, NW, PF>(X, W, Y, S, Z, M, N, K);                                     \
+  }
+#define TM_GEMV4_Z(BF, ACT, NW, PF)                                   \
+  TM_GEMV4(BF, ACT, n, -1, NW, PF)                                    \
+  TM_GEMV4(BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), NW, PF)         \
+  TM_GEMV4(BF, ACT, u, 3, NW, PF)
+TM_GEMV4_Z(false, f16, 8, 4)
+TM_GEMV4_Z(true, bf16, 8, 4)
+TM_GEMV4_Z(false, f16, 4, 8)
+TM_GEMV4_Z(true, bf16, 4, 8)
+TM_GEMV4_Z(false, f16, 8, 8)
+TM_GEMV4_Z(true, bf16, 8, 8)
