@@ -109,6 +109,23 @@ def dense(dev, M=512, N=512, K=512):
                 flops=2 * M * N * K, bound="mfma", dtype="fp16", config={"workload": f"dense_{M}x{N}x{K}", "M": M, "N": N, "K": K})
 
 
+def flash(dev, causal, B=4, H=32, S=4096, D=128):
+    import torch
+    import triton_metal_amd as tm
+    g = torch.Generator(device=dev).manual_seed(4)
+    q, k, v = (torch.randn(B, H, S, D, device=dev, generator=g).bfloat16() for _ in range(3))
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, S, device=dev, dtype=torch.float32)
+    launches = [tm.plan_flash_attention(q, k, v, o, lse, causal=causal)]
+    flops = 4 * B * H * S * S * D // (2 if causal else 1)
+    nbytes = 2 * 4 * B * H * S * D + 4 * B * H * S
+    return dict(launches=launches, keep=(q, k, v, o, lse), bytes=nbytes, flops=flops,
+                bound="mfma", dtype="bf16",
+                config={"workload": f"flash_fwd_{'causal' if causal else 'full'}", "B": B,
+                        "H": H, "S": S, "D": D, "causal": causal,
+                        "flops_convention": "4*B*H*S^2*D, halved when causal"})
+
+
 WORKLOADS = {
     "w4a16_m1": lambda d: w4a16(d, 1),
     "w4a16_m8": lambda d: w4a16(d, 8),
@@ -119,6 +136,8 @@ WORKLOADS = {
     "w8a16_m128": lambda d: w8a16(d, 128),
     "dense_512": lambda d: dense(d),
     "dense_4096": lambda d: dense(d, 4096, 4096, 4096),
+    "flash_causal": lambda d: flash(d, True),
+    "flash_full": lambda d: flash(d, False),
 }
 HEADLINE = "w4a16_m1"
 

@@ -123,6 +123,24 @@ int tm_matmul(const void* A, const void* B, void* C, int M, int N, int K, int ld
 int tm_linear(const void* input, const void* weight, const void* bias, void* output, int M,
               int N, int K, int in_dtype, int out_dtype, void* stream);
 
+/* ---- flash attention forward -------------------------------------------------
+ * O = softmax(scale * Q K^T [+ causal mask]) V per (batch, head), fp32 softmax
+ * and accumulation; lse (may be NULL) receives the natural-log logsumexp of
+ * each row as fp32 [batch, heads, seq_len].
+ * q, k, v, o: [batch, heads, seq_len, head_dim] with element strides
+ * strides[12] = {q_b, q_h, q_s, k_b, k_h, k_s, v_b, v_h, v_s, o_b, o_h, o_s}
+ * (NULL = contiguous); the head dimension must be contiguous.
+ * Masking follows make_flash_attention_kernel (_msl_templates.py:1610-1619):
+ * key j is excluded when j >= seq_len or (causal) j > i; a row with no key
+ * gives O = 0 and lse = -inf (1747-1754).  Replaces the template's buffer ABI
+ * Q, K, V, O, seq_len, scale (1624-1634) and the @triton.jit _flash_attn_fwd
+ * signature (tests/test_flash_attention.py:24-33).
+ * dtype F16/BF16 (MFMA kernel for head_dim 32/64/128) or F32; head_dim <= 128. */
+int tm_flash_attention(const void* q, const void* k, const void* v, void* o, float* lse,
+                       int batch, int heads, int seq_len, int head_dim,
+                       const long long* strides, float scale, int causal, int dtype,
+                       void* stream);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

@@ -1,0 +1,141 @@
+"""FlashAttention forward parity on the GPU against the oracle.
+
+bf16/fp16 outputs within atol 2e-2 / rtol 1e-2 of the oracle's fp64 attention
+on the same (rounded) inputs; LSE (fp32) within 1e-3; the reference's own
+known-answer tests with the reference's tolerances.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import triton_metal_amd as tm
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def _rand(shape, seed, dt, dev):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g).to(dt).to(dev)
+
+
+def _ref(q, k, v, causal, scale=None):
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    return oracle.flash_attention(q.float().cpu().numpy(), k.float().cpu().numpy(),
+                                  v.float().cpu().numpy(), scale, causal)
+
+
+# --- reference known-answer tests (fp32 template ABI, [n_heads*seq, D]) -------
+@pytest.mark.parametrize("name", ["flash_seed555", "flash_seed666", "flash_seed1234",
+                                  "flash_seed123"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_flash_reference_kat(kats, dev, name, dtype):
+    m, a = kats[name]
+    S, D = m["S"], m["D"]
+    Q, K, V = (torch.tensor(a[x], dtype=dtype, device=dev).reshape(S, D) for x in "QKV")
+    O = torch.empty_like(Q)
+    kern = tm.make_flash_attention_kernel(head_dim=D, causal=m["causal"])
+    kern(Q, K, V, O, S, 1.0 / math.sqrt(D))
+    got = O.float().cpu().numpy().reshape(S, D)
+    exp = a["expected"].reshape(S, D)
+    sel = np.zeros((S, D), bool)
+    sel[::m["pos_step"], ::m["dim_step"]] = True
+    tol = np.maximum(m["tol_abs"], np.abs(exp) * m["tol_rel"])
+    if dtype != torch.float32:
+        tol = np.maximum(tol, ATOL + RTOL * np.abs(exp))
+    assert np.all(np.abs(got - exp)[sel] < tol[sel])
+
+
+# --- @triton.jit signature (tests/test_flash_attention.py shapes, seed 42) ----
+FA_SHAPES_NC = [(1, 1, 32, 32), (1, 1, 64, 32), (1, 1, 64, 64), (1, 2, 64, 32), (2, 2, 64, 32),
+                (1, 1, 128, 32)]
+FA_SHAPES_C = [(1, 1, 32, 32), (1, 1, 64, 32), (1, 1, 64, 64), (1, 2, 64, 32), (1, 1, 128, 32)]
+
+
+@pytest.mark.parametrize("causal,shape", [(False, s) for s in FA_SHAPES_NC] +
+                                         [(True, s) for s in FA_SHAPES_C])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_flash_attn_fwd_signature(dev, causal, shape, dtype):
+    Z, H, N, D = shape
+    torch.manual_seed(42)
+    q = torch.randn(Z, H, N, D, dtype=torch.float32)
+    k = torch.randn(Z, H, N, D, dtype=torch.float32)
+    v = torch.randn(Z, H, N, D, dtype=torch.float32)
+    q, k, v = (t.to(dtype).to(dev) for t in (q, k, v))
+    out = torch.empty_like(q)
+    tm.flash_attn_fwd(q, k, v, out, *q.stride(), *k.stride(), *v.stride(), *out.stride(),
+                      Z, H, N, BLOCK_M=min(32, N), BLOCK_N=min(32, N), HEAD_DIM=D,
+                      IS_CAUSAL=causal)
+    ref, _ = _ref(q, k, v, causal)
+    err = np.abs(out.float().cpu().numpy() - ref)
+    if dtype == torch.float32:
+        assert err.max() < 0.01   # the reference test's bound
+    else:
+        assert np.all(err <= ATOL + RTOL * np.abs(ref))
+
+
+# --- MFMA path: shapes, partial tiles, LSE ---------------------------------------
+@pytest.mark.parametrize("S", [1, 17, 64, 100, 128, 257])
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_flash_mfma_shapes(dev, S, D, causal, dtype):
+    B, H = 2, 3
+    q, k, v = (_rand((B, H, S, D), s, dtype, dev) for s in (1, 2, 3))
+    o, lse = tm.attention(q, k, v, causal=causal, return_lse=True)
+    ref, ref_lse = _ref(q, k, v, causal)
+    np.testing.assert_allclose(o.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
+
+
+def test_flash_strided_views(dev):
+    """q, k, v as views into a packed [B, S, 3, H, D] tensor."""
+    B, S, H, D = 2, 96, 4, 64
+    qkv = _rand((B, S, 3, H, D), 7, torch.bfloat16, dev)
+    q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+    o = torch.empty(B, S, H, D, dtype=torch.bfloat16, device=dev).transpose(1, 2)
+    tm.plan_flash_attention(q, k, v, o, causal=True)()
+    ref, _ = _ref(q, k, v, True)
+    np.testing.assert_allclose(o.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+
+
+def test_flash_custom_scale_and_closed_forms(dev):
+    B, H, S, D = 1, 2, 130, 128
+    v = _rand((B, H, S, D), 9, torch.bfloat16, dev)
+    k = _rand((B, H, S, D), 10, torch.bfloat16, dev)
+    q = torch.zeros_like(k)                       # uniform scores
+    o, lse = tm.attention(q, k, v, causal=False, scale=0.3, return_lse=True)
+    np.testing.assert_allclose(o.float().cpu().numpy(),
+                               v.float().mean(2, keepdim=True).expand_as(v).cpu().numpy(),
+                               atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(lse.cpu().numpy(), math.log(S), atol=1e-4)
+    q = _rand((B, H, S, D), 11, torch.bfloat16, dev)
+    o = tm.attention(q, k, v, causal=True, scale=0.3)
+    assert torch.equal(o[:, :, 0], v[:, :, 0])    # row 0 sees only key 0
+
+
+# --- benchmark configuration C4 (sampled rows against the oracle) -----------------
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_config_c4(dev, causal):
+    B, H, S, D = 4, 32, 4096, 128
+    q, k, v = (_rand((B, H, S, D), s, torch.bfloat16, dev) for s in (21, 22, 23))
+    o, lse = tm.attention(q, k, v, causal=causal, return_lse=True)
+    rng = np.random.default_rng(0)
+    for b, h in [(0, 0), (3, 31), (2, 17)]:
+        rows = np.sort(rng.choice(S, 128, replace=False))
+        rows[-1] = S - 1
+        qs = q[b, h, rows].float().cpu().numpy()
+        kk, vv = k[b, h].float().cpu().numpy(), v[b, h].float().cpu().numpy()
+        s = (qs @ kk.T) / math.sqrt(D)
+        if causal:
+            s = np.where(np.arange(S)[None, :] > rows[:, None], -np.inf, s)
+        mx = s.max(1, keepdims=True)
+        p = np.exp(s - mx)
+        ref = (p @ vv) / p.sum(1, keepdims=True)
+        ref_lse = mx[:, 0] + np.log(p.sum(1))
+        np.testing.assert_allclose(o[b, h, rows].float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(lse[b, h, rows].cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)

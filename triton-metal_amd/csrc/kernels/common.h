@@ -34,25 +34,26 @@ enum { TM_DT_F32 = 0, TM_DT_F16 = 1, TM_DT_BF16 = 2 };
 // ---- scalar conversions -----------------------------------------------------
 TM_DEV float bf16_bits_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
-// fp32 -> bf16, round to nearest even (NaN kept quiet).
+typedef float f2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 / fp16 with round to nearest even (v_cvt_pk_bf16_f32 /
+// v_cvt_pk_f16_f32 on gfx950).
 TM_DEV uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 TM_DEV uint16_t f32_to_f16_bits(float f) {
-  half_t h = (half_t)f;  // v_cvt_f16_f32, round to nearest even
+  half_t h = (half_t)f;
   return __builtin_bit_cast(uint16_t, h);
 }
 TM_DEV float f16_bits_to_f32(uint16_t b) { return (float)__builtin_bit_cast(half_t, b); }
 
-// Two fp32 -> packed bf16x2 (RNE).
+// Two fp32 -> packed 16-bit pair (lo in bits 0..15), one instruction.
 TM_DEV uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{lo, hi}, bf2_t));
 }
 TM_DEV uint32_t pack_f16x2(float lo, float hi) {
-  return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{lo, hi}, h2_t));
 }
 
 template <int DT> TM_DEV float load_as_f32(const void* p, size_t i) {
@@ -63,6 +64,18 @@ template <int DT> TM_DEV float load_as_f32(const void* p, size_t i) {
 template <int DT> TM_DEV void store_from_f32(void* p, size_t i, float v) {
   if constexpr (DT == TM_DT_F32) ((float*)p)[i] = v;
   else if constexpr (DT == TM_DT_F16) ((uint16_t*)p)[i] = f32_to_f16_bits(v);
+  else ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
+}
+
+// Runtime-dtype element access (general / fallback kernels only).
+TM_DEV float load_as_f32_rt(const void* p, long long i, int dt) {
+  if (dt == TM_DT_F32) return ((const float*)p)[i];
+  if (dt == TM_DT_F16) return (float)((const half_t*)p)[i];
+  return bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+TM_DEV void store_as_f32_rt(void* p, long long i, int dt, float v) {
+  if (dt == TM_DT_F32) ((float*)p)[i] = v;
+  else if (dt == TM_DT_F16) ((uint16_t*)p)[i] = f32_to_f16_bits(v);
   else ((uint16_t*)p)[i] = f32_to_bf16_bits(v);
 }
 

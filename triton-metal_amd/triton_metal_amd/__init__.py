@@ -9,6 +9,11 @@ from .errors import HipLaunchError, KernelLoadError, NativeLibraryMissing, NoDev
 from .ops import (
     Kernel,
     Launch,
+    attention,
+    flash_attention,
+    flash_attn_fwd,
+    make_flash_attention_kernel,
+    plan_flash_attention,
     plan_int4_matmul,
     plan_int8_matmul,
     plan_matmul,
@@ -26,7 +31,8 @@ from .ops import (
 
 __all__ = [
     "errors", "HipLaunchError", "KernelLoadError", "NativeLibraryMissing", "NoDeviceError",
-    "Kernel", "Launch", "plan_int4_matmul", "plan_int8_matmul", "plan_matmul", "fused_linear", "int4_matmul", "int8_matmul", "make_fused_linear_kernel",
+    "Kernel", "Launch", "attention", "flash_attention", "flash_attn_fwd",
+    "make_flash_attention_kernel", "plan_flash_attention", "plan_int4_matmul", "plan_int8_matmul", "plan_matmul", "fused_linear", "int4_matmul", "int8_matmul", "make_fused_linear_kernel",
     "make_int4_matmul_kernel", "make_int8_matmul_kernel", "make_matmul_kernel",
     "make_simdgroup_matmul_kernel", "matmul", "wq_dequant",
 ]

@@ -39,6 +39,8 @@ SIGNATURES = {
     "tm_wq_dequant": [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_matmul": [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_linear": [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp],
+    "tm_flash_attention": [vp, vp, vp, vp, vp, i32, i32, i32, i32, C.POINTER(C.c_longlong),
+                           C.c_float, i32, i32, vp],
 }
 _RESTYPES = {
     "tm_last_error": C.c_char_p,

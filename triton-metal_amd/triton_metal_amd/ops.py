@@ -14,6 +14,7 @@ raised; nothing falls back to the CPU.
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 
 import torch
@@ -85,7 +86,7 @@ class Launch:
     current stream of the tensors' device then) or on ``stream`` if given.
     The device must be the current HIP device when called."""
 
-    __slots__ = ("_f", "_args", "_what", "dev", "stream")
+    __slots__ = ("_f", "_args", "_what", "dev", "stream", "_keep")
 
     def __init__(self, f, args, what, dev, stream=None):
         self._f = f
@@ -93,6 +94,7 @@ class Launch:
         self._what = what
         self.dev = dev
         self.stream = _stream(dev) if stream is None else stream
+        self._keep = None
 
     def __call__(self, stream=None):
         rc = self._f(*self._args, self.stream if stream is None else stream)
@@ -286,3 +288,99 @@ def make_fused_linear_kernel(has_bias=True):
     def run(input, weight, C, M, N, K):
         return fused_linear(input, weight, C, None, M, N, K)
     return Kernel("fused_linear", run, {"has_bias": False})
+
+
+# ---------------------------------------------------------------------------
+# flash attention forward (A9, A10)
+# ---------------------------------------------------------------------------
+def _bhsd_strides(t, what):
+    if t.dim() != 4:
+        raise ValueError(f"{what} must be [B, H, S, D]")
+    if t.stride(3) != 1:
+        raise ValueError(f"{what}: the head dimension must be contiguous")
+    return list(t.stride()[:3])
+
+
+def plan_flash_attention(q, k, v, o, lse=None, causal=False, scale=None,
+                         stream=None) -> Launch:
+    """Validate and bind a flash attention forward on [B, H, S, D] views.
+
+    ``lse`` (optional) is fp32 [B, H, S] contiguous.  ``scale`` defaults to
+    1/sqrt(D)."""
+    dev = _device_of(q, k, v, o, lse)
+    if not (q.shape == k.shape == v.shape == o.shape):
+        raise ValueError(f"shape mismatch: {q.shape} {k.shape} {v.shape} {o.shape}")
+    if not (q.dtype == k.dtype == v.dtype == o.dtype):
+        raise TypeError("q, k, v and o must share a dtype")
+    B, H, S, D = q.shape
+    if lse is not None:
+        if lse.dtype != torch.float32 or not lse.is_contiguous() or lse.numel() < B * H * S:
+            raise ValueError("lse must be a contiguous fp32 tensor of B*H*S elements")
+    st = (_bhsd_strides(q, "q") + _bhsd_strides(k, "k") + _bhsd_strides(v, "v")
+          + _bhsd_strides(o, "o"))
+    strides = (C.c_longlong * 12)(*st)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), B, H, S, D, strides, float(scale),
+            1 if causal else 0, _dt(q, "q"))
+    launch = Launch(_lib.lib().tm_flash_attention, args, "flash_attention", dev, stream)
+    launch._keep = strides
+    return launch
+
+
+def attention(q, k, v, causal=False, scale=None, return_lse=False):
+    """Allocate O (and LSE) and run flash attention on [B, H, S, D] tensors."""
+    o = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = None
+    if return_lse:
+        B, H, S, _ = q.shape
+        lse = torch.empty(B, H, S, dtype=torch.float32, device=q.device)
+    _run(plan_flash_attention(q, k, v, o, lse, causal, scale))
+    return (o, lse) if return_lse else o
+
+
+def flash_attention(Q, K, V, O, seq_len, scale, causal=False, lse=None):
+    """Buffer order of make_flash_attention_kernel (_msl_templates.py:1624-1634):
+    Q, K, V, O are [n_heads * seq_len, head_dim] contiguous."""
+    D = Q.shape[-1]
+    views = [t.reshape(1, -1, seq_len, D) for t in (Q, K, V, O)]
+    _run(plan_flash_attention(*views, lse=lse, causal=causal, scale=scale))
+    return O
+
+
+def flash_attn_fwd(Q, K, V, Out,
+                   stride_qz, stride_qh, stride_qm, stride_qk,
+                   stride_kz, stride_kh, stride_kn, stride_kk,
+                   stride_vz, stride_vh, stride_vn, stride_vk,
+                   stride_oz, stride_oh, stride_om, stride_ok,
+                   Z, H, N_CTX, BLOCK_M=None, BLOCK_N=None, HEAD_DIM=None, IS_CAUSAL=False,
+                   lse=None):
+    """The signature of the @triton.jit _flash_attn_fwd kernel
+    (tests/test_flash_attention.py:24-33); softmax scale 1/sqrt(HEAD_DIM)
+    (line 54).  BLOCK_M / BLOCK_N are accepted for signature compatibility;
+    the library picks its own tiles."""
+    D = HEAD_DIM if HEAD_DIM is not None else Q.shape[-1]
+    if stride_qk != 1 or stride_kk != 1 or stride_vk != 1 or stride_ok != 1:
+        raise ValueError("the head dimension must be contiguous (stride_*k == 1)")
+
+    def view(t, sz, sh, sm):
+        return torch.as_strided(t, (Z, H, N_CTX, D), (sz, sh, sm, 1), t.storage_offset())
+
+    q = view(Q, stride_qz, stride_qh, stride_qm)
+    k = view(K, stride_kz, stride_kh, stride_kn)
+    v = view(V, stride_vz, stride_vh, stride_vn)
+    o = view(Out, stride_oz, stride_oh, stride_om)
+    _run(plan_flash_attention(q, k, v, o, lse=lse, causal=IS_CAUSAL,
+                              scale=1.0 / math.sqrt(D)))
+    return Out
+
+
+def make_flash_attention_kernel(head_dim=64, Br=16, Bc=16, block_size=256, causal=False):
+    """Returns a callable with the template's buffer order (Q, K, V, O,
+    seq_len, scale); Br/Bc/block_size are accepted for the reference
+    signature (_msl_templates.py:1568), the library chooses its own tiles."""
+    def run(Q, K, V, O, seq_len, scale, lse=None):
+        if Q.shape[-1] != head_dim:
+            raise ValueError(f"kernel built for head_dim={head_dim}, got {Q.shape[-1]}")
+        return flash_attention(Q, K, V, O, seq_len, scale, causal=causal, lse=lse)
+    return Kernel("flash_attention", run, {"head_dim": head_dim, "causal": causal})
