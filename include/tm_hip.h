@@ -141,6 +141,28 @@ int tm_flash_attention(const void* q, const void* k, const void* v, void* o, flo
                        const long long* strides, float scale, int causal, int dtype,
                        void* stream);
 
+/* ---- KDA chunked forward -----------------------------------------------------
+ * No counterpart in the reference (it has no linear attention): the gated
+ * delta rule of Kimi Delta Attention in the [B, T, H, D] layout of its chunked
+ * operator.  Per (batch, head), with S in R^{key_dim x value_dim}:
+ *   S <- diag(exp(g_t)) S;  S <- S + beta_t k_t (v_t - S^T k_t)^T;
+ *   o_t = S^T (scale q_t).
+ * q, k: bf16 [batch, seq_len, heads, key_dim]; v, o: bf16 [.., value_dim];
+ * g: fp32 [batch, seq_len, heads, key_dim] (log decay, finite);
+ * beta: [batch, seq_len, heads], beta_dtype F32 or BF16;
+ * initial_state, final_state: fp32 [batch, heads, key_dim, value_dim], either
+ * may be NULL (zero initial state / final state not returned).
+ * key_dim = value_dim = 128 and chunk_size = 64 (else TM_ERR_UNSUPPORTED).
+ * workspace: 16-byte aligned device memory of at least
+ * tm_kda_workspace_size(...) bytes; its contents are scratch. */
+size_t tm_kda_workspace_size(int batch, int seq_len, int heads, int key_dim, int value_dim,
+                             int chunk_size);
+int tm_kda_chunk_fwd(const void* q, const void* k, const void* v, const float* g,
+                     const void* beta, const float* initial_state, void* o, float* final_state,
+                     int batch, int seq_len, int heads, int key_dim, int value_dim,
+                     int chunk_size, float scale, int beta_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
 #if defined(__GNUC__)
 #pragma GCC visibility pop
 #endif

@@ -45,3 +45,16 @@ extern "C" __global__ void probe_mfma32_layout(float* out) {
   c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   for (int e = 0; e < 16; ++e) out[l * 16 + e] = c[e];
 }
+
+// 16x16x4 fp32: A lane l holds A[l%16][l/16], B lane l holds B[l/16][l%16].
+// A[i][k] = (k == i%4) * (1 + i/4), B[k][j] = 100 k + j, so
+// D[i][j] = (1 + i/4) * (100 (i%4) + j).  out[l * 4 + e] = D element e of lane l.
+extern "C" __global__ void probe_mfma16x4_f32_layout(float* out) {
+  int l = threadIdx.x;
+  int i = l % 16, k = l / 16;
+  float a = (k == i % 4) ? (float)(1 + i / 4) : 0.0f;
+  float b = (float)(100 * k + (l % 16));
+  f4_t c = {0.f, 0.f, 0.f, 0.f};
+  c = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  for (int e = 0; e < 4; ++e) out[l * 4 + e] = c[e];
+}

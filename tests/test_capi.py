@@ -73,3 +73,26 @@ def test_argument_validation_before_any_hip_call():
     assert lib.tm_matmul(p, p, p, 0, 4, 4, 4, 4, 4, L.TM_DT_F16, L.TM_DT_F16, None) == 0
     with pytest.raises(RuntimeError):
         L.check(L.TM_ERR_INVALID_ARG, "probe")
+
+
+def test_kda_workspace_and_validation():
+    import triton_metal_amd._lib as L
+    lib = L.lib()
+    # 74240 bytes per (batch*head, 64-step chunk); C5 = 1 x 16 heads x 128 chunks
+    assert lib.tm_kda_workspace_size(1, 8192, 16, 128, 128, 64) == 16 * 128 * 74240
+    assert lib.tm_kda_workspace_size(2, 65, 3, 128, 128, 64) == 2 * 3 * 2 * 74240
+    assert lib.tm_kda_workspace_size(1, 64, 1, 64, 128, 64) == 0        # unsupported dims
+    assert lib.tm_kda_workspace_size(1, 64, 1, 128, 128, 32) == 0
+    p = ctypes.c_void_p(16)
+    args = [p, p, p, p, p, None, p, None]
+    rc = lib.tm_kda_chunk_fwd(*args, 1, 64, 1, 64, 128, 64, 0.1, L.TM_DT_F32, p, 1 << 20, None)
+    assert rc == L.TM_ERR_UNSUPPORTED and "key_dim" in L.last_error()
+    rc = lib.tm_kda_chunk_fwd(*args, 1, 64, 1, 128, 128, 64, 0.1, L.TM_DT_F16, p, 1 << 20, None)
+    assert rc == L.TM_ERR_INVALID_ARG and "beta_dtype" in L.last_error()
+    rc = lib.tm_kda_chunk_fwd(*args, 1, 64, 1, 128, 128, 64, 0.1, L.TM_DT_F32, p, 100, None)
+    assert rc == L.TM_ERR_INVALID_ARG and "workspace" in L.last_error()
+    rc = lib.tm_kda_chunk_fwd(*args, -1, 64, 1, 128, 128, 64, 0.1, L.TM_DT_F32, p, 0, None)
+    assert rc == L.TM_ERR_INVALID_ARG
+    # no heads: nothing to do
+    assert lib.tm_kda_chunk_fwd(*args, 1, 64, 0, 128, 128, 64, 0.1, L.TM_DT_F32, p, 0,
+                                None) == 0

@@ -60,3 +60,15 @@ def test_mfma32x32x16_layout(utils, dev):
     # only rows < 16 have a non-zero identity entry in A (k < 16)
     expect = np.where(row < 16, expect, 0)
     assert np.array_equal(got, expect.astype(np.float32))
+
+
+def test_mfma16x16x4_f32_layout(utils, dev):
+    _, fn, *_ = utils.load_binary("probe_mfma16x4_f32_layout", PROBE.read_bytes(), 0)
+    out = torch.zeros(64 * 4, dtype=torch.float32, device=dev)
+    utils.launch(fn, (1,), (64,), [out], sync=True)
+    got = out.cpu().numpy().reshape(64, 4)
+    l = np.arange(64)[:, None]
+    e = np.arange(4)[None, :]
+    i = 4 * (l // 16) + e                                   # D[4(l/16)+e][l%16]
+    expect = (1 + i // 4) * (100 * (i % 4) + (l % 16))
+    assert np.array_equal(got, expect.astype(np.float32))

@@ -1,0 +1,174 @@
+"""KDA chunked forward parity on the GPU against the oracle.
+
+The reference has no linear attention, so KDA parity is pinned by the oracle's
+own checks (recurrent vs chunked restatements and closed forms) and, here, by
+the kernel against the fp64 token-by-token recurrence on the same bf16 inputs.
+
+Tolerance (rtol 2e-2 for outputs and final state), written per element as
+    |got - ref| <= 2e-2 * |ref| + 2e-2 * max|ref|
+over each compared tensor: the kernel computes in bf16 MFMA operands with
+fp32 accumulation and an fp32 state, so near-zero entries carry an error set
+by the tensor's scale rather than their own.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+import triton_metal_amd as tm
+
+pytestmark = pytest.mark.gpu
+RTOL = 2e-2
+
+
+def _close(got, ref, what):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    tol = RTOL * np.abs(ref) + RTOL * np.abs(ref).max()
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside tolerance, "
+                           f"max err {np.abs(got - ref).max():.3e}, max|ref| {np.abs(ref).max():.3e}")
+
+
+def kda_inputs(B, T, H, seed=0, gscale=1.0, beta_bf16=False):
+    """C5 recipe: q, k ~ N(0,1) -> bf16 -> L2-normalised over K in fp32 -> bf16;
+    v ~ N(0,1) bf16; beta = sigmoid(N(0,1)); g = -softplus(N(0,1)) * gscale."""
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, 128, generator=gen).to(torch.bfloat16)
+    k = torch.randn(B, T, H, 128, generator=gen).to(torch.bfloat16)
+    q = F.normalize(q.float(), dim=-1).to(torch.bfloat16)
+    k = F.normalize(k.float(), dim=-1).to(torch.bfloat16)
+    v = torch.randn(B, T, H, 128, generator=gen).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    if beta_bf16:
+        beta = beta.to(torch.bfloat16)
+    g = (-F.softplus(torch.randn(B, T, H, 128, generator=gen)) * gscale).float()
+    return q, k, v, g, beta
+
+
+def _ref(q, k, v, g, beta, s0=None, scale=None):
+    f = lambda t: t.float().cpu().numpy()
+    return oracle.kda_recurrent(f(q), f(k), f(v), f(g), f(beta), scale=scale,
+                                initial_state=None if s0 is None else f(s0))
+
+
+def _run(dev, q, k, v, g, beta, s0=None, scale=None):
+    d = lambda t: None if t is None else t.to(dev)
+    o, st = tm.chunk_kda(d(q), d(k), d(v), d(g), d(beta), scale=scale, initial_state=d(s0),
+                         output_final_state=True)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), st.cpu().numpy()
+
+
+@pytest.mark.parametrize("B,T,H", [(1, 1, 1), (1, 64, 1), (2, 100, 2), (1, 257, 3),
+                                   (1, 320, 2)])
+@pytest.mark.parametrize("beta_bf16", [False, True])
+def test_kda_shapes_vs_recurrence(dev, B, T, H, beta_bf16):
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=T + H, beta_bf16=beta_bf16)
+    o, st = _run(dev, q, k, v, g, beta)
+    o_ref, st_ref = _ref(q, k, v, g, beta)
+    _close(o, o_ref, "o")
+    _close(st, st_ref, "final state")
+
+
+@pytest.mark.parametrize("gscale", [0.0, 0.01, 0.3])
+def test_kda_decay_range_with_initial_state(dev, gscale):
+    """Weak or no decay keeps the state (and the initial state) alive across
+    every chunk, so chunk-to-chunk hand-over is exercised."""
+    B, T, H = 1, 200, 2
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=5, gscale=gscale)
+    s0 = torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(9)) * 0.5
+    o, st = _run(dev, q, k, v, g, beta, s0=s0, scale=0.2)
+    o_ref, st_ref = _ref(q, k, v, g, beta, s0=s0, scale=0.2)
+    _close(o, o_ref, "o")
+    _close(st, st_ref, "final state")
+
+
+def test_kda_strong_decay_exact_path(dev):
+    """Decays beyond e^-80 inside a 16-step block take the exact pairwise path."""
+    B, T, H = 1, 130, 2
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=11, gscale=12.0)
+    assert (g.sum(1) < -80).any()
+    o, st = _run(dev, q, k, v, g, beta)
+    o_ref, st_ref = _ref(q, k, v, g, beta)
+    _close(o, o_ref, "o")
+    _close(st, st_ref, "final state")
+
+
+def test_kda_closed_forms(dev):
+    B, T, H = 1, 96, 2
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=3)
+    # beta = 0 and no initial state: nothing is ever written
+    o, st = _run(dev, q, k, v, g, torch.zeros_like(beta))
+    assert not o.any() and not st.any()
+    # one step, no decay, beta = 1: S = k v^T, o = scale (q.k) v
+    q1, k1, v1 = q[:, :1], k[:, :1], v[:, :1]
+    o, st = _run(dev, q1, k1, v1, torch.zeros_like(g[:, :1]), torch.ones_like(beta[:, :1]))
+    kf, vf, qf = (t.double().numpy() for t in (k1, v1, q1))
+    np.testing.assert_allclose(st[0], np.einsum("bhk,bhv->hkv", kf[:, 0], vf[:, 0]),
+                               atol=1e-2, rtol=RTOL)
+    ok = 128 ** -0.5 * np.einsum("bthk,bthk->bth", qf, kf)[..., None] * vf
+    _close(o, ok, "one-step o")
+    # memoryless (decay e^-200 per step): o_t = beta_t scale (q_t . k_t) v_t
+    o, st = _run(dev, q, k, v, torch.full_like(g, -200.0), beta)
+    qf, kf, vf, bf = (t.double().numpy() for t in (q, k, v, beta))
+    om = bf[..., None] * 128 ** -0.5 * np.einsum("bthk,bthk->bth", qf, kf)[..., None] * vf
+    _close(o, om, "memoryless o")
+
+
+def test_kda_orthonormal_keys_retrieval(dev):
+    """No decay, beta = 1, orthonormal keys: S_T = sum_t k_t v_t^T exactly and
+    querying with k_j after step j returns v_j."""
+    B, T, H = 1, 128, 1
+    perm = torch.randperm(128, generator=torch.Generator().manual_seed(4))
+    k = torch.zeros(B, T, H, 128, dtype=torch.bfloat16)
+    k[0, torch.arange(T), 0, perm] = 1.0
+    v = torch.randn(B, T, H, 128, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    q = torch.roll(k, shifts=7, dims=1)        # q_t = k_{t-7}: retrieves v_{t-7} for t >= 7
+    g = torch.zeros(B, T, H, 128)
+    beta = torch.ones(B, T, H)
+    o, st = _run(dev, q, k, v, g, beta, scale=1.0)
+    S_exp = np.zeros((128, 128))
+    S_exp[perm.numpy()] = v[0, :, 0].double().numpy()
+    _close(st[0, 0], S_exp, "final state")
+    _close(o[0, 7:, 0], v[0, :-7, 0].double().numpy(), "retrieved values")
+
+
+def test_kda_split_sequence_bitwise(dev):
+    """Running T steps at once equals running the first half, then the second
+    half from the first half's final state (chunk-aligned split): the state
+    handed over is the kernel's own fp32 state, so the results are identical."""
+    B, T, H = 1, 512, 4
+    q, k, v, g, beta = (t.to(dev) for t in kda_inputs(B, T, H, seed=21, gscale=0.05))
+    o_all, st_all = tm.chunk_kda(q, k, v, g, beta, output_final_state=True)
+    h = 256
+    o1, st1 = tm.chunk_kda(q[:, :h].contiguous(), k[:, :h].contiguous(), v[:, :h].contiguous(),
+                           g[:, :h].contiguous(), beta[:, :h].contiguous(),
+                           output_final_state=True)
+    o2, st2 = tm.chunk_kda(q[:, h:].contiguous(), k[:, h:].contiguous(), v[:, h:].contiguous(),
+                           g[:, h:].contiguous(), beta[:, h:].contiguous(), initial_state=st1,
+                           output_final_state=True)
+    assert torch.equal(o_all[:, :h], o1) and torch.equal(o_all[:, h:], o2)
+    assert torch.equal(st_all, st2)
+
+
+def test_kda_empty_sequence_passes_state_through(dev):
+    q, k, v, g, beta = (t.to(dev) for t in kda_inputs(1, 0, 2, seed=1))
+    s0 = torch.randn(1, 2, 128, 128, device=dev)
+    o, st = tm.chunk_kda(q, k, v, g, beta, initial_state=s0, output_final_state=True)
+    assert o.shape == (1, 0, 2, 128) and torch.equal(st, s0)
+
+
+def test_kda_config_c5_sampled_heads(dev):
+    """Benchmark configuration C5 (B=1, H=16, T=8192): two heads against the
+    fp64 recurrence, every head finite."""
+    B, T, H = 1, 8192, 16
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=0)
+    o, st = _run(dev, q, k, v, g, beta)
+    assert np.isfinite(o).all() and np.isfinite(st).all()
+    for h in (0, 13):
+        sl = slice(h, h + 1)
+        o_ref, st_ref = _ref(q[:, :, sl], k[:, :, sl], v[:, :, sl], g[:, :, sl], beta[:, :, sl])
+        _close(o[:, :, sl], o_ref, f"o head {h}")
+        _close(st[:, sl], st_ref, f"final state head {h}")

@@ -41,11 +41,15 @@ SIGNATURES = {
     "tm_linear": [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp],
     "tm_flash_attention": [vp, vp, vp, vp, vp, i32, i32, i32, i32, C.POINTER(C.c_longlong),
                            C.c_float, i32, i32, vp],
+    "tm_kda_workspace_size": [i32, i32, i32, i32, i32, i32],
+    "tm_kda_chunk_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, C.c_float,
+                         i32, vp, sz, vp],
 }
 _RESTYPES = {
     "tm_last_error": C.c_char_p,
     "tm_version": C.c_char_p,
     "tm_builtin_module_name": C.c_char_p,
+    "tm_kda_workspace_size": sz,
 }
 
 _lock = threading.Lock()

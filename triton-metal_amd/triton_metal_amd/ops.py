@@ -384,3 +384,84 @@ def make_flash_attention_kernel(head_dim=64, Br=16, Bc=16, block_size=256, causa
             raise ValueError(f"kernel built for head_dim={head_dim}, got {Q.shape[-1]}")
         return flash_attention(Q, K, V, O, seq_len, scale, causal=causal, lse=lse)
     return Kernel("flash_attention", run, {"head_dim": head_dim, "causal": causal})
+
+
+# ---------------------------------------------------------------------------
+# KDA chunked forward (no counterpart in the reference)
+# ---------------------------------------------------------------------------
+KDA_KEY_DIM = KDA_VALUE_DIM = 128
+KDA_CHUNK = 64
+
+
+def kda_workspace_size(batch, seq_len, heads, key_dim=KDA_KEY_DIM, value_dim=KDA_VALUE_DIM,
+                       chunk_size=KDA_CHUNK) -> int:
+    """Bytes of device workspace tm_kda_chunk_fwd needs (0 = unsupported shape)."""
+    return int(_lib.lib().tm_kda_workspace_size(batch, seq_len, heads, key_dim, value_dim,
+                                                chunk_size))
+
+
+def plan_chunk_kda(q, k, v, g, beta, o, scale=None, initial_state=None, final_state=None,
+                   workspace=None, chunk_size=KDA_CHUNK, stream=None) -> Launch:
+    """Validate and bind one KDA chunked forward.
+
+    q, k: bf16 [B, T, H, 128]; v, o: bf16 [B, T, H, 128]; g: fp32 [B, T, H, 128]
+    (log decay); beta: fp32 or bf16 [B, T, H]; initial_state / final_state:
+    fp32 [B, H, 128, 128] or None; workspace: a uint8 device tensor of at least
+    kda_workspace_size(B, T, H) bytes (allocated here when None)."""
+    dev = _device_of(q, k, v, g, beta, o, initial_state, final_state, workspace)
+    if q.dim() != 4 or k.shape != q.shape or g.shape != q.shape:
+        raise ValueError(f"q, k, g must share a [B, T, H, K] shape: {q.shape} {k.shape} {g.shape}")
+    B, T, H, Dk = q.shape
+    if v.dim() != 4 or v.shape[:3] != q.shape[:3] or o.shape != v.shape:
+        raise ValueError(f"v and o must be [B, T, H, V]: {v.shape} {o.shape}")
+    Dv = v.shape[3]
+    if beta.shape != (B, T, H):
+        raise ValueError(f"beta must be [B, T, H], got {tuple(beta.shape)}")
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (o, "o")):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if g.dtype != torch.float32:
+        raise TypeError(f"g must be float32, got {g.dtype}")
+    if beta.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"beta must be float32 or bfloat16, got {beta.dtype}")
+    for t, name in ((initial_state, "initial_state"), (final_state, "final_state")):
+        if t is not None and (t.dtype != torch.float32 or tuple(t.shape) != (B, H, Dk, Dv)):
+            raise ValueError(f"{name} must be fp32 [B, H, K, V] = {(B, H, Dk, Dv)}")
+    for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta"), (o, "o"),
+                    (initial_state, "initial_state"), (final_state, "final_state")):
+        _need_contig(t, name)
+    need = _lib.lib().tm_kda_workspace_size(B, T, H, Dk, Dv, chunk_size)
+    if need == 0 and B * T * H > 0:
+        raise ValueError(f"unsupported KDA shape: key_dim={Dk} value_dim={Dv} "
+                         f"chunk_size={chunk_size} (supported: 128, 128, 64)")
+    if workspace is None:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} "
+                         f"bytes, needs {need}")
+    if scale is None:
+        scale = Dk ** -0.5
+    bdt = TM_DT_BF16 if beta.dtype == torch.bfloat16 else TM_DT_F32
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(initial_state), _ptr(o),
+            _ptr(final_state), B, T, H, Dk, Dv, chunk_size, float(scale), bdt, _ptr(workspace),
+            workspace.numel() * workspace.element_size())
+    launch = Launch(_lib.lib().tm_kda_chunk_fwd, args, "kda_chunk_fwd", dev, stream)
+    launch._keep = workspace
+    return launch
+
+
+def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
+              chunk_size=KDA_CHUNK):
+    """Kimi Delta Attention, chunked forward, in the calling convention of the
+    published ``chunk_kda`` operator: [B, T, H, D] tensors, g the per-channel
+    log decay, beta the per-step write strength, scale default K**-0.5.
+
+    Returns (o [B, T, H, V] bf16, final_state fp32 [B, H, K, V] or None)."""
+    B, T, H, Dk = q.shape
+    Dv = v.shape[-1]
+    o = torch.empty(B, T, H, Dv, dtype=torch.bfloat16, device=q.device)
+    st = (torch.empty(B, H, Dk, Dv, dtype=torch.float32, device=q.device)
+          if output_final_state else None)
+    _run(plan_chunk_kda(q, k, v, g, beta, o, scale=scale, initial_state=initial_state,
+                        final_state=st, chunk_size=chunk_size))
+    return o, st
