@@ -115,6 +115,23 @@ TM_DEV uint32_t h2_bits(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
 
 // Buffer-free 16-byte global load that the compiler keeps as one dwordx4.
 TM_DEV u4_t ldg128(const void* p) { return *(const u4_t*)p; }
+
+// Direct global -> LDS copy (global_load_lds_dwordx4): lane l of the wave
+// deposits the 16 bytes at g at LDS address lds_base + 16 l (lds_base must be
+// wave-uniform).  The copy is counted by vmcnt like a load.
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void glb_void_t;
+TM_DEV void g2lds16(const void* g, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)lds_base, 16, 0, 0);
+}
+
+// Workgroup barrier for data exchanged through LDS alone: waits for this
+// wave's LDS operations (lgkmcnt) and meets the other waves, without draining
+// outstanding global loads, stores or global -> LDS copies as the fence of
+// __syncthreads() does.  The asm's memory clobber keeps the compiler from
+// moving memory accesses across it; reads of LDS filled by global -> LDS
+// copies still get their vmcnt wait from the compiler.
+TM_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 TM_DEV u2_t ldg64(const void* p) { return *(const u2_t*)p; }
 
 // A 32-bit constant the compiler must keep in a VGPR (it cannot see its value).

@@ -93,14 +93,9 @@ template <int D> TM_DEV int v_swz(int r) {
   else return 0;
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef const __attribute__((address_space(1))) void glb_void_t;
 typedef short s4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s4_t lds_s4_t;
 
-TM_DEV void g2lds16(const void* g, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)lds_base, 16, 0, 0);
-}
 TM_DEV u2_t lds_tr16(const uint16_t* p) {
   s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_t*)(p));
   return __builtin_bit_cast(u2_t, v);

@@ -31,23 +31,37 @@
 // factor is >= 1; the fast path is used while every |G_t - G_r| in the chunk
 // is <= 80 (factors within [e^-80, e^80], normal fp32/bf16 numbers), else the
 // diagonal blocks are recomputed with the exact pairwise exponent.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
 constexpr int KC = 64;    // chunk length
 constexpr int KD = 128;   // key dim
 constexpr int VD = 128;   // value dim
-constexpr float kExpRange = 80.0f;
+constexpr int GP = KD + 4;             // padded row of the decay tile (bank spread)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kExp2Range = 80.0f * kLog2e;  // |G_t - G_r| <= 80 in natural-log units
 
-// Workspace of one (head, chunk), bytes.
-constexpr size_t WS_WK = 0;                    // bf16 [64][128]  W_k
-constexpr size_t WS_WV = WS_WK + KC * KD * 2;  // bf16 [64][128]  W_v
-constexpr size_t WS_QD = WS_WV + KC * VD * 2;  // bf16 [64][128]  scale q exp(G)
-constexpr size_t WS_KT = WS_QD + KC * KD * 2;  // bf16 [128][64]  (k exp(G_C - G))^T
-constexpr size_t WS_AQ = WS_KT + KD * KC * 2;  // bf16 [64][64]   Aqk
-constexpr size_t WS_GC = WS_AQ + KC * KC * 2;  // fp32 [128]      exp(G_C)
+// Workspace of one (head, chunk), bytes.  The matrices kda_state reads as
+// MFMA operands are stored in fragment order: 1 KB blocks, one per (16-row
+// block, 32-column step), in which lane l = 16 q + r of the reading wave finds
+// its 16 bytes (row r, columns 8q..8q+7 of the step) at 16 l - so every load
+// there is one contiguous 1 KB.
+constexpr size_t WS_WK = 0;                    // W_k [64][128]      fragments (16 blocks)
+constexpr size_t WS_WV = WS_WK + KC * KD * 2;  // W_v [64/4][128][4] (4 steps of a column together)
+constexpr size_t WS_QD = WS_WV + KC * VD * 2;  // scale q exp(G) [64][128] fragments
+constexpr size_t WS_KT = WS_QD + KC * KD * 2;  // (k exp(G_C - G))^T [128][64] fragments
+constexpr size_t WS_AQ = WS_KT + KD * KC * 2;  // Aqk [64][64]       fragments (8 blocks)
+constexpr size_t WS_GC = WS_AQ + KC * KC * 2;  // exp(G_C), fp32 [128]
 constexpr size_t WS_CHUNK = WS_GC + KD * 4;
 static_assert(WS_CHUNK == 74240, "workspace layout is part of the C ABI");
+
+// Byte offset of (row, 8-column group cg) of a matrix with `steps` 32-column
+// steps per row, stored in fragment order.
+TM_DEV int frag_off(int row, int cg, int steps) {
+  return (((row >> 4) * steps + (cg >> 2)) * 64 + (cg & 3) * 16 + (row & 15)) * 16;
+}
 
 TM_DEV u4_t pack8_bf16(const float* x) {
   u4_t r;
@@ -68,6 +82,8 @@ TM_DEV void load8_f32(const float* p, float* x) {
   x[0] = a[0]; x[1] = a[1]; x[2] = a[2]; x[3] = a[3];
   x[4] = b[0]; x[5] = b[1]; x[6] = b[2]; x[7] = b[3];
 }
+// 2^x on the transcendental unit (v_exp_f32).
+TM_DEV float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 TM_DEV f4_t mfma_f32_16x16x4(float a, float b, f4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -95,14 +111,14 @@ struct KdaParams {
 // ----------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
   // LDS regions; the ones marked "then" are reused after a barrier.
-  __shared__ __align__(16) unsigned char lds_g[KC * KD * 4];   // G, then T fp32 + R
+  __shared__ __align__(16) unsigned char lds_g[KC * GP * 4];   // G log2(e), then T fp32 + R
   __shared__ __align__(16) unsigned char lds_k[KC * 136 * 2];  // k, then T bf16
   __shared__ __align__(16) unsigned char lds_v[KC * 136 * 2];  // v, then Aqk bf16
   __shared__ __align__(16) float Af[KC][68];                   // scan totals, then A
   __shared__ __align__(16) uint16_t Bt[KD + VD][72];           // [beta k e^G | beta v]^T
   __shared__ float bet[KC];
 
-  float(*Gs)[KD] = (float(*)[KD])lds_g;
+  float(*Gs)[GP] = (float(*)[GP])lds_g;
   float(*Tf)[68] = (float(*)[68])lds_g;                      // 17408 B
   float(*Rs)[16][17] = (float(*)[16][17])(lds_g + KC * 68 * 4);
   uint16_t(*Ks)[136] = (uint16_t(*)[136])lds_k;
@@ -163,14 +179,14 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
     *(u4_t*)&Ks[row][8 * c8] = kr[j];
     *(u4_t*)&Vs[row][8 * c8] = vr[j];
   }
-  __syncthreads();
+  lds_barrier();
   {
     f4_t pre = {0.f, 0.f, 0.f, 0.f};
     for (int j = 0; j < seg; ++j) pre += *(const f4_t*)&tot[j][4 * c4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) *(f4_t*)&Gs[8 * seg + e][4 * c4] = gv[e] + pre;
+    for (int e = 0; e < 8; ++e) *(f4_t*)&Gs[8 * seg + e][4 * c4] = (gv[e] + pre) * kLog2e;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 2. t-side operands, Qd, K_end^T, B^T, exp(G_C) ----------------------
   u4_t kt_op[4], qt_op[4];
@@ -186,15 +202,15 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float d = gt[e] - gr[e];
-      ok &= (d >= -kExpRange) && (d <= kExpRange);
-      const float ex = __expf(d);
+      ok &= (d >= -kExp2Range) && (d <= kExp2Range);
+      const float ex = ex2(d);
       kt[e] = kf[e] * ex;
       qt[e] = p.scale * qf[e] * ex;
-      qd[e] = p.scale * qf[e] * __expf(gt[e]);
+      qd[e] = p.scale * qf[e] * ex2(gt[e]);
     }
     kt_op[ks] = pack8_bf16(kt);
     qt_op[ks] = pack8_bf16(qt);
-    *(u4_t*)(ws + WS_QD + 2 * (trow * KD + c0)) = pack8_bf16(qd);
+    *(u4_t*)(ws + WS_QD + frag_off(trow, 4 * ks + q4, 4)) = pack8_bf16(qd);
   }
   // (c, 8-step group) tasks: K_end^T to the workspace, B^T to LDS
 #pragma unroll
@@ -207,15 +223,15 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
       const int t = 8 * tg + e;
       const float kf = bf16_bits_to_f32(Ks[t][c]);
       const float gtc = Gs[t][c];
-      ke[e] = kf * __expf(gend - gtc);
-      bk[e] = bet[t] * kf * __expf(gtc);
+      ke[e] = kf * ex2(gend - gtc);
+      bk[e] = bet[t] * kf * ex2(gtc);
       bvv[e] = bet[t] * bf16_bits_to_f32(Vs[t][c]);
     }
-    *(u4_t*)(ws + WS_KT + 2 * (c * KC + 8 * tg)) = pack8_bf16(ke);
+    *(u4_t*)(ws + WS_KT + frag_off(c, tg, 2)) = pack8_bf16(ke);
     *(u4_t*)&Bt[c][8 * tg] = pack8_bf16(bk);
     *(u4_t*)&Bt[KD + c][8 * tg] = pack8_bf16(bvv);
   }
-  if (tid < KD) ((float*)(ws + WS_GC))[tid] = __expf(Gs[KC - 1][tid]);
+  if (tid < KD) ((float*)(ws + WS_GC))[tid] = ex2(Gs[KC - 1][tid]);
   const int slow = __syncthreads_or(!ok);  // also orders Vs reads before AQs writes
 
   // ---- 3. A and Aqk: wave w computes rows 16w..16w+15 ----------------------
@@ -230,7 +246,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
       load8_f32(&Gs[r0][c0], gr);
       unpack8_bf16(*(const u4_t*)&Ks[srow][c0], kf);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = kf[e] * __expf(gr[e] - gs[e]);
+      for (int e = 0; e < 8; ++e) x[e] = kf[e] * ex2(gr[e] - gs[e]);
       ks_op[ks] = pack8_bf16(x);
     }
     f4_t acc_a = {0.f, 0.f, 0.f, 0.f}, acc_q = {0.f, 0.f, 0.f, 0.f};
@@ -251,14 +267,14 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
     for (int e = 0; e < 4; ++e) AQs[r0 + 4 * q4 + e][16 * sb + l16] = 0;
   if (slow) {
     // exact pairwise exponent for the diagonal blocks (s <= t, same block)
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < 4 * 256; i += 256) {
       const int blk = i >> 8, tl = (i >> 4) & 15, sl = i & 15;
       if (sl > tl) continue;
       const int t = 16 * blk + tl, s = 16 * blk + sl;
       float a = 0.0f, aq = 0.0f;
       for (int c = 0; c < KD; ++c) {
-        const float ex = __expf(Gs[t][c] - Gs[s][c]);
+        const float ex = ex2(Gs[t][c] - Gs[s][c]);
         const float ksv = bf16_bits_to_f32(Ks[s][c]) * ex;
         a += bf16_bits_to_f32(Ks[t][c]) * ksv;
         const float qv = t < nt ? bf16_bits_to_f32(p.q[base_k + t * rs + c]) : 0.0f;
@@ -268,13 +284,15 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
       AQs[t][s] = f32_to_bf16_bits(p.scale * aq);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 4. Aqk to the workspace; T = (I + A)^-1 -----------------------------
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int i = tid + 256 * j, row = i >> 3, c8 = i & 7;
-    *(u4_t*)(ws + WS_AQ + 2 * (row * KC + 8 * c8)) = *(const u4_t*)&AQs[row][8 * c8];
+    // fragment slot i: block i/64 = (row block, step), lane = 16 q + r
+    const int i = tid + 256 * j, blk = i >> 6, ln = i & 63;
+    const int row = 16 * (blk >> 1) + (ln & 15), cg = 4 * (blk & 1) + (ln >> 4);
+    *(u4_t*)(ws + WS_AQ + 16 * i) = *(const u4_t*)&AQs[row][8 * cg];
   }
   if (wave == 0) {
     // diagonal blocks by forward substitution: lane = (block, column)
@@ -290,7 +308,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
 #pragma unroll
     for (int m = 0; m < 16; ++m) Tf[base + m][base + j] = x[m];
   }
-  __syncthreads();
+  lds_barrier();
   // off-diagonal blocks, by distance d from the diagonal:
   //   T_ij = -T_ii sum_{m=j}^{i-1} A_im T_mj
   for (int d = 1; d < 4; ++d) {
@@ -315,7 +333,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) Tf[16 * ib + 4 * q4 + e][16 * jb + l16] = -tij[e];
     }
-    __syncthreads();
+    lds_barrier();
   }
   {
     // T to bf16 with the upper blocks zeroed
@@ -326,26 +344,41 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
     *(u4_t*)&Tb[row][cb] = pack8_bf16(x);
     *(u4_t*)&Tb[row][cb + 8] = pack8_bf16(x + 8);
   }
-  __syncthreads();
+  lds_barrier();
 
-  // ---- 5. [W_k | W_v]^T = B^T T^T: wave w owns columns 64w..64w+63 --------
-  uint16_t* wout = (uint16_t*)(ws + (wave < 2 ? WS_WK : WS_WV));
+  // ---- 5. W_k = T B_k, W_v = T B_v: wave w owns columns 64w..64w+63 -------
+  // W_k is computed transposed (D = [column][step]) so that each lane holds 4
+  // consecutive columns of one step (8 bytes of a fragment); W_v straight
+  // (D = [step][column]), 4 consecutive steps of one column.
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
-    const int c = 64 * wave + 16 * cb + l16;
-    const u4_t a0 = *(const u4_t*)&Bt[c][8 * q4];
-    const u4_t a1 = *(const u4_t*)&Bt[c][32 + 8 * q4];
-    const int colg = (64 * wave + 16 * cb + 4 * q4) & 127;
+    const int c = 64 * wave + 16 * cb + l16;  // B^T row this lane reads
+    const u4_t b0 = *(const u4_t*)&Bt[c][8 * q4];
+    const u4_t b1 = *(const u4_t*)&Bt[c][32 + 8 * q4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = 16 * i + l16;
+      const int t = 16 * i + l16;             // T row this lane reads
+      const u4_t t0 = *(const u4_t*)&Tb[t][8 * q4];
       f4_t acc = {0.f, 0.f, 0.f, 0.f};
-      acc = mfma16<true>(a0, *(const u4_t*)&Tb[t][8 * q4], acc);
-      if (i >= 2) acc = mfma16<true>(a1, *(const u4_t*)&Tb[t][32 + 8 * q4], acc);
+      if (wave < 2) {
+        acc = mfma16<true>(b0, t0, acc);
+        if (i >= 2) acc = mfma16<true>(b1, *(const u4_t*)&Tb[t][32 + 8 * q4], acc);
+      } else {
+        acc = mfma16<true>(t0, b0, acc);
+        if (i >= 2) acc = mfma16<true>(*(const u4_t*)&Tb[t][32 + 8 * q4], b1, acc);
+      }
       u2_t w;
       w.x = pack_bf16x2(acc[0], acc[1]);
       w.y = pack_bf16x2(acc[2], acc[3]);
-      *(u2_t*)(wout + t * KD + colg) = w;
+      if (wave < 2) {
+        // W_k[t][c0 .. c0+3], c0 = 64w + 16cb + 4q4
+        const int c0 = 64 * wave + 16 * cb + 4 * q4;
+        *(u2_t*)(ws + WS_WK + frag_off(t, c0 >> 3, 4) + 2 * (c0 & 7)) = w;
+      } else {
+        // W_v[t0 .. t0+3][cv], t0 = 16i + 4q4, cv = 64(w-2) + 16cb + l16
+        const int cv = 64 * (wave - 2) + 16 * cb + l16, tq = 4 * i + q4;
+        *(u2_t*)(ws + WS_WV + 8 * (tq * VD + cv)) = w;
+      }
     }
   }
 }
@@ -355,41 +388,48 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
 // value columns v0 .. v0+15 of one head and walks the chunks in order.
 // Wave w holds state rows 32w .. 32w+31 (two 16x16 tiles, fp32) and computes
 // U / O rows 16w .. 16w+15.  S and U are shared through LDS transposed
-// ([column][row], bf16) so that B-operand reads are 16 bytes.  The operands
-// of chunk c+1 are loaded while chunk c is computed.  When B*H is a multiple
-// of 8 the 8 column slices of a head run on one XCD and share its L2.
+// ([column][row], bf16) so that B-operand reads are 16 bytes.  The chunk
+// operands are read straight from the fragment-ordered workspace (one
+// contiguous 1 KB per load instruction) one chunk ahead, alternating two
+// register sets so that no prefetched value is ever copied (a copy would
+// wait for the load).  O is computed transposed (D = [column][step]) so that
+// each lane stores 4 consecutive columns.  When B*H is a multiple of 8 the 8
+// column slices of a head run on one XCD and share its L2.
 // ----------------------------------------------------------------------------
 namespace {
 struct ChunkOps {
   u4_t wk[4], qd[4], aq[2], kt[4];
   f4_t gc[2];
-  float wv[4];
+  u2_t wv;  // 4 raw bf16 values of W_v: converted where used
 };
-TM_DEV void load_chunk(const uint8_t* ws, int wave, int q4, int l16, int v0, ChunkOps& o) {
-  const uint16_t* wk = (const uint16_t*)(ws + WS_WK);
-  const uint16_t* wv = (const uint16_t*)(ws + WS_WV);
-  const uint16_t* qd = (const uint16_t*)(ws + WS_QD);
-  const uint16_t* kt = (const uint16_t*)(ws + WS_KT);
-  const uint16_t* aq = (const uint16_t*)(ws + WS_AQ);
+
+// The loads of one chunk in three groups, so that a step can spread them
+// over its phases (the per-CU address path, not latency, bounds the step).
+TM_DEV void load_chunk_a(const uint8_t* ws, int wave, int lane, ChunkOps& o) {
+  const uint8_t* lw = ws + 16 * lane;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) o.wk[ks] = ldg128(lw + WS_WK + 1024 * (4 * wave + ks));
+}
+TM_DEV void load_chunk_b(const uint8_t* ws, int wave, int lane, int q4, int v0, ChunkOps& o) {
+  const uint8_t* lw = ws + 16 * lane;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o.kt[j] = ldg128(lw + WS_KT + 1024 * (4 * wave + j));
   const float* gc = (const float*)(ws + WS_GC);
-  const int urow = 16 * wave + l16;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    o.wk[ks] = ldg128(wk + urow * KD + 32 * ks + 8 * q4);
-    o.qd[ks] = ldg128(qd + urow * KD + 32 * ks + 8 * q4);
-  }
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) o.aq[ks] = ldg128(aq + urow * KC + 32 * ks + 8 * q4);
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      o.kt[2 * tt + ks] = ldg128(kt + (32 * wave + 16 * tt + l16) * KC + 32 * ks + 8 * q4);
 #pragma unroll
   for (int tt = 0; tt < 2; ++tt) o.gc[tt] = *(const f4_t*)(gc + 32 * wave + 16 * tt + 4 * q4);
+  o.wv = ldg64(ws + WS_WV + 8 * ((4 * wave + q4) * VD + v0 + (lane & 15)));
+}
+TM_DEV void load_chunk_c(const uint8_t* ws, int wave, int lane, ChunkOps& o) {
+  const uint8_t* lw = ws + 16 * lane;
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
-    o.wv[e] = bf16_bits_to_f32(wv[(16 * wave + 4 * q4 + e) * VD + v0 + l16]);
+  for (int ks = 0; ks < 4; ++ks) o.qd[ks] = ldg128(lw + WS_QD + 1024 * (4 * wave + ks));
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) o.aq[ks] = ldg128(lw + WS_AQ + 1024 * (2 * wave + ks));
+}
+TM_DEV void load_chunk(const uint8_t* ws, int wave, int lane, int q4, int v0, ChunkOps& o) {
+  load_chunk_a(ws, wave, lane, o);
+  load_chunk_b(ws, wave, lane, q4, v0, o);
+  load_chunk_c(ws, wave, lane, o);
 }
 }  // namespace
 
@@ -425,12 +465,13 @@ extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
     }
 
   const uint8_t* wsh = p.ws + (size_t)bh * p.NC * WS_CHUNK;
-  ChunkOps cur;
-  if (p.NC > 0) load_chunk(wsh, wave, q4, l16, v0, cur);
-  for (int c = 0; c < p.NC; ++c) {
-    const int buf = c & 1;
-    ChunkOps nxt;
-    load_chunk(wsh + (size_t)min(c + 1, p.NC - 1) * WS_CHUNK, wave, q4, l16, v0, nxt);
+  // One chunk step: consume `cur` (chunk c) and start loading chunk c+1
+  // into `nxt`.
+  auto step = [&](const int c, auto bufc, const ChunkOps& cur, ChunkOps& nxt) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint8_t* wsn = wsh + (size_t)min(c + 1, p.NC - 1) * WS_CHUNK;
+    load_chunk_a(wsn, wave, lane, nxt);
+    asm volatile("" ::: "memory");  // issue points of the next chunk's loads stay spread
 
     // (a) S -> LDS as S^T bf16
 #pragma unroll
@@ -439,44 +480,47 @@ extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
       u2_t w;
       w.x = pack_bf16x2(S[tt][0], S[tt][1]);
       w.y = pack_bf16x2(S[tt][2], S[tt][3]);
-      *(u2_t*)(&Sbt[buf][l16][row]) = w;
+      *(u2_t*)(&Sbt[BUF][l16][row]) = w;
     }
-    __syncthreads();
+    lds_barrier();
+    load_chunk_b(wsn, wave, lane, q4, v0, nxt);
+    asm volatile("" ::: "memory");
 
-    // (b) U rows 16w.. : U = W_v - W_k S
+    // (b) U rows 16w.. : U = W_v - W_k S; O^T = S^T Qd^T (first part)
     u4_t sb[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) sb[ks] = *(const u4_t*)(&Sbt[buf][l16][32 * ks + 8 * q4]);
+    for (int ks = 0; ks < 4; ++ks) sb[ks] = *(const u4_t*)(&Sbt[BUF][l16][32 * ks + 8 * q4]);
     f4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mfma16<true>(cur.wk[ks], sb[ks], acc);
-    f4_t U;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) U[e] = cur.wv[e] - acc[e];
+    const float wv[4] = {__uint_as_float(cur.wv.x << 16), __uint_as_float(cur.wv.x & 0xffff0000u),
+                         __uint_as_float(cur.wv.y << 16), __uint_as_float(cur.wv.y & 0xffff0000u)};
     {
       u2_t w;
-      w.x = pack_bf16x2(U[0], U[1]);
-      w.y = pack_bf16x2(U[2], U[3]);
-      *(u2_t*)(&Ubt[buf][l16][16 * wave + 4 * q4]) = w;
+      w.x = pack_bf16x2(wv[0] - acc[0], wv[1] - acc[1]);
+      w.y = pack_bf16x2(wv[2] - acc[2], wv[3] - acc[3]);
+      *(u2_t*)(&Ubt[BUF][l16][16 * wave + 4 * q4]) = w;
     }
-    // O partial from S while U is shared
     f4_t o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) o = mfma16<true>(cur.qd[ks], sb[ks], o);
-    __syncthreads();
+    for (int ks = 0; ks < 4; ++ks) o = mfma16<true>(sb[ks], cur.qd[ks], o);
+    lds_barrier();
+    load_chunk_c(wsn, wave, lane, nxt);
+    asm volatile("" ::: "memory");
 
-    // (c) O rows 16w.. += Aqk U
+    // (c) O^T += U^T Aqk^T; lane holds O[t][v0 + 4q4 .. +3], t = 64c + 16w + l16
     u4_t ub[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) ub[ks] = *(const u4_t*)(&Ubt[buf][l16][32 * ks + 8 * q4]);
+    for (int ks = 0; ks < 2; ++ks) ub[ks] = *(const u4_t*)(&Ubt[BUF][l16][32 * ks + 8 * q4]);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) o = mfma16<true>(cur.aq[ks], ub[ks], o);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = c * KC + 16 * wave + 4 * q4 + e;
+    for (int ks = 0; ks < 2; ++ks) o = mfma16<true>(ub[ks], cur.aq[ks], o);
+    {
+      const int t = c * KC + 16 * wave + l16;
+      u2_t w;
+      w.x = pack_bf16x2(o[0], o[1]);
+      w.y = pack_bf16x2(o[2], o[3]);
       if (t < p.T)
-        p.o[((long long)b * p.T + t) * rsv + (long long)h * VD + v0 + l16] =
-            f32_to_bf16_bits(o[e]);
+        *(u2_t*)(p.o + ((long long)b * p.T + t) * rsv + (long long)h * VD + v0 + 4 * q4) = w;
     }
 
     // (d) S = diag(exp(G_C)) S + K_end^T U
@@ -486,8 +530,17 @@ extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) S[tt] = mfma16<true>(cur.kt[2 * tt + ks], ub[ks], S[tt]);
     }
-    cur = nxt;
+  };
+  ChunkOps ops0, ops1;
+  if (p.NC > 0) load_chunk(wsh, wave, lane, q4, v0, ops0);
+  // pairs of steps with no branch between them, so that each operand set
+  // keeps its registers around the loop; an odd last chunk after the loop
+  int c = 0;
+  for (; c + 1 < p.NC; c += 2) {
+    step(c, std::integral_constant<int, 0>(), ops0, ops1);
+    step(c + 1, std::integral_constant<int, 1>(), ops1, ops0);
   }
+  if (c < p.NC) step(c, std::integral_constant<int, 0>(), ops0, ops1);
 
   if (p.st) {
 #pragma unroll
