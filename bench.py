@@ -168,6 +168,28 @@ WORKLOADS = {
 HEADLINE = "w4a16_m1"
 
 
+def hbm_copy(dev, nbytes=512 << 20):
+    """Plain device copy of a known size: the calibration kernel for the
+    FETCH_SIZE / WRITE_SIZE counters (not part of the default run)."""
+    import torch
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+
+    def run(stream=None):
+        if stream is None:
+            dst.copy_(src)
+        else:
+            with torch.cuda.stream(torch.cuda.ExternalStream(stream)):
+                dst.copy_(src)
+    return dict(launches=[run], keep=(src, dst), bytes=2 * nbytes, flops=0, bound="hbm",
+                dtype="bf16", config={"workload": "hbm_copy", "bytes_read": nbytes,
+                                      "bytes_written": nbytes})
+
+
+# opt-in workloads (--only NAME), not part of the default run
+EXTRA = {"hbm_copy": hbm_copy}
+
+
 def time_workload(w, steps, warmup, graph=True):
     """Average ms per step: eagerly enqueued, and replayed from one HIP graph
     holding the K steps (the launch pattern of a captured decode loop)."""
@@ -252,6 +274,21 @@ def cpu_baseline(target_s=12.0):
                        f"{cores} threads")
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "wq_gemv4_w4a16_m1_hbm_traffic.md"
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the headline kernel, from the calibrated
+    FETCH_SIZE / WRITE_SIZE passes committed under profiles/ (None if absent)."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -264,7 +301,7 @@ def main():
                     help="time eagerly enqueued calls only (no HIP graph)")
     args = ap.parse_args()
     if args.list:
-        print("\n".join(WORKLOADS))
+        print("\n".join(list(WORKLOADS) + [f"{n} (opt-in)" for n in EXTRA]))
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -281,7 +318,7 @@ def main():
     results = {}
     for name in names:
         log(f"[bench] {name}: setup")
-        w = WORKLOADS[name](dev)
+        w = (WORKLOADS.get(name) or EXTRA[name])(dev)
         ms, eager_ms = time_workload(w, args.steps, args.warmup, graph=not args.eager)
         results[name] = summarize(w, ms, eager_ms)
         log(f"[bench] {name}: {results[name]['us_per_call']} us/call "
@@ -308,7 +345,7 @@ def main():
         "timing": "eager" if args.eager else "K steps replayed from one HIP graph; "
                   "eager_us_per_call is the same loop enqueued from Python",
         "config": head["config"],
-        "roofline": dict(head["roofline"], traffic=None),
+        "roofline": dict(head["roofline"], traffic=profiled_traffic()),
         "workloads": {k: v for k, v in results.items() if k != HEADLINE},
     }
     if not args.no_cpu:

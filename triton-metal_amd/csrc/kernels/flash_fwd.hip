@@ -19,9 +19,10 @@
 //   O^T += V^T P^T: P leaves the S^T accumulators directly as the B operand
 //         (the key order inside a 16-key MFMA step is chosen to match the
 //         accumulator layout, and V^T is read from LDS in that same order).
-// K tiles are stored row-major and V tiles transposed ([D][64 keys]) in LDS,
-// both double-buffered; the next block's global loads are in flight while
-// the current block computes.  Softmax runs in the exp2 domain with
+// K and V tiles stream from global memory straight into LDS
+// (global_load_lds_dwordx4, row-major with XOR swizzles, double-buffered); V^T
+// operands are read with ds_read_b64_tr_b16.  The next block's copies are in
+// flight while the current block computes.  Softmax runs in the exp2 domain with
 // scale * log2(e) folded into the scores.  Causal: key blocks past a wave's
 // last query are skipped, and the heaviest query blocks are scheduled first.
 //
