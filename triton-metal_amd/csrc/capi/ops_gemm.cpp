@@ -64,8 +64,9 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
   const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
   const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
   // exact-shape int4 GEMV: K = NW * PF * 128, G = 128
-  if (fast && qbits == 4 && M <= 8 && G == 128 && (K == 4096 || K == 8192)) {
-    size_t glds = (size_t)M * (K + 8) * 2 + (size_t)(K / 128) * 8 * 4;
+  if (fast && qbits == 4 && M <= 8 && G == 128 && (K == 4096 || K == 8192) && aligned16(S) &&
+      (!Z || aligned16(Z))) {
+    size_t glds = (size_t)M * (K + 8) * 2 + (size_t)(K / 128) * 8 * 4 + (size_t)(K / 128) * 64;
     if (glds <= (size_t)max_dynamic_lds()) {
       const int pf = K == 4096 ? 4 : 8;
       char name[64];

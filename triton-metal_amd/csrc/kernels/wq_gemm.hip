@@ -346,8 +346,10 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
 // block = NW waves; wave w owns k = w*PF*128 .. +PF*128 of the workgroup's
 // 16 columns.  Everything is unrolled at compile time: PF 16-byte weight
 // loads per lane, one vector load of the PF scales (and zero-points) per
-// lane, PF independent MFMA chains.  Dynamic LDS: M * (K + 8) * 2 bytes of X
-// plus (K / 128) * 8 * 4 bytes of chunk sums laid out [chunk][row 0..7].
+// lane, MFMAs chunk by chunk as the weights arrive.  Dynamic LDS: M * (K + 8)
+// * 2 bytes of X, (K / 128) * 8 * 4 bytes of chunk sums laid out
+// [chunk][row 0..7], then the workgroup's scales and zero-points (16 rows x
+// K / 128, 2 bytes each).  S (and Z) must be 16-byte aligned.
 // ----------------------------------------------------------------------------
 template <bool BF16, int ZDT, int NW, int PF>
 __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
@@ -363,43 +365,32 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
   const int ldx = K + 8;
   const int nch = K >> 7;
   float* xsum = (float*)(xs + (size_t)M * ldx);  // [nch][8]
+  uint16_t* sst = (uint16_t*)(xsum + nch * 8);   // scales of the 16 columns [16][nch]
+  uint16_t* zst = sst + 16 * nch;                // zero-points [16][nch] (bytes if uint8)
   const int n = blockIdx.x * 16 + (lane & 15), q = lane >> 4;
   const int m = min(lane & 15, M - 1);
   const int kbeg = wave * (PF * 128);
   const uint32_t vmask = vgpr_const(0x000F000Fu), vmagic = vgpr_const(w4_magic<BF16>());
 
-  // 1. first X row pieces (PF / 4 per thread), 2. weights + scales, 3. stage
+  // 1. first X row pieces (PF / 4 per thread), this workgroup's scales and
+  //    zero-points (16 rows x nch, one contiguous block each), 2. weights,
+  //    3. stage.  The few small loads go first so that each chunk's MFMAs
+  //    can start as soon as that chunk's weights arrive.
   constexpr int XP = PF / 4;  // pieces per thread per row: K / 8 / NT
   u4_t xv[XP];
 #pragma unroll
   for (int u = 0; u < XP; ++u) xv[u] = ldg128(X + (size_t)(tid + NT * u) * 8);
+  const int sbytes = 32 * nch;
+  const int zbytes = ZDT == 3 ? 16 * nch : 32 * nch;
+  u4_t sv = {0u, 0u, 0u, 0u}, zv = {0u, 0u, 0u, 0u};
+  if (16 * tid < sbytes) sv = ldg128((const uint8_t*)S + (size_t)blockIdx.x * sbytes + 16 * tid);
+  if constexpr (ZDT >= 0)
+    if (16 * tid < zbytes) zv = ldg128((const uint8_t*)Z + (size_t)blockIdx.x * zbytes + 16 * tid);
 
   const uint8_t* wrow = W + (size_t)n * (K >> 1) + (kbeg >> 1) + 16 * q;
   u4_t wv[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) wv[i] = ldg128(wrow + 64 * i);
-  const size_t g0 = (size_t)n * nch + (kbeg >> 7);
-  uint32_t sw[PF / 2], zw[PF / 2];
-  if constexpr (PF == 4) {
-    const u2_t v = ldg64(S + g0);
-    sw[0] = v.x; sw[1] = v.y;
-  } else {
-    const u4_t v = ldg128(S + g0);
-    sw[0] = v.x; sw[1] = v.y; sw[2] = v.z; sw[3] = v.w;
-  }
-  uint32_t zb8[(PF + 3) / 4];
-  if constexpr (ZDT == 3) {
-    if constexpr (PF == 4) zb8[0] = *(const uint32_t*)((const uint8_t*)Z + g0);
-    else { const u2_t v = ldg64((const uint8_t*)Z + g0); zb8[0] = v.x; zb8[1] = v.y; }
-  } else if constexpr (ZDT >= 0) {
-    if constexpr (PF == 4) {
-      const u2_t v = ldg64((const uint16_t*)Z + g0);
-      zw[0] = v.x; zw[1] = v.y;
-    } else {
-      const u4_t v = ldg128((const uint16_t*)Z + g0);
-      zw[0] = v.x; zw[1] = v.y; zw[2] = v.z; zw[3] = v.w;
-    }
-  }
 
   auto stage = [&](int r, const u4_t* v) {
 #pragma unroll
@@ -411,6 +402,9 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
     }
   };
   stage(0, xv);
+  if (16 * tid < sbytes) *(u4_t*)((uint8_t*)sst + 16 * tid) = sv;
+  if constexpr (ZDT >= 0)
+    if (16 * tid < zbytes) *(u4_t*)((uint8_t*)zst + 16 * tid) = zv;
   for (int r = 1; r < M; ++r) {
 #pragma unroll
     for (int u = 0; u < XP; ++u) xv[u] = ldg128(X + (size_t)r * K + (size_t)(tid + NT * u) * 8);
@@ -419,30 +413,30 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
   __syncthreads();
 
   const uint16_t* xa = xs + m * ldx + kbeg + 32 * q;
-  f4_t a[PF];
-#pragma unroll
-  for (int i = 0; i < PF; ++i) a[i] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < PF; ++i) {
-      const u4_t w = wv[i];
-      const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
-      a[i] = mfma16<BF16>(*(const u4_t*)(xa + 128 * i + 8 * j), w4_operand(wj, vmask, vmagic),
-                          a[i]);
-    }
-  f4_t y = {0.f, 0.f, 0.f, 0.f};
   const float* xsr = xsum + (kbeg >> 7) * 8 + 4 * (q & 1);
+  // Chunk by chunk: 4 MFMAs into one of two alternating accumulators, then the
+  // chunk's scale / zero-point correction folded into y (keeps the register
+  // count within 8 waves per SIMD).
+  f4_t y = {0.f, 0.f, 0.f, 0.f};
+  f4_t a2[2];
 #pragma unroll
   for (int i = 0; i < PF; ++i) {
-    const uint16_t sr = (uint16_t)(sw[i >> 1] >> (16 * (i & 1)));
-    const float sc = raw_to_f32<SDT>(sr);
+    f4_t& a = a2[i & 1];
+    a = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u4_t w = wv[i];
+      const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+      a = mfma16<BF16>(*(const u4_t*)(xa + 128 * i + 8 * j), w4_operand(wj, vmask, vmagic), a);
+    }
+    const int gi = (lane & 15) * nch + (kbeg >> 7) + i;
+    const float sc = raw_to_f32<SDT>(sst[gi]);
     float zb = w4_offset<BF16>();
-    if constexpr (ZDT == 3) zb += (float)((zb8[i >> 2] >> (8 * (i & 3))) & 0xFFu);
-    else if constexpr (ZDT >= 0) zb += raw_to_f32<ZDT>((uint16_t)(zw[i >> 1] >> (16 * (i & 1))));
+    if constexpr (ZDT == 3) zb += (float)((const uint8_t*)zst)[gi];
+    else if constexpr (ZDT >= 0) zb += raw_to_f32<ZDT>(zst[gi]);
     const f4_t xv4 = *(const f4_t*)(xsr + 8 * i);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] += sc * (a[i][e] - zb * xv4[e]);
+    for (int e = 0; e < 4; ++e) y[e] += sc * (a[e] - zb * xv4[e]);
   }
 
   if (wave > 0) red[wave - 1][lane] = y;
@@ -724,8 +718,13 @@ TM_WQ_Z(tiled, 8, false, f16, , )
 TM_WQ_Z(tiled, 8, true, bf16, , )
 
 // GEMV (int4, exact K = NW * PF * 128, G = 128): wq_gemv4_<act>_z<zs>_w<NW>p<PF>
+// Occupancy of the K = 4096 variant: 8 waves per SIMD (<= 64 VGPRs), so that
+// a whole N = 14336 grid (896 workgroups of 8 waves) is resident at once
+// instead of leaving a second, partial round of workgroups.
 #define TM_GEMV4(BF, ACT, ZS, ZDT, NW, PF)                                                     \
-  extern "C" __global__ __launch_bounds__(NW * 64) void wq_gemv4_##ACT##_z##ZS##_w##NW##p##PF(  \
+  extern "C" __global__ __launch_bounds__(NW * 64)                                              \
+  __attribute__((amdgpu_waves_per_eu(NW == 8 && PF == 4 ? 8 : 1)))                             \
+  void wq_gemv4_##ACT##_z##ZS##_w##NW##p##PF(                                                   \
       const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S, const void* Z, int M, \
       int N, int K) {                                                                           \
     wq_gemv4_body<BF, ZDT, NW, PF>(X, W, Y, S, Z, M, N, K);                                     \
