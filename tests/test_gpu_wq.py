@@ -96,14 +96,14 @@ def test_int4_dequant_tile_bit_exact(dev, act):
     assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("kind", ["skinny", "gemv", "gemv8k", "tiled"])
+@pytest.mark.parametrize("kind", ["skinny", "gemv", "gemv8k", "wide", "tiled"])
 @pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
 def test_int4_in_register_dequant_bit_exact(dev, kind, act):
     """One-hot activation rows make each output equal one dequantised weight,
     so the GEMM's in-register dequantisation is compared bit for bit."""
     N, G = 64, 128
-    K = {"skinny": 512, "gemv": 4096, "gemv8k": 8192, "tiled": 512}[kind]
-    M = 64 if kind == "tiled" else 8
+    K = {"skinny": 512, "gemv": 4096, "gemv8k": 8192, "wide": 2048, "tiled": 512}[kind]
+    M = {"tiled": 64, "wide": 32}.get(kind, 8)
     _, q, packed, s, z = make_int4_problem(M, N, K, G, seed=12, act=act)
     ks = torch.randperm(K, generator=_gen(3))[:M]
     x = torch.zeros(M, K, dtype=act)
@@ -114,10 +114,11 @@ def test_int4_in_register_dequant_bit_exact(dev, kind, act):
     assert torch.equal(out.cpu().view(torch.int16), ref[:, ks].T.contiguous().view(torch.int16))
 
 
-@pytest.mark.parametrize("kind", ["skinny", "tiled"])
+@pytest.mark.parametrize("kind", ["skinny", "wide", "tiled"])
 def test_int8_in_register_dequant_bit_exact(dev, kind):
-    N, K = 64, 512
-    M = 8 if kind == "skinny" else 64
+    N = 64
+    K = 2048 if kind == "wide" else 512
+    M = {"skinny": 8, "wide": 16, "tiled": 64}[kind]
     _, w, s, _ = make_int8_problem(M, N, K, seed=13)
     ks = torch.randperm(K, generator=_gen(4))[:M]
     x = torch.zeros(M, K, dtype=torch.float16)
@@ -216,6 +217,34 @@ def test_int8_shapes(dev, M, N, K, zeros):
                    M, N, K)
     ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
     check_close(out.cpu(), ref)
+
+
+# --- wide kernel (8 < M <= 64, K = 1024..4096 in steps of 512) ------------------
+@pytest.mark.parametrize("M,K", [(9, 1024), (16, 4096), (17, 2048), (32, 1536), (33, 4096),
+                                 (64, 1024)])
+@pytest.mark.parametrize("zeros", ["f16", "u8", None])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int4_wide_shapes(dev, M, K, zeros, act):
+    N, G = 128, 128
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 13 + K, act=act, zeros=zeros)
+    out = torch.empty(M, N, dtype=act, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
+                   None if z is None else z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 32, 1024), (16, 96, 4096), (31, 64, 2048),
+                                   (64, 32, 1536)])
+@pytest.mark.parametrize("zeros", [False, True])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int8_wide_shapes(dev, M, N, K, zeros, act):
+    x, w, s, z = make_int8_problem(M, N, K, seed=M + N + K, act=act, zeros=zeros or None)
+    out = torch.empty(M, N, dtype=act, device=dev)
+    tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None if z is None else z.to(dev),
+                   M, N, K)
+    ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
+    check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
 
 
 def test_empty_and_errors(dev):

@@ -75,6 +75,20 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
                     Z, M, N, K);
     }
   }
+  // wide kernel: 8 < M <= 64, weights of the whole matrix in flight at once
+  const int wnt = qbits == 4 ? 4 : 2;  // MFMA n-tiles per workgroup
+  const bool aligned8 = ((uintptr_t)S & 7u) == 0 && (!Z || ((uintptr_t)Z & 7u) == 0);
+  if (fast && M > 8 && M <= 64 && N % (16 * wnt) == 0 && K % 512 == 0 && K >= 1024 &&
+      K <= 4096 && (qbits == 8 || (G == 128 && aligned8))) {
+    const int mt = M <= 16 ? 1 : 2, nwv = K / 512;
+    const size_t wlds = (size_t)nwv * 64 * 4 * mt * wnt * sizeof(float);
+    if (wlds <= (size_t)max_dynamic_lds()) {
+      char name[64];
+      snprintf(name, sizeof name, "wq_wide_q%d_%s_z%c_m%d", qbits, act, zc, mt);
+      return launch(kernel(name), dim3(N / (16 * wnt)), dim3(64 * nwv), (unsigned)wlds, stream,
+                    X, W, Y, S, Z, M, N, K);
+    }
+  }
   size_t lds = (size_t)M * (K + 8) * 2 + (size_t)M * (K / 128) * 4;
   if (fast && M <= 8 && K % (4 * CK) == 0 && lds <= (size_t)max_dynamic_lds()) {
     char name[64];

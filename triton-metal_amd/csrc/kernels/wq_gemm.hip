@@ -453,6 +453,222 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
 }
 
 // ----------------------------------------------------------------------------
+// Wide kernel: 8 < M <= 64.  A workgroup owns 16 NT output columns (NT MFMA
+// n-tiles: 4 for int4, 2 for int8) and all M rows; its K / 512 waves (at most
+// 8) split K into slices of 512.  Each wave loads all weights of its slice up
+// front - 16 x 16 bytes per lane, so the whole matrix is in flight at once -
+// and then walks the slice in 32-k MFMA steps, MT m-tiles (16 MT rows) at a
+// time, with the X operands read straight from global memory (X is read by
+// every workgroup and stays in L2) one chunk ahead.  The K-slices are reduced
+// through LDS.  int4 (group 128): per 128-k chunk
+//   Y += s * (sum x (OFF + q) - (OFF + z) * sum x),
+// int8: Y = s * (sum x q - z * sum x); sum x comes from v_dot2 on the X
+// operands.  Dynamic LDS: (K / 512) * 64 * 4 MT NT floats.
+// ----------------------------------------------------------------------------
+namespace {
+// (The dwords go through by-value helpers: __builtin_bit_cast applied directly
+// to a vector element such as v.y reads element 0 in this compiler.)
+TM_DEV bf2_t as_bf2(uint32_t u) { return __builtin_bit_cast(bf2_t, u); }
+TM_DEV float xsum8(u4_t v, bool bf16) {
+  float a = 0.0f;
+  if (bf16) {
+    const bf2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(v.x), one, a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(v.y), one, a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(v.z), one, a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(v.w), one, a, false);
+  } else {
+    const h2_t one = {(half_t)1.0f, (half_t)1.0f};
+    a = __builtin_amdgcn_fdot2(as_h2(v.x), one, a, false);
+    a = __builtin_amdgcn_fdot2(as_h2(v.y), one, a, false);
+    a = __builtin_amdgcn_fdot2(as_h2(v.z), one, a, false);
+    a = __builtin_amdgcn_fdot2(as_h2(v.w), one, a, false);
+  }
+  return a;
+}
+// 16-bit element e of a packed pair of dwords
+TM_DEV uint16_t half_of(u2_t v, int e) {
+  return (uint16_t)(((e >> 1) ? v.y : v.x) >> (16 * (e & 1)));
+}
+}  // namespace
+
+template <int QB, bool BF16, int SDT, int ZDT, int MT>
+__device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
+                                             const uint8_t* __restrict__ W,
+                                             uint16_t* __restrict__ Y,
+                                             const void* __restrict__ S,
+                                             const void* __restrict__ Z, int M, int N, int K) {
+  constexpr int KS = 512;                  // k per wave
+  constexpr int NT = QB == 4 ? 4 : 2;      // n-tiles per workgroup
+  constexpr int NJ = QB == 4 ? 4 : 2;      // 32-k MFMA steps per chunk (one 16-byte load)
+  constexpr int CKK = 32 * NJ;             // k per chunk
+  constexpr int NCH = KS / CKK;            // chunks per slice (4 or 8)
+  constexpr int NF = 4 * MT * NT;          // partial sums per lane per pass of 16 MT rows
+  extern __shared__ __align__(16) float red[];  // [waves][NF][64]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nwv = blockDim.x >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int kb = wave * KS;
+  const int n0 = blockIdx.x * 16 * NT;
+  const size_t rowbytes = QB == 4 ? (size_t)(K >> 1) : (size_t)K;
+
+  // 1. the slice's weights: n-tile t, chunk i = 16 bytes of row n0 + 16t + l16
+  u4_t wv[NT][NCH];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const uint8_t* wr =
+        W + (size_t)(n0 + 16 * t + l16) * rowbytes + (QB == 4 ? (kb >> 1) : kb) + 16 * q;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) wv[t][i] = ldg128(wr + 64 * i);
+  }
+  // 2. scales / zero-points of the lane's D-layout columns n0 + 16t + l16:
+  //    int4 (group 128): the 4 groups of the slice; int8: per channel
+  u2_t sv[NT], zv[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = n0 + 16 * t + l16;
+    if constexpr (QB == 4) {
+      const size_t g0 = (size_t)n * (K >> 7) + (kb >> 7);
+      sv[t] = ldg64((const uint16_t*)S + g0);
+      if constexpr (ZDT == 3) zv[t] = u2_t{*(const uint32_t*)((const uint8_t*)Z + g0), 0u};
+      else if constexpr (ZDT >= 0) zv[t] = ldg64((const uint16_t*)Z + g0);
+    } else {
+      sv[t] = u2_t{(uint32_t)ld_raw<SDT>(S, (size_t)n), 0u};
+      if constexpr (ZDT >= 0) zv[t] = u2_t{(uint32_t)ld_raw<ZDT>(Z, (size_t)n), 0u};
+    }
+  }
+
+  auto load_x = [&](int mp, int i, u4_t (&xo)[MT][NJ]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = min(16 * MT * mp + 16 * mt + l16, M - 1);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        xo[mt][j] = ldg128(X + (size_t)r * K + kb + CKK * i + 8 * NJ * q + 8 * j);
+    }
+  };
+
+  for (int mp = 0; 16 * MT * mp < M; ++mp) {
+    // made inside the pass loop (volatile asm) so that the weight conversions
+    // below cannot be hoisted out of it - all of them at once would not fit in
+    // registers
+    const uint32_t vmask = vgpr_const(0x000F000Fu), vmagic = vgpr_const(w4_magic<BF16>());
+    f4_t y[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) y[mt][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+    float xtot[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xtot[mt] = 0.f;  // int8: sum x over the slice, row 16mt + l16
+    u4_t xa[MT][NJ], xb[MT][NJ];
+    load_x(mp, 0, xa);
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      // keep each chunk's operand conversions inside its own iteration (the
+      // scheduler would otherwise hoist all of them and run out of registers)
+      __builtin_amdgcn_sched_barrier(0);
+      u4_t (&xo)[MT][NJ] = (i & 1) ? xb : xa;
+      u4_t (&xn)[MT][NJ] = (i & 1) ? xa : xb;
+      if (i + 1 < NCH) load_x(mp, i + 1, xn);
+      f4_t acc[MT][NT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[mt][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        u4_t xop[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) xop[mt] = QB == 4 ? perm_x8(xo[mt][j]) : xo[mt][j];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const u4_t w = wv[t][i];
+          u4_t wop;
+          if constexpr (QB == 4) {
+            const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+            wop = w4_operand(wj, vmask, vmagic);
+          } else {
+            wop = j == 0 ? w8_operand<BF16>(w.x, w.y) : w8_operand<BF16>(w.z, w.w);
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt][t] = mfma16<BF16>(xop[mt], wop, acc[mt][t]);
+        }
+      }
+      // sum x of the chunk for row 16mt + l16 (all four lane quarters)
+      float xs[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float v = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) v += xsum8(xo[mt][j], BF16);
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        xs[mt] = v;
+      }
+      if constexpr (QB == 4) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          float xr[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xr[e] = __shfl(xs[mt], 4 * q + e, 64);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const float sc = raw_to_f32<SDT>(half_of(sv[t], i));
+            float zb = w4_offset<BF16>();
+            if constexpr (ZDT == 3) zb += (float)((zv[t].x >> (8 * i)) & 0xFFu);
+            else if constexpr (ZDT >= 0) zb += raw_to_f32<ZDT>(half_of(zv[t], i));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[mt][t][e] += sc * (acc[mt][t][e] - zb * xr[e]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          xtot[mt] += xs[mt];
+#pragma unroll
+          for (int t = 0; t < NT; ++t) y[mt][t] += acc[mt][t];
+        }
+      }
+    }
+    if constexpr (QB == 8) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float xr[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xr[e] = __shfl(xtot[mt], 4 * q + e, 64);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const float sc = raw_to_f32<SDT>((typename Raw<SDT>::T)sv[t].x);
+          float z = 0.0f;
+          if constexpr (ZDT >= 0) z = raw_to_f32<ZDT>((typename Raw<ZDT>::T)zv[t].x);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[mt][t][e] = sc * (y[mt][t][e] - z * xr[e]);
+        }
+      }
+    }
+
+    // reduce the K-slices: red[wave][f][lane], f = 4 (NT mt + t) + e
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          red[(wave * NF + 4 * (NT * mt + t) + e) * 64 + lane] = y[mt][t][e];
+    __syncthreads();
+    for (int f = wave; f < NF; f += nwv) {
+      float v = 0.0f;
+      for (int w2 = 0; w2 < nwv; ++w2) v += red[(w2 * NF + f) * 64 + lane];
+      const int mt = (f >> 2) / NT, t = (f >> 2) % NT, e = f & 3;
+      const int row = 16 * MT * mp + 16 * mt + 4 * q + e;
+      if (row < M) store_out(Y, (size_t)row * N + n0 + 16 * t + l16, v, BF16);
+    }
+    __syncthreads();
+  }
+}
+
+// ----------------------------------------------------------------------------
 // Tiled kernel: any M.  Output tile 64 (m) x 64 (n); block = 256 (4 waves),
 // wave w owns columns n0 + 16w .. +15 for all 64 rows (4 m-tiles).
 // K steps of KS = 256 with X tiles (and their 128-k chunk sums)
@@ -716,6 +932,26 @@ TM_WQ_Z(tiled, 4, false, f16, , )
 TM_WQ_Z(tiled, 4, true, bf16, , )
 TM_WQ_Z(tiled, 8, false, f16, , )
 TM_WQ_Z(tiled, 8, true, bf16, , )
+
+// Wide (8 < M <= 64): wq_wide_q<QB>_<act>_z<zs>_m<MT>; block = 64 * K / 512 (<= 512)
+#define TM_WIDE(QB, BF, ACT, ZS, ZDT, MT)                                                      \
+  extern "C" __global__ __launch_bounds__(512) void wq_wide_q##QB##_##ACT##_z##ZS##_m##MT(     \
+      const uint16_t* X, const uint8_t* W, uint16_t* Y, const void* S, const void* Z, int M,   \
+      int N, int K) {                                                                          \
+    wq_wide_body<QB, BF, (BF ? TM_DT_BF16 : TM_DT_F16), ZDT, MT>(X, W, Y, S, Z, M, N, K);      \
+  }
+#define TM_WIDE_Z(QB, BF, ACT, MT)                          \
+  TM_WIDE(QB, BF, ACT, n, -1, MT)                           \
+  TM_WIDE(QB, BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), MT) \
+  TM_WIDE(QB, BF, ACT, u, 3, MT)
+TM_WIDE_Z(4, false, f16, 1)
+TM_WIDE_Z(4, true, bf16, 1)
+TM_WIDE_Z(8, false, f16, 1)
+TM_WIDE_Z(8, true, bf16, 1)
+TM_WIDE_Z(4, false, f16, 2)
+TM_WIDE_Z(4, true, bf16, 2)
+TM_WIDE_Z(8, false, f16, 2)
+TM_WIDE_Z(8, true, bf16, 2)
 
 // GEMV (int4, exact K = NW * PF * 128, G = 128): wq_gemv4_<act>_z<zs>_w<NW>p<PF>
 // Occupancy of the K = 4096 variant: 8 waves per SIMD (<= 64 VGPRs), so that
