@@ -96,14 +96,23 @@ def test_int4_dequant_tile_bit_exact(dev, act):
     assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("kind", ["skinny", "gemv", "gemv8k", "wide", "tiled"])
+# (M, K) of each kernel kind: the stream kernel takes 1 < M <= 64 with
+# K <= 4096; the GEMV M = 1 and K = 8192; skinny the remaining M <= 8 shapes
+# with K % 512 == 0; tiled M > 64.
+INT4_KINDS = {"skinny": (8, 5120), "gemv": (1, 4096), "gemv8k": (8, 8192),
+              "stream8": (8, 4096), "stream16": (16, 2048), "stream_multi": (40, 2048),
+              "tiled": (72, 512)}
+INT8_KINDS = {"skinny": (8, 768), "stream8": (8, 2048), "stream16": (16, 2048),
+              "stream_multi": (40, 1024), "tiled": (72, 512)}
+
+
+@pytest.mark.parametrize("kind", list(INT4_KINDS))
 @pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
 def test_int4_in_register_dequant_bit_exact(dev, kind, act):
     """One-hot activation rows make each output equal one dequantised weight,
     so the GEMM's in-register dequantisation is compared bit for bit."""
     N, G = 64, 128
-    K = {"skinny": 512, "gemv": 4096, "gemv8k": 8192, "wide": 2048, "tiled": 512}[kind]
-    M = {"tiled": 64, "wide": 32}.get(kind, 8)
+    M, K = INT4_KINDS[kind]
     _, q, packed, s, z = make_int4_problem(M, N, K, G, seed=12, act=act)
     ks = torch.randperm(K, generator=_gen(3))[:M]
     x = torch.zeros(M, K, dtype=act)
@@ -114,11 +123,10 @@ def test_int4_in_register_dequant_bit_exact(dev, kind, act):
     assert torch.equal(out.cpu().view(torch.int16), ref[:, ks].T.contiguous().view(torch.int16))
 
 
-@pytest.mark.parametrize("kind", ["skinny", "wide", "tiled"])
+@pytest.mark.parametrize("kind", list(INT8_KINDS))
 def test_int8_in_register_dequant_bit_exact(dev, kind):
     N = 64
-    K = 2048 if kind == "wide" else 512
-    M = {"skinny": 8, "wide": 16, "tiled": 64}[kind]
+    M, K = INT8_KINDS[kind]
     _, w, s, _ = make_int8_problem(M, N, K, seed=13)
     ks = torch.randperm(K, generator=_gen(4))[:M]
     x = torch.zeros(M, K, dtype=torch.float16)
@@ -219,14 +227,17 @@ def test_int8_shapes(dev, M, N, K, zeros):
     check_close(out.cpu(), ref)
 
 
-# --- wide kernel (8 < M <= 64, K = 1024..4096 in steps of 512) ------------------
-@pytest.mark.parametrize("M,K", [(9, 1024), (16, 4096), (17, 2048), (32, 1536), (33, 4096),
-                                 (64, 1024)])
+# --- stream kernel (1 < M <= 64, K = 512..4096 in steps of 512) ------------------
+# N not a multiple of the workgroup's columns (int4: 64, int8: 48) leaves a
+# partial last workgroup.
+@pytest.mark.parametrize("M,N,K", [(2, 64, 512), (8, 80, 4096), (9, 128, 1024), (16, 128, 4096),
+                                   (17, 80, 2048), (32, 128, 1536), (33, 64, 4096),
+                                   (64, 128, 1024)])
 @pytest.mark.parametrize("zeros", ["f16", "u8", None])
 @pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
-def test_int4_wide_shapes(dev, M, K, zeros, act):
-    N, G = 128, 128
-    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 13 + K, act=act, zeros=zeros)
+def test_int4_stream_shapes(dev, M, N, K, zeros, act):
+    G = 128
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 13 + K + N, act=act, zeros=zeros)
     out = torch.empty(M, N, dtype=act, device=dev)
     tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
                    None if z is None else z.to(dev), M, N, K, G)
@@ -234,17 +245,28 @@ def test_int4_wide_shapes(dev, M, K, zeros, act):
     check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
 
 
-@pytest.mark.parametrize("M,N,K", [(9, 32, 1024), (16, 96, 4096), (31, 64, 2048),
-                                   (64, 32, 1536)])
+@pytest.mark.parametrize("M,N,K", [(2, 48, 512), (8, 208, 4096), (9, 32, 1024), (16, 96, 4096),
+                                   (31, 64, 2048), (64, 32, 1536)])
 @pytest.mark.parametrize("zeros", [False, True])
 @pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
-def test_int8_wide_shapes(dev, M, N, K, zeros, act):
+def test_int8_stream_shapes(dev, M, N, K, zeros, act):
     x, w, s, z = make_int8_problem(M, N, K, seed=M + N + K, act=act, zeros=zeros or None)
     out = torch.empty(M, N, dtype=act, device=dev)
     tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None if z is None else z.to(dev),
                    M, N, K)
     ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
     check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
+
+
+def test_int8_stream_u8_zero_points(dev):
+    """int8 with uint8 zero-points through the stream kernel (one per channel)."""
+    M, N, K = 12, 80, 1024
+    x, w, s, _ = make_int8_problem(M, N, K, seed=5)
+    z = torch.randint(0, 5, (N,), generator=_gen(6), dtype=torch.uint8)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), z.to(dev), M, N, K)
+    ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
+    check_close(out.cpu(), ref)
 
 
 def test_empty_and_errors(dev):

@@ -63,6 +63,25 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
               aligned16(W);
   const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
   const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
+  // streaming kernel: 1 < M <= 64, K-slices of 512 per wave (at most 8)
+  const bool aligned4 = ((uintptr_t)S & 3u) == 0 && (!Z || ((uintptr_t)Z & 3u) == 0);
+  if (fast && M > 1 && M <= 64 && K % 512 == 0 && K <= 4096 && aligned4 &&
+      (qbits == 8 || G == 128)) {
+    const int nwv = K / 512;
+    const int nt = qbits == 4 ? 4 : 3;           // 16-column tiles per workgroup
+    const int xr = M <= 8 ? 8 : 16;              // X rows staged per chunk
+    const int rs = qbits == 4 ? 2 : 3;           // ring slots per wave
+    const int slot = nt * 1024 + xr * (qbits == 4 ? 256 : 128);
+    const size_t slds = (size_t)nwv * (rs * slot + 1024) + (size_t)nwv * 8 * 64 * sizeof(float);
+    if (slds <= (size_t)max_dynamic_lds()) {
+      char name[64];
+      snprintf(name, sizeof name, "wq_stream_q%d_%s_z%c_x%d%c", qbits, act, zc, xr,
+               M <= 16 ? 's' : 'm');
+      const int tiles = N / 16;
+      return launch(kernel(name), dim3((tiles + nt - 1) / nt), dim3(64 * nwv), (unsigned)slds,
+                    stream, X, W, Y, S, Z, M, N, K);
+    }
+  }
   // exact-shape int4 GEMV: K = NW * PF * 128, G = 128
   if (fast && qbits == 4 && M <= 8 && G == 128 && (K == 4096 || K == 8192) && aligned16(S) &&
       (!Z || aligned16(Z))) {
@@ -73,20 +92,6 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
       snprintf(name, sizeof name, "wq_gemv4_%s_z%c_w8p%d", act, zc, pf);
       return launch(kernel(name), dim3(N / 16), dim3(512), (unsigned)glds, stream, X, W, Y, S,
                     Z, M, N, K);
-    }
-  }
-  // wide kernel: 8 < M <= 64, weights of the whole matrix in flight at once
-  const int wnt = qbits == 4 ? 4 : 2;  // MFMA n-tiles per workgroup
-  const bool aligned8 = ((uintptr_t)S & 7u) == 0 && (!Z || ((uintptr_t)Z & 7u) == 0);
-  if (fast && M > 8 && M <= 64 && N % (16 * wnt) == 0 && K % 512 == 0 && K >= 1024 &&
-      K <= 4096 && (qbits == 8 || (G == 128 && aligned8))) {
-    const int mt = M <= 16 ? 1 : 2, nwv = K / 512;
-    const size_t wlds = (size_t)nwv * 64 * 4 * mt * wnt * sizeof(float);
-    if (wlds <= (size_t)max_dynamic_lds()) {
-      char name[64];
-      snprintf(name, sizeof name, "wq_wide_q%d_%s_z%c_m%d", qbits, act, zc, mt);
-      return launch(kernel(name), dim3(N / (16 * wnt)), dim3(64 * nwv), (unsigned)wlds, stream,
-                    X, W, Y, S, Z, M, N, K);
     }
   }
   size_t lds = (size_t)M * (K + 8) * 2 + (size_t)M * (K / 128) * 4;

@@ -13,6 +13,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 
 typedef _Float16 half_t;
 typedef __bf16 bf16_t;
@@ -132,6 +133,39 @@ TM_DEV void g2lds16(const void* g, void* lds_base) {
 // moving memory accesses across it; reads of LDS filled by global -> LDS
 // copies still get their vmcnt wait from the compiler.
 TM_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Byte offset of an LDS location (the address a global -> LDS copy takes).
+TM_DEV uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)(lds_void_t*)p; }
+
+// Global -> LDS copies issued in asm: lane l deposits its 16 (4) bytes at LDS
+// byte offset lds + 16 l (4 l); lds must be wave-uniform.  The compiler does
+// not see these copies, so it adds no waits for them (given the builtin, it
+// waits for every outstanding copy before any LDS read).  The caller waits with
+// wait_vm<N>() - N = copies (and other vector memory operations) issued after
+// the awaited one - before reading the data, and must not overwrite LDS that
+// a copy still targets.  m0 is written here; the kernels that use these
+// helpers use m0 for nothing else.
+TM_DEV void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+}
+TM_DEV void dma4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory");
+}
+// Wait until at most N vector memory operations of this wave are outstanding
+// (they complete in issue order).
+template <int N> TM_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// f(std::integral_constant<int, I>) for I = B .. E-1, unrolled with I usable
+// in constant expressions.
+template <int B, int E, typename F> TM_DEV void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 TM_DEV u2_t ldg64(const void* p) { return *(const u2_t*)p; }
 
 // A 32-bit constant the compiler must keep in a VGPR (it cannot see its value).

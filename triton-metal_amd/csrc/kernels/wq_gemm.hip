@@ -25,9 +25,13 @@
 // is staged into LDS.
 //
 // Kernels
-//   wq_skinny_*  M <= 8: the whole X[M, K] is staged once per workgroup in LDS;
-//                one workgroup owns 16 output columns, its 4 waves split K and
-//                are reduced through LDS.  Weights stream with 128-bit loads.
+//   wq_gemv4_*   int4, M = 1 (and M <= 8 when K = 8192): GEMV, the whole grid
+//                resident, per-chunk MFMAs as the weights land.
+//   wq_stream_*  1 < M <= 64, K <= 4096: weights and X streamed through LDS
+//                rings by global -> LDS copies, K split over the waves.
+//   wq_skinny_*  other M <= 8 shapes: the whole X[M, K] is staged once per
+//                workgroup in LDS; one workgroup owns 16 output columns, its 4
+//                waves split K and are reduced through LDS.
 //   wq_tiled_*   larger M: 64 x 64 output tiles, X tiles double-buffered in LDS,
 //                each wave unpacks its own 16 weight rows in registers.
 //   wq_general   any shape / dtype: fp32 arithmetic exactly as the reference
@@ -79,6 +83,17 @@ template <int DT> TM_DEV float raw_to_f32(typename Raw<DT>::T v) {
 // element order [n0, n4, n1, n5, n2, n6, n3, n7].
 // `mask` = 0x000F000F and `magic` = the OFF exponent pattern, both held in
 // VGPRs (vgpr_const) so each half-pair costs one v_and_or_b32.
+// Same with the shift amounts held in registers (vgpr_const inside a loop
+// keeps the whole conversion inside that loop).
+TM_DEV u4_t w4_operand_v(uint32_t w, uint32_t mask, uint32_t magic, uint32_t s4, uint32_t s8,
+                         uint32_t s12) {
+  u4_t r;
+  r.x = (w & mask) | magic;
+  r.y = ((w >> s4) & mask) | magic;
+  r.z = ((w >> s8) & mask) | magic;
+  r.w = ((w >> s12) & mask) | magic;
+  return r;
+}
 TM_DEV u4_t w4_operand(uint32_t w, uint32_t mask, uint32_t magic) {
   u4_t r;
   r.x = (w & mask) | magic;
@@ -453,17 +468,28 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
 }
 
 // ----------------------------------------------------------------------------
-// Wide kernel: 8 < M <= 64.  A workgroup owns 16 NT output columns (NT MFMA
-// n-tiles: 4 for int4, 2 for int8) and all M rows; its K / 512 waves (at most
-// 8) split K into slices of 512.  Each wave loads all weights of its slice up
-// front - 16 x 16 bytes per lane, so the whole matrix is in flight at once -
-// and then walks the slice in 32-k MFMA steps, MT m-tiles (16 MT rows) at a
-// time, with the X operands read straight from global memory (X is read by
-// every workgroup and stays in L2) one chunk ahead.  The K-slices are reduced
-// through LDS.  int4 (group 128): per 128-k chunk
-//   Y += s * (sum x (OFF + q) - (OFF + z) * sum x),
-// int8: Y = s * (sum x q - z * sum x); sum x comes from v_dot2 on the X
-// operands.  Dynamic LDS: (K / 512) * 64 * 4 MT NT floats.
+// Streaming kernel: 1 < M <= 64.  A workgroup owns NT 16-column tiles (int4:
+// 4, int8: 3) and all M rows; its K / 512 waves (at most 8) split K into
+// slices of 512 and are reduced through LDS after each pass of 16 rows.
+// Weights and X reach LDS by global -> LDS copies issued in an order where
+// every 4 consecutive lanes read one 64-byte segment: the vector memory path
+// serves such groups at about three times the rate of the MFMA operand order,
+// in which 4 consecutive lanes touch 4 different rows.  The operands are read
+// back in MFMA order through XOR swizzles that keep those reads free of bank
+// conflicts.  Each wave streams its chunks (64 weight bytes per row: 128 k for
+// int4, 64 k for int8) through a ring of RS slots of its own LDS:
+//   slot  [NT][16 rows][64 B] weights, then [XR rows][XB] X
+//         weight piece p (16 B) of row r at 64 r + 16 (p ^ ((r >> 2) & 3))
+//         X piece p of row r at r XB + 16 (p ^ xsw(r))
+// and waits for each with an explicit vmcnt (copies complete in issue order).
+// The single-pass kernel (M <= XR) takes each chunk's weights from LDS; the
+// multi-pass one keeps the first pass's weight registers for the later passes,
+// which stream X only.  Scales and zero-points are copied to LDS ahead of the
+// first chunks.
+// int4 (group 128 = one chunk):  Y += s * (sum x (OFF + q) - (OFF + z) sum x)
+// int8:                          Y  = s * (sum x q - z sum x)
+// sum x per chunk comes from v_dot2 on the X operands.
+// Dynamic LDS: nwv * (RS * SLOT + 1024) + nwv * 2 KB.
 // ----------------------------------------------------------------------------
 namespace {
 // (The dwords go through by-value helpers: __builtin_bit_cast applied directly
@@ -486,186 +512,240 @@ TM_DEV float xsum8(u4_t v, bool bf16) {
   }
   return a;
 }
-// 16-bit element e of a packed pair of dwords
-TM_DEV uint16_t half_of(u2_t v, int e) {
-  return (uint16_t)(((e >> 1) ? v.y : v.x) >> (16 * (e & 1)));
+// Copies issued after chunk i's (copies per item: c0 in the first pass, c1
+// later; rs - 1 items run ahead, the ones past the pass end only if another
+// pass follows).
+constexpr int stream_ahead(int rs, int nch, int c0, int c1, bool first, int i, bool next) {
+  int a = 0;
+  for (int d = 1; d < rs; ++d) {
+    if (i + d < nch) a += first ? c0 : c1;
+    else if (next) a += c1;
+  }
+  return a;
 }
 }  // namespace
 
-template <int QB, bool BF16, int SDT, int ZDT, int MT>
-__device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
-                                             const uint8_t* __restrict__ W,
-                                             uint16_t* __restrict__ Y,
-                                             const void* __restrict__ S,
-                                             const void* __restrict__ Z, int M, int N, int K) {
-  constexpr int KS = 512;                  // k per wave
-  constexpr int NT = QB == 4 ? 4 : 2;      // n-tiles per workgroup
-  constexpr int NJ = QB == 4 ? 4 : 2;      // 32-k MFMA steps per chunk (one 16-byte load)
-  constexpr int CKK = 32 * NJ;             // k per chunk
-  constexpr int NCH = KS / CKK;            // chunks per slice (4 or 8)
-  constexpr int NF = 4 * MT * NT;          // partial sums per lane per pass of 16 MT rows
-  extern __shared__ __align__(16) float red[];  // [waves][NF][64]
+template <int QB, bool BF16, int SDT, int ZDT, int NT, int XR, bool MULTI>
+__device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t* W,
+                                               uint16_t* __restrict__ Y, const void* S,
+                                               const void* Z, int M, int N, int K) {
+  constexpr int KS = 512;                 // k per wave
+  constexpr int CK = QB == 4 ? 128 : 64;  // k per chunk: 64 weight bytes of a row
+  constexpr int NCH = KS / CK;            // chunks per wave
+  constexpr int NJ = CK / 32;             // MFMA k-steps per chunk
+  constexpr int XB = 2 * CK;              // X bytes per row per chunk
+  constexpr int XPR = XB / 16;            // 16-byte pieces per X row per chunk
+  constexpr int XI = XR * XPR / 64;       // X copies (1 KB each) per chunk
+  constexpr int RS = QB == 4 ? 2 : 3;     // ring slots per wave
+  constexpr int SLOT = NT * 1024 + XR * XB;
+  constexpr int WB = RS * SLOT + 1024;    // per-wave LDS: ring, scales / zero-points
+  constexpr int C0 = NT + XI, C1 = XI;    // copies per first-pass / later-pass chunk
+  constexpr int NF = 4 * NT;              // partial sums per lane per pass
+  static_assert(XI >= 1 && NCH >= RS && (QB == 8 || NT == 4), "stream kernel shape");
+  extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nwv = blockDim.x >> 6;
   const int q = lane >> 4, l16 = lane & 15;
   const int kb = wave * KS;
-  const int n0 = blockIdx.x * 16 * NT;
+  const int n0 = blockIdx.x * (16 * NT);
+  const int npass = MULTI ? (M + 15) >> 4 : 1;
   const size_t rowbytes = QB == 4 ? (size_t)(K >> 1) : (size_t)K;
+  const uint8_t* const wl = lds + wave * WB;  // this wave's ring
+  const uint8_t* const scl = wl + RS * SLOT;  // its scales / zero-points
+  const uint32_t wlo = __builtin_amdgcn_readfirstlane(lds_off(wl));
+  const uint32_t slo = wlo + RS * SLOT;
+  float* const red = (float*)(lds + nwv * WB);  // [nwv][8][64]
 
-  // 1. the slice's weights: n-tile t, chunk i = 16 bytes of row n0 + 16t + l16
-  u4_t wv[NT][NCH];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const uint8_t* wr =
-        W + (size_t)(n0 + 16 * t + l16) * rowbytes + (QB == 4 ? (kb >> 1) : kb) + 16 * q;
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) wv[t][i] = ldg128(wr + 64 * i);
-  }
-  // 2. scales / zero-points of the lane's D-layout columns n0 + 16t + l16:
-  //    int4 (group 128): the 4 groups of the slice; int8: per channel
-  u2_t sv[NT], zv[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int n = n0 + 16 * t + l16;
-    if constexpr (QB == 4) {
-      const size_t g0 = (size_t)n * (K >> 7) + (kb >> 7);
-      sv[t] = ldg64((const uint16_t*)S + g0);
-      if constexpr (ZDT == 3) zv[t] = u2_t{*(const uint32_t*)((const uint8_t*)Z + g0), 0u};
-      else if constexpr (ZDT >= 0) zv[t] = ldg64((const uint16_t*)Z + g0);
-    } else {
-      sv[t] = u2_t{(uint32_t)ld_raw<SDT>(S, (size_t)n), 0u};
-      if constexpr (ZDT >= 0) zv[t] = u2_t{(uint32_t)ld_raw<ZDT>(Z, (size_t)n), 0u};
+  // ---- copies
+  // Scales / zero-points.  int4: dword d of column n0 + lane holds groups
+  // 2d, 2d + 1 of the slice (zero-points u8: one dword, 4 groups).  int8: dword
+  // c holds columns n0 + 2c, 2c + 1 (u8 zero-points: 4c .. 4c + 3).
+  if constexpr (QB == 4) {
+    const size_t g0 = (size_t)min(n0 + lane, N - 1) * (K >> 7) + (kb >> 7);
+    dma4((const uint16_t*)S + g0, slo);
+    dma4((const uint16_t*)S + g0 + 2, slo + 256);
+    if constexpr (ZDT == 3) {
+      dma4((const uint8_t*)Z + g0, slo + 512);
+    } else if constexpr (ZDT >= 0) {
+      dma4((const uint16_t*)Z + g0, slo + 512);
+      dma4((const uint16_t*)Z + g0 + 2, slo + 768);
     }
+  } else {
+    const int c2 = min((n0 >> 1) + lane, (N >> 1) - 1);
+    dma4((const uint16_t*)S + 2 * c2, slo);
+    if constexpr (ZDT == 3) dma4((const uint8_t*)Z + 4 * min((n0 >> 2) + lane, (N >> 2) - 1), slo + 256);
+    else if constexpr (ZDT >= 0) dma4((const uint16_t*)Z + 2 * c2, slo + 256);
   }
-
-  auto load_x = [&](int mp, int i, u4_t (&xo)[MT][NJ]) {
+  // weights: lane l -> row r = l / 4 of the tile, piece (l % 4) ^ ((r >> 2) & 3)
+  const uint8_t* wsrc[NT];
+  {
+    const int r = lane >> 2, pc = (lane & 3) ^ ((r >> 2) & 3);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = min(16 * MT * mp + 16 * mt + l16, M - 1);
+    for (int t = 0; t < NT; ++t)
+      wsrc[t] = W + (size_t)min(n0 + 16 * t + r, N - 1) * rowbytes + (size_t)kb * QB / 8 + 16 * pc;
+  }
+  auto xsw = [](int r) { return QB == 4 ? (r & 15) : ((r >> 1) & 7); };
+  // X: copy h, lane l -> row h (64 / XPR) + l / XPR, piece (l % XPR) ^ xsw(row)
+  auto issue = [&](auto FIRSTC, int p, int i, int slot) {
+    const uint32_t sb = wlo + slot * SLOT;
+    // the slot's previous contents have been read
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if constexpr (decltype(FIRSTC)::value) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        xo[mt][j] = ldg128(X + (size_t)r * K + kb + CKK * i + 8 * NJ * q + 8 * j);
+      for (int t = 0; t < NT; ++t) dma16(wsrc[t] + 64 * i, sb + 1024 * t);
+    }
+#pragma unroll
+    for (int h = 0; h < XI; ++h) {
+      const int rr = h * (64 / XPR) + lane / XPR;
+      const int pc = (lane % XPR) ^ xsw(rr);
+      const int m = min(16 * p + rr, M - 1);
+      dma16(X + (size_t)m * K + kb + CK * i + 8 * pc, sb + NT * 1024 + 1024 * h);
     }
   };
+  const std::integral_constant<bool, true> first_c;
+  const std::integral_constant<bool, false> later_c;
+  static_for<0, RS>([&](auto IC) { issue(first_c, 0, decltype(IC)::value, decltype(IC)::value); });
 
-  for (int mp = 0; 16 * MT * mp < M; ++mp) {
-    // made inside the pass loop (volatile asm) so that the weight conversions
-    // below cannot be hoisted out of it - all of them at once would not fit in
-    // registers
+  // operand offsets in a slot: weight piece q of row l16; X piece of row l16
+  // for k-step j (int4 4q + j, int8 2q + j, matching the weight dwords)
+  const int woff = 64 * l16 + 16 * (q ^ ((l16 >> 2) & 3));
+  const int xrow = l16 & (XR - 1);
+  u4_t wv[NT][NCH];
+
+  // One pass: 16 rows of X against the slice's weights.  The first pass is
+  // peeled off the loop (it also reads the weights, and its waits count
+  // different copies).
+  auto run_pass = [&](auto FIRSTC, int p) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(FIRSTC)::value;
+    // made per pass (volatile asm) so that the weight conversions below stay
+    // in the pass loop
     const uint32_t vmask = vgpr_const(0x000F000Fu), vmagic = vgpr_const(w4_magic<BF16>());
-    f4_t y[MT][NT];
+    const uint32_t s4 = vgpr_const(4u), s8 = vgpr_const(8u), s12 = vgpr_const(12u);
+    const bool next = MULTI && p + 1 < npass;
+    f4_t y[NT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int t = 0; t < NT; ++t) y[mt][t] = f4_t{0.f, 0.f, 0.f, 0.f};
-    float xtot[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xtot[mt] = 0.f;  // int8: sum x over the slice, row 16mt + l16
-    u4_t xa[MT][NJ], xb[MT][NJ];
-    load_x(mp, 0, xa);
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      // keep each chunk's operand conversions inside its own iteration (the
-      // scheduler would otherwise hoist all of them and run out of registers)
+    for (int t = 0; t < NT; ++t) y[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+    float xtot = 0.f;  // int8: sum x over the slice, row 16p + l16
+    static_for<0, NCH>([&](auto IC) {
+      constexpr int i = decltype(IC)::value;
       __builtin_amdgcn_sched_barrier(0);
-      u4_t (&xo)[MT][NJ] = (i & 1) ? xb : xa;
-      u4_t (&xn)[MT][NJ] = (i & 1) ? xa : xb;
-      if (i + 1 < NCH) load_x(mp, i + 1, xn);
-      f4_t acc[MT][NT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[mt][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+      if (next) wait_vm<stream_ahead(RS, NCH, C0, C1, FIRST, i, true)>();
+      else wait_vm<stream_ahead(RS, NCH, C0, C1, FIRST, i, false)>();
+      const int slot = MULTI ? (p * NCH + i) % RS : i % RS;
+      const uint8_t* sp = wl + slot * SLOT;
+      u4_t xo[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        u4_t xop[MT];
+        const int pc = QB == 4 ? 4 * q + j : 2 * q + j;
+        xo[j] = *(const u4_t*)(sp + NT * 1024 + xrow * XB + 16 * (pc ^ xsw(xrow)));
+      }
+      if constexpr (FIRST) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) xop[mt] = QB == 4 ? perm_x8(xo[mt][j]) : xo[mt][j];
+        for (int t = 0; t < NT; ++t) wv[t][i] = *(const u4_t*)(sp + 1024 * t + woff);
+      }
+      // the slot takes the chunk RS ahead
+      if constexpr (i + RS < NCH) issue(FIRSTC, p, i + RS, slot);
+      else if (next) issue(later_c, p + 1, i + RS - NCH, slot);
+
+      f4_t acc[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const u4_t xop = QB == 4 ? perm_x8(xo[j]) : xo[j];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const u4_t w = wv[t][i];
           u4_t wop;
           if constexpr (QB == 4) {
             const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
-            wop = w4_operand(wj, vmask, vmagic);
+            wop = w4_operand_v(wj, vmask, vmagic, s4, s8, s12);
           } else {
-            wop = j == 0 ? w8_operand<BF16>(w.x, w.y) : w8_operand<BF16>(w.z, w.w);
+            // (opaque copies, so that the conversion stays in the pass loop)
+            uint32_t w0 = j == 0 ? w.x : w.z, w1 = j == 0 ? w.y : w.w;
+            asm volatile("" : "+v"(w0), "+v"(w1));
+            wop = w8_operand<BF16>(w0, w1);
           }
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) acc[mt][t] = mfma16<BF16>(xop[mt], wop, acc[mt][t]);
+          acc[t] = mfma16<BF16>(xop, wop, acc[t]);
         }
       }
-      // sum x of the chunk for row 16mt + l16 (all four lane quarters)
-      float xs[MT];
+      // sum x of the chunk for row 16p + l16 (all four lane quarters)
+      float xs = 0.0f;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        float v = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) v += xsum8(xo[mt][j], BF16);
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        xs[mt] = v;
-      }
+      for (int j = 0; j < NJ; ++j) xs += xsum8(xo[j], BF16);
+      xs += __shfl_xor(xs, 16, 64);
+      xs += __shfl_xor(xs, 32, 64);
       if constexpr (QB == 4) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          float xr[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) xr[e] = __shfl(xs[mt], 4 * q + e, 64);
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const float sc = raw_to_f32<SDT>(half_of(sv[t], i));
-            float zb = w4_offset<BF16>();
-            if constexpr (ZDT == 3) zb += (float)((zv[t].x >> (8 * i)) & 0xFFu);
-            else if constexpr (ZDT >= 0) zb += raw_to_f32<ZDT>(half_of(zv[t], i));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[mt][t][e] += sc * (acc[mt][t][e] - zb * xr[e]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          xtot[mt] += xs[mt];
-#pragma unroll
-          for (int t = 0; t < NT; ++t) y[mt][t] += acc[mt][t];
-        }
-      }
-    }
-    if constexpr (QB == 8) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
         float xr[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xr[e] = __shfl(xtot[mt], 4 * q + e, 64);
+        for (int e = 0; e < 4; ++e) xr[e] = __shfl(xs, 4 * q + e, 64);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const float sc = raw_to_f32<SDT>((typename Raw<SDT>::T)sv[t].x);
-          float z = 0.0f;
-          if constexpr (ZDT >= 0) z = raw_to_f32<ZDT>((typename Raw<ZDT>::T)zv[t].x);
+          const int c = 16 * t + l16;
+          const uint32_t sw = *(const uint32_t*)(scl + 256 * (i >> 1) + 4 * c);
+          const float sc = raw_to_f32<SDT>((uint16_t)(sw >> (16 * (i & 1))));
+          float zb = w4_offset<BF16>();
+          if constexpr (ZDT == 3) {
+            zb += (float)((*(const uint32_t*)(scl + 512 + 4 * c) >> (8 * i)) & 0xFFu);
+          } else if constexpr (ZDT >= 0) {
+            const uint32_t zw = *(const uint32_t*)(scl + 512 + 256 * (i >> 1) + 4 * c);
+            zb += raw_to_f32<ZDT>((uint16_t)(zw >> (16 * (i & 1))));
+          }
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[mt][t][e] = sc * (y[mt][t][e] - z * xr[e]);
+          for (int e = 0; e < 4; ++e) y[t][e] += sc * (acc[t][e] - zb * xr[e]);
         }
+      } else {
+        xtot += xs;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) y[t] += acc[t];
+      }
+      // (pins the chunk's epilogue here: the compiler would otherwise sink it
+      // and keep every chunk's accumulators live)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) asm volatile("" : "+v"(y[t]));
+    });
+    if constexpr (QB == 8) {
+      float xr[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xr[e] = __shfl(xtot, 4 * q + e, 64);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int c = 16 * t + l16;
+        const uint32_t sw = *(const uint32_t*)(scl + 4 * (c >> 1));
+        const float sc = raw_to_f32<SDT>((uint16_t)(sw >> (16 * (c & 1))));
+        float z = 0.0f;
+        if constexpr (ZDT == 3) {
+          z = (float)((*(const uint32_t*)(scl + 256 + 4 * (c >> 2)) >> (8 * (c & 3))) & 0xFFu);
+        } else if constexpr (ZDT >= 0) {
+          const uint32_t zw = *(const uint32_t*)(scl + 256 + 4 * (c >> 1));
+          z = raw_to_f32<ZDT>((uint16_t)(zw >> (16 * (c & 1))));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[t][e] = sc * (y[t][e] - z * xr[e]);
       }
     }
 
-    // reduce the K-slices: red[wave][f][lane], f = 4 (NT mt + t) + e
+    // reduce the K-slices, 8 partial sums f = 4 t + e per round:
+    // red[wave][f - 8 r][lane]
+    static_for<0, (NF + 7) / 8>([&](auto RC) {
+      constexpr int r = decltype(RC)::value;
+      constexpr int FN = NF - 8 * r < 8 ? NF - 8 * r : 8;
+      lds_barrier();  // earlier reads of red are done
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          red[(wave * NF + 4 * (NT * mt + t) + e) * 64 + lane] = y[mt][t][e];
-    __syncthreads();
-    for (int f = wave; f < NF; f += nwv) {
-      float v = 0.0f;
-      for (int w2 = 0; w2 < nwv; ++w2) v += red[(w2 * NF + f) * 64 + lane];
-      const int mt = (f >> 2) / NT, t = (f >> 2) % NT, e = f & 3;
-      const int row = 16 * MT * mp + 16 * mt + 4 * q + e;
-      if (row < M) store_out(Y, (size_t)row * N + n0 + 16 * t + l16, v, BF16);
-    }
-    __syncthreads();
-  }
+      for (int f = 0; f < FN; ++f) red[(wave * 8 + f) * 64 + lane] = y[(8 * r + f) >> 2][(8 * r + f) & 3];
+      lds_barrier();
+      for (int f = wave; f < FN; f += nwv) {
+        float v = 0.0f;
+        for (int w2 = 0; w2 < nwv; ++w2) v += red[(w2 * 8 + f) * 64 + lane];
+        const int F = 8 * r + f, t = F >> 2, e = F & 3;
+        const int row = 16 * p + 4 * q + e, col = n0 + 16 * t + l16;
+        if (row < M && col < N) store_out(Y, (size_t)row * N + col, v, BF16);
+      }
+    });
+  };
+  run_pass(first_c, 0);
+  if constexpr (MULTI)
+    for (int p = 1; p < npass; ++p) run_pass(later_c, p);
 }
 
 // ----------------------------------------------------------------------------
@@ -933,25 +1013,27 @@ TM_WQ_Z(tiled, 4, true, bf16, , )
 TM_WQ_Z(tiled, 8, false, f16, , )
 TM_WQ_Z(tiled, 8, true, bf16, , )
 
-// Wide (8 < M <= 64): wq_wide_q<QB>_<act>_z<zs>_m<MT>; block = 64 * K / 512 (<= 512)
-#define TM_WIDE(QB, BF, ACT, ZS, ZDT, MT)                                                      \
-  extern "C" __global__ __launch_bounds__(512) void wq_wide_q##QB##_##ACT##_z##ZS##_m##MT(     \
-      const uint16_t* X, const uint8_t* W, uint16_t* Y, const void* S, const void* Z, int M,   \
+// Streaming kernels: wq_stream_q<QB>_<act>_z<zs>_x<XR><s|m> (s: single pass,
+// M <= XR; m: multi-pass, M <= 64).  Scales are of the activation dtype.
+#define TM_STREAM(QB, BF, ACT, ZS, ZDT, NT, XR, MS, MULTI)                                     \
+  extern "C" __global__ __launch_bounds__(512) void wq_stream_q##QB##_##ACT##_z##ZS##_x##XR##MS( \
+      const uint16_t* X, const uint8_t* W, uint16_t* Y, const void* S, const void* Z, int M,    \
       int N, int K) {                                                                          \
-    wq_wide_body<QB, BF, (BF ? TM_DT_BF16 : TM_DT_F16), ZDT, MT>(X, W, Y, S, Z, M, N, K);      \
+    wq_stream_body<QB, BF, (BF ? TM_DT_BF16 : TM_DT_F16), ZDT, NT, XR, MULTI>(X, W, Y, S, Z, M, \
+                                                                              N, K);           \
   }
-#define TM_WIDE_Z(QB, BF, ACT, MT)                          \
-  TM_WIDE(QB, BF, ACT, n, -1, MT)                           \
-  TM_WIDE(QB, BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), MT) \
-  TM_WIDE(QB, BF, ACT, u, 3, MT)
-TM_WIDE_Z(4, false, f16, 1)
-TM_WIDE_Z(4, true, bf16, 1)
-TM_WIDE_Z(8, false, f16, 1)
-TM_WIDE_Z(8, true, bf16, 1)
-TM_WIDE_Z(4, false, f16, 2)
-TM_WIDE_Z(4, true, bf16, 2)
-TM_WIDE_Z(8, false, f16, 2)
-TM_WIDE_Z(8, true, bf16, 2)
+#define TM_STREAM_V(QB, BF, ACT, ZS, ZDT, NT) \
+  TM_STREAM(QB, BF, ACT, ZS, ZDT, NT, 8, s, false) \
+  TM_STREAM(QB, BF, ACT, ZS, ZDT, NT, 16, s, false) \
+  TM_STREAM(QB, BF, ACT, ZS, ZDT, NT, 16, m, true)
+#define TM_STREAM_Z(QB, BF, ACT, NT)                          \
+  TM_STREAM_V(QB, BF, ACT, n, -1, NT)                         \
+  TM_STREAM_V(QB, BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), NT) \
+  TM_STREAM_V(QB, BF, ACT, u, 3, NT)
+TM_STREAM_Z(4, false, f16, 4)
+TM_STREAM_Z(4, true, bf16, 4)
+TM_STREAM_Z(8, false, f16, 3)
+TM_STREAM_Z(8, true, bf16, 3)
 
 // GEMV (int4, exact K = NW * PF * 128, G = 128): wq_gemv4_<act>_z<zs>_w<NW>p<PF>
 // Occupancy of the K = 4096 variant: 8 waves per SIMD (<= 64 VGPRs), so that
