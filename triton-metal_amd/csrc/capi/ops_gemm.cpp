@@ -72,7 +72,9 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
     const int xr = M <= 8 ? 8 : 16;              // X rows staged per chunk
     const int rs = qbits == 4 ? 2 : 3;           // ring slots per wave
     const int slot = nt * 1024 + xr * (qbits == 4 ? 256 : 128);
-    const size_t slds = (size_t)nwv * (rs * slot + 1024) + (size_t)nwv * 8 * 64 * sizeof(float);
+    // per wave: ring, scales / zero-points (int4 2 KB, int8 1 KB); reduction
+    const size_t slds = (size_t)nwv * (rs * slot + (qbits == 4 ? 2048 : 1024)) +
+                        (size_t)nwv * 8 * 64 * sizeof(float);
     if (slds <= (size_t)max_dynamic_lds()) {
       char name[64];
       snprintf(name, sizeof name, "wq_stream_q%d_%s_z%c_x%d%c", qbits, act, zc, xr,

@@ -146,10 +146,14 @@ TM_DEV uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)(lds_void_t
 // a copy still targets.  m0 is written here; the kernels that use these
 // helpers use m0 for nothing else.
 TM_DEV void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory");
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
 }
 TM_DEV void dma4(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory");
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
 }
 // Wait until at most N vector memory operations of this wave are outstanding
 // (they complete in issue order).

@@ -469,8 +469,10 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
 
 // ----------------------------------------------------------------------------
 // Streaming kernel: 1 < M <= 64.  A workgroup owns NT 16-column tiles (int4:
-// 4, int8: 3) and all M rows; its K / 512 waves (at most 8) split K into
-// slices of 512 and are reduced through LDS after each pass of 16 rows.
+// 4, int8: 3) and all M rows; its nwv = K / 512 waves (at most 8) split K and
+// are reduced through LDS after each pass of 16 rows.  Wave w takes the chunks
+// c = nwv i + w (i = 0, 1, ...), so that at any time the waves of a workgroup
+// read adjacent segments of the same weight rows.
 // Weights and X reach LDS by global -> LDS copies issued in an order where
 // every 4 consecutive lanes read one 64-byte segment: the vector memory path
 // serves such groups at about three times the rate of the MFMA operand order,
@@ -484,12 +486,15 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
 // and waits for each with an explicit vmcnt (copies complete in issue order).
 // The single-pass kernel (M <= XR) takes each chunk's weights from LDS; the
 // multi-pass one keeps the first pass's weight registers for the later passes,
-// which stream X only.  Scales and zero-points are copied to LDS ahead of the
-// first chunks.
+// which stream X only.  Scales and zero-points are copied to each wave's LDS
+// ahead of its first chunks (int4: for lane (l16, q) the dword holding the
+// value of column 16 t + l16 in group nwv q + wave, the group of the wave's
+// chunk q; int8: the per-channel values).
 // int4 (group 128 = one chunk):  Y += s * (sum x (OFF + q) - (OFF + z) sum x)
 // int8:                          Y  = s * (sum x q - z sum x)
 // sum x per chunk comes from v_dot2 on the X operands.
-// Dynamic LDS: nwv * (RS * SLOT + 1024) + nwv * 2 KB.
+// Dynamic LDS: nwv * (RS * SLOT + SCB) + nwv * 2 KB (reduction), SCB = 2 KB
+// (int4) or 1 KB (int8) of scales / zero-points.
 // ----------------------------------------------------------------------------
 namespace {
 // (The dwords go through by-value helpers: __builtin_bit_cast applied directly
@@ -538,15 +543,16 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
   constexpr int XI = XR * XPR / 64;       // X copies (1 KB each) per chunk
   constexpr int RS = QB == 4 ? 2 : 3;     // ring slots per wave
   constexpr int SLOT = NT * 1024 + XR * XB;
-  constexpr int WB = RS * SLOT + 1024;    // per-wave LDS: ring, scales / zero-points
+  constexpr int SCB = QB == 4 ? 512 * NT : 1024;  // per-wave scales / zero-points
+  constexpr int WB = RS * SLOT + SCB;     // per-wave LDS: ring, scales
   constexpr int C0 = NT + XI, C1 = XI;    // copies per first-pass / later-pass chunk
   constexpr int NF = 4 * NT;              // partial sums per lane per pass
   static_assert(XI >= 1 && NCH >= RS && (QB == 8 || NT == 4), "stream kernel shape");
   extern __shared__ __align__(16) uint8_t lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nwv = blockDim.x >> 6;
   const int q = lane >> 4, l16 = lane & 15;
-  const int kb = wave * KS;
   const int n0 = blockIdx.x * (16 * NT);
   const int npass = MULTI ? (M + 15) >> 4 : 1;
   const size_t rowbytes = QB == 4 ? (size_t)(K >> 1) : (size_t)K;
@@ -557,18 +563,17 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
   float* const red = (float*)(lds + nwv * WB);  // [nwv][8][64]
 
   // ---- copies
-  // Scales / zero-points.  int4: dword d of column n0 + lane holds groups
-  // 2d, 2d + 1 of the slice (zero-points u8: one dword, 4 groups).  int8: dword
-  // c holds columns n0 + 2c, 2c + 1 (u8 zero-points: 4c .. 4c + 3).
+  // Scales / zero-points.  int4: [t][s, z][64 lanes] dwords, lane (l16, q)
+  // holding group g = nwv q + wave of column n0 + 16 t + l16 (its half / byte
+  // is fixed by g, as K / 128 is a multiple of 4).  int8: dword c holds
+  // columns n0 + 2c, 2c + 1 (u8 zero-points: 4c .. 4c + 3).
   if constexpr (QB == 4) {
-    const size_t g0 = (size_t)min(n0 + lane, N - 1) * (K >> 7) + (kb >> 7);
-    dma4((const uint16_t*)S + g0, slo);
-    dma4((const uint16_t*)S + g0 + 2, slo + 256);
-    if constexpr (ZDT == 3) {
-      dma4((const uint8_t*)Z + g0, slo + 512);
-    } else if constexpr (ZDT >= 0) {
-      dma4((const uint16_t*)Z + g0, slo + 512);
-      dma4((const uint16_t*)Z + g0 + 2, slo + 768);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const size_t gi = (size_t)min(n0 + 16 * t + l16, N - 1) * (K >> 7) + nwv * q + wave;
+      dma4((const uint16_t*)S + (gi & ~(size_t)1), slo + 512 * t);
+      if constexpr (ZDT == 3) dma4((const uint8_t*)Z + (gi & ~(size_t)3), slo + 512 * t + 256);
+      else if constexpr (ZDT >= 0) dma4((const uint16_t*)Z + (gi & ~(size_t)1), slo + 512 * t + 256);
     }
   } else {
     const int c2 = min((n0 >> 1) + lane, (N >> 1) - 1);
@@ -577,12 +582,13 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
     else if constexpr (ZDT >= 0) dma4((const uint16_t*)Z + 2 * c2, slo + 256);
   }
   // weights: lane l -> row r = l / 4 of the tile, piece (l % 4) ^ ((r >> 2) & 3)
+  // of the 64-byte segment of chunk c = nwv i + wave
   const uint8_t* wsrc[NT];
   {
     const int r = lane >> 2, pc = (lane & 3) ^ ((r >> 2) & 3);
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      wsrc[t] = W + (size_t)min(n0 + 16 * t + r, N - 1) * rowbytes + (size_t)kb * QB / 8 + 16 * pc;
+      wsrc[t] = W + (size_t)min(n0 + 16 * t + r, N - 1) * rowbytes + 64 * wave + 16 * pc;
   }
   auto xsw = [](int r) { return QB == 4 ? (r & 15) : ((r >> 1) & 7); };
   // X: copy h, lane l -> row h (64 / XPR) + l / XPR, piece (l % XPR) ^ xsw(row)
@@ -592,14 +598,14 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if constexpr (decltype(FIRSTC)::value) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) dma16(wsrc[t] + 64 * i, sb + 1024 * t);
+      for (int t = 0; t < NT; ++t) dma16(wsrc[t] + 64 * nwv * i, sb + 1024 * t);
     }
 #pragma unroll
     for (int h = 0; h < XI; ++h) {
       const int rr = h * (64 / XPR) + lane / XPR;
       const int pc = (lane % XPR) ^ xsw(rr);
       const int m = min(16 * p + rr, M - 1);
-      dma16(X + (size_t)m * K + kb + CK * i + 8 * pc, sb + NT * 1024 + 1024 * h);
+      dma16(X + (size_t)m * K + CK * (nwv * i + wave) + 8 * pc, sb + NT * 1024 + 1024 * h);
     }
   };
   const std::integral_constant<bool, true> first_c;
@@ -643,9 +649,11 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
 #pragma unroll
         for (int t = 0; t < NT; ++t) wv[t][i] = *(const u4_t*)(sp + 1024 * t + woff);
       }
-      // the slot takes the chunk RS ahead
+      // the slot takes the chunk RS ahead (issued before the MFMAs: nothing
+      // is scheduled across)
       if constexpr (i + RS < NCH) issue(FIRSTC, p, i + RS, slot);
       else if (next) issue(later_c, p + 1, i + RS - NCH, slot);
+      __builtin_amdgcn_sched_barrier(0);
 
       f4_t acc[NT];
 #pragma unroll
@@ -679,18 +687,17 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
         float xr[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) xr[e] = __shfl(xs, 4 * q + e, 64);
+        const int g = nwv * i + wave;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-          const int c = 16 * t + l16;
-          const uint32_t sw = *(const uint32_t*)(scl + 256 * (i >> 1) + 4 * c);
-          const float sc = raw_to_f32<SDT>((uint16_t)(sw >> (16 * (i & 1))));
+          // dword of lane (l16, i): group g of column 16 t + l16
+          const uint8_t* sp2 = scl + 512 * t + 4 * (16 * i + l16);
+          const float sc = raw_to_f32<SDT>((uint16_t)(*(const uint32_t*)sp2 >> (16 * (g & 1))));
           float zb = w4_offset<BF16>();
-          if constexpr (ZDT == 3) {
-            zb += (float)((*(const uint32_t*)(scl + 512 + 4 * c) >> (8 * i)) & 0xFFu);
-          } else if constexpr (ZDT >= 0) {
-            const uint32_t zw = *(const uint32_t*)(scl + 512 + 256 * (i >> 1) + 4 * c);
-            zb += raw_to_f32<ZDT>((uint16_t)(zw >> (16 * (i & 1))));
-          }
+          if constexpr (ZDT == 3)
+            zb += (float)((*(const uint32_t*)(sp2 + 256) >> (8 * (g & 3))) & 0xFFu);
+          else if constexpr (ZDT >= 0)
+            zb += raw_to_f32<ZDT>((uint16_t)(*(const uint32_t*)(sp2 + 256) >> (16 * (g & 1))));
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[t][e] += sc * (acc[t][e] - zb * xr[e]);
         }
