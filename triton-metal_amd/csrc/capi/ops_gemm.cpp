@@ -87,7 +87,8 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
   // exact-shape int4 GEMV: K = NW * PF * 128, G = 128
   if (fast && qbits == 4 && M <= 8 && G == 128 && (K == 4096 || K == 8192) && aligned16(S) &&
       (!Z || aligned16(Z))) {
-    size_t glds = (size_t)M * (K + 8) * 2 + (size_t)(K / 128) * 8 * 4 + (size_t)(K / 128) * 64;
+    // X, two [chunk][8] float sums (sum x, sum x * offset), scales + zero-points
+    size_t glds = (size_t)M * (K + 8) * 2 + 2 * (size_t)(K / 128) * 8 * 4 + (size_t)(K / 128) * 64;
     if (glds <= (size_t)max_dynamic_lds()) {
       const int pf = K == 4096 ? 4 : 8;
       char name[64];

@@ -142,6 +142,32 @@ TM_DEV u4_t perm_x8(u4_t x) {
   return r;
 }
 
+// fp16 int4 operand in 5 instructions: a nibble at bits 0-3 of a half ORed
+// under 0x6400 (1024) is 1024 + q; one at bits 4-7 ORed under 0x5400 (64,
+// whose ulp is 1/16) is 64 + q.  The halves come out in w4_operand's order
+// [n0 n4] [n1 n5] [n2 n6] [n3 n7]: nibble j (k = 8 w + j) carries the offset
+// 1024 for even j, 64 for odd j.
+TM_DEV u4_t w4_operand_h(uint32_t w, uint32_t m_lo, uint32_t m_hi, uint32_t g_lo,
+                         uint32_t g_hi) {
+  const uint32_t t = w >> 8;
+  u4_t r;
+  r.x = (w & m_lo) | g_lo;
+  r.y = (w & m_hi) | g_hi;
+  r.z = (t & m_lo) | g_lo;
+  r.w = (t & m_hi) | g_hi;
+  return r;
+}
+// sum of x_k * off_k over 8 fp16 values in k order (off: 1024 even k, 64 odd k)
+TM_DEV float sumoff8_h(u4_t v) {
+  const h2_t off = {(half_t)1024.0f, (half_t)64.0f};
+  float a = 0.0f;
+  a = __builtin_amdgcn_fdot2(as_h2(v.x), off, a, false);
+  a = __builtin_amdgcn_fdot2(as_h2(v.y), off, a, false);
+  a = __builtin_amdgcn_fdot2(as_h2(v.z), off, a, false);
+  a = __builtin_amdgcn_fdot2(as_h2(v.w), off, a, false);
+  return a;
+}
+
 template <bool BF16> TM_DEV float sum8(u4_t v) {
   uint32_t d[4] = {v.x, v.y, v.z, v.w};
   float s = 0.0f;
@@ -361,10 +387,12 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
 // block = NW waves; wave w owns k = w*PF*128 .. +PF*128 of the workgroup's
 // 16 columns.  Everything is unrolled at compile time: PF 16-byte weight
 // loads per lane, one vector load of the PF scales (and zero-points) per
-// lane, MFMAs chunk by chunk as the weights arrive.  Dynamic LDS: M * (K + 8)
-// * 2 bytes of X, (K / 128) * 8 * 4 bytes of chunk sums laid out
-// [chunk][row 0..7], then the workgroup's scales and zero-points (16 rows x
-// K / 128, 2 bytes each).  S (and Z) must be 16-byte aligned.
+// lane, MFMAs chunk by chunk as the weights arrive.  fp16 activations use the
+// 5-instruction operand (w4_operand_h) and a second per-chunk sum, of x * off.
+// Dynamic LDS: M * (K + 8) * 2 bytes of X, 2 * (K / 128) * 8 * 4 bytes of
+// chunk sums laid out [chunk][row 0..7] (sum x, then sum x * off), then the
+// workgroup's scales and zero-points (16 rows x K / 128, 2 bytes each).  S
+// (and Z) must be 16-byte aligned.
 // ----------------------------------------------------------------------------
 template <bool BF16, int ZDT, int NW, int PF>
 __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
@@ -380,12 +408,14 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
   const int ldx = K + 8;
   const int nch = K >> 7;
   float* xsum = (float*)(xs + (size_t)M * ldx);  // [nch][8]
-  uint16_t* sst = (uint16_t*)(xsum + nch * 8);   // scales of the 16 columns [16][nch]
+  float* xoff = xsum + nch * 8;                  // fp16: [nch][8] sums of x * off
+  uint16_t* sst = (uint16_t*)(xoff + nch * 8);   // scales of the 16 columns [16][nch]
   uint16_t* zst = sst + 16 * nch;                // zero-points [16][nch] (bytes if uint8)
   const int n = blockIdx.x * 16 + (lane & 15), q = lane >> 4;
   const int m = min(lane & 15, M - 1);
   const int kbeg = wave * (PF * 128);
   const uint32_t vmask = vgpr_const(0x000F000Fu), vmagic = vgpr_const(w4_magic<BF16>());
+  const uint32_t vmask_hi = vgpr_const(0x00F000F0u), vmagic_hi = vgpr_const(0x54005400u);
 
   // 1. first X row pieces (PF / 4 per thread), this workgroup's scales and
   //    zero-points (16 rows x nch, one contiguous block each), 2. weights,
@@ -413,6 +443,10 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
       const int p = tid + NT * u;
       const float sm = sum16(sum8<BF16>(v[u]));
       if ((p & 15) == 0) xsum[(p >> 4) * 8 + r] = sm;
+      if constexpr (!BF16) {
+        const float so = sum16(sumoff8_h(v[u]));
+        if ((p & 15) == 0) xoff[(p >> 4) * 8 + r] = so;
+      }
       *(u4_t*)(xs + r * ldx + p * 8) = perm_x8(v[u]);
     }
   };
@@ -442,16 +476,25 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
     for (int j = 0; j < 4; ++j) {
       const u4_t w = wv[i];
       const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
-      a = mfma16<BF16>(*(const u4_t*)(xa + 128 * i + 8 * j), w4_operand(wj, vmask, vmagic), a);
+      const u4_t wop = BF16 ? w4_operand(wj, vmask, vmagic)
+                            : w4_operand_h(wj, vmask, vmask_hi, vmagic, vmagic_hi);
+      a = mfma16<BF16>(*(const u4_t*)(xa + 128 * i + 8 * j), wop, a);
     }
     const int gi = (lane & 15) * nch + (kbeg >> 7) + i;
     const float sc = raw_to_f32<SDT>(sst[gi]);
-    float zb = w4_offset<BF16>();
-    if constexpr (ZDT == 3) zb += (float)((const uint8_t*)zst)[gi];
-    else if constexpr (ZDT >= 0) zb += raw_to_f32<ZDT>(zst[gi]);
+    float z = 0.0f;
+    if constexpr (ZDT == 3) z = (float)((const uint8_t*)zst)[gi];
+    else if constexpr (ZDT >= 0) z = raw_to_f32<ZDT>(zst[gi]);
     const f4_t xv4 = *(const f4_t*)(xsr + 8 * i);
+    if constexpr (BF16) {
+      const float zb = w4_offset<BF16>() + z;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) y[e] += sc * (a[e] - zb * xv4[e]);
+      for (int e = 0; e < 4; ++e) y[e] += sc * (a[e] - zb * xv4[e]);
+    } else {
+      const f4_t xo4 = *(const f4_t*)(xsr + nch * 8 + 8 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] += sc * (a[e] - xo4[e] - z * xv4[e]);
+    }
   }
 
   if (wave > 0) red[wave - 1][lane] = y;
