@@ -138,6 +138,7 @@ int dense(const void* A, const void* B, void* C, const void* bias, int M, int N,
     int bm;
     if (t128 >= 256) { tile = "t128"; bm = 128; }
     else if (t64 >= 192) { tile = "t64"; bm = 64; }
+    else if (K <= 512) { tile = "t32k"; bm = 32; }  // one load stage
     else { tile = "t32"; bm = 32; }
     char name[96];
     snprintf(name, sizeof name, "gemm_%s_%s_%s_%s%s", tile, bt ? "nt" : "nn",

@@ -222,10 +222,13 @@ extern "C" __global__ __launch_bounds__(256) void gemm_general(
     gemm_body<BM, BN, BK, WM, WN, BT, BF, ODT, BIAS>(A, B, C, bias, M, N, K, lda, ldb, ldc);    \
   }
 
+// t32k: 32 x 32 tiles with the whole K <= 512 staged at once - for small
+// problems the K loop of t32 is a chain of exposed load latencies
 #define TM_GEMM_TILES(BT, BTN, BF, IN, ODT, OUT, BIAS, BN_)                               \
   TM_GEMM_INST(gemm_t128_##BTN##_##IN##_##OUT##BN_, 128, 128, 64, 2, 2, BT, BF, ODT, BIAS) \
   TM_GEMM_INST(gemm_t64_##BTN##_##IN##_##OUT##BN_, 64, 64, 64, 2, 2, BT, BF, ODT, BIAS)    \
-  TM_GEMM_INST(gemm_t32_##BTN##_##IN##_##OUT##BN_, 32, 32, 64, 2, 2, BT, BF, ODT, BIAS)
+  TM_GEMM_INST(gemm_t32_##BTN##_##IN##_##OUT##BN_, 32, 32, 64, 2, 2, BT, BF, ODT, BIAS)    \
+  TM_GEMM_INST(gemm_t32k_##BTN##_##IN##_##OUT##BN_, 32, 32, 512, 2, 2, BT, BF, ODT, BIAS)
 
 #define TM_GEMM_OUTS(BT, BTN, BF, IN, BIAS, BN_)                      \
   TM_GEMM_TILES(BT, BTN, BF, IN, (BF ? TM_DT_BF16 : TM_DT_F16), same, BIAS, BN_) \
