@@ -227,12 +227,12 @@ def test_int8_shapes(dev, M, N, K, zeros):
     check_close(out.cpu(), ref)
 
 
-# --- stream kernel (1 < M <= 64, K = 512..4096 in steps of 512) ------------------
+# --- stream kernel (1 < M <= 128 for int4, 64 for int8; K = 512..4096 by 512) -----
 # N not a multiple of the workgroup's columns (int4: 64, int8: 48) leaves a
 # partial last workgroup.
 @pytest.mark.parametrize("M,N,K", [(2, 64, 512), (8, 80, 4096), (9, 128, 1024), (16, 128, 4096),
                                    (17, 80, 2048), (32, 128, 1536), (33, 64, 4096),
-                                   (64, 128, 1024)])
+                                   (64, 128, 1024), (100, 64, 1024), (128, 80, 2048)])
 @pytest.mark.parametrize("zeros", ["f16", "u8", None])
 @pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
 def test_int4_stream_shapes(dev, M, N, K, zeros, act):

@@ -63,9 +63,10 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
               aligned16(W);
   const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
   const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
-  // streaming kernel: 1 < M <= 64, K-slices of 512 per wave (at most 8)
+  // streaming kernel: 1 < M <= 64 (int4: 128), K-slices of 512 per wave (at
+  // most 8); past 64 rows the int8 tiled kernel is the faster one
   const bool aligned4 = ((uintptr_t)S & 3u) == 0 && (!Z || ((uintptr_t)Z & 3u) == 0);
-  if (fast && M > 1 && M <= 64 && K % 512 == 0 && K <= 4096 && aligned4 &&
+  if (fast && M > 1 && M <= (qbits == 4 ? 128 : 64) && K % 512 == 0 && K <= 4096 && aligned4 &&
       (qbits == 8 || G == 128)) {
     const int nwv = K / 512;
     const int nt = qbits == 4 ? 4 : 3;           // 16-column tiles per workgroup

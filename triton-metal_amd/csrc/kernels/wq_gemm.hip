@@ -27,7 +27,7 @@
 // Kernels
 //   wq_gemv4_*   int4, M = 1 (and M <= 8 when K = 8192): GEMV, the whole grid
 //                resident, per-chunk MFMAs as the weights land.
-//   wq_stream_*  1 < M <= 64, K <= 4096: weights and X streamed through LDS
+//   wq_stream_*  1 < M <= 64 (int4: 128), K <= 4096: weights and X streamed through LDS
 //                rings by global -> LDS copies, K split over the waves.
 //   wq_skinny_*  other M <= 8 shapes: the whole X[M, K] is staged once per
 //                workgroup in LDS; one workgroup owns 16 output columns, its 4
@@ -511,7 +511,7 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
 }
 
 // ----------------------------------------------------------------------------
-// Streaming kernel: 1 < M <= 64.  A workgroup owns NT 16-column tiles (int4:
+// Streaming kernel: 1 < M <= 128.  A workgroup owns NT 16-column tiles (int4:
 // 4, int8: 3) and all M rows; its nwv = K / 512 waves (at most 8) split K and
 // are reduced through LDS after each pass of 16 rows.  Wave w takes the chunks
 // c = nwv i + w (i = 0, 1, ...), so that at any time the waves of a workgroup
@@ -1064,7 +1064,7 @@ TM_WQ_Z(tiled, 8, false, f16, , )
 TM_WQ_Z(tiled, 8, true, bf16, , )
 
 // Streaming kernels: wq_stream_q<QB>_<act>_z<zs>_x<XR><s|m> (s: single pass,
-// M <= XR; m: multi-pass, M <= 64).  Scales are of the activation dtype.
+// M <= XR; m: multi-pass, M <= 128).  Scales are of the activation dtype.
 #define TM_STREAM(QB, BF, ACT, ZS, ZDT, NT, XR, MS, MULTI)                                     \
   extern "C" __global__ __launch_bounds__(512) void wq_stream_q##QB##_##ACT##_z##ZS##_x##XR##MS( \
       const uint16_t* X, const uint8_t* W, uint16_t* Y, const void* S, const void* Z, int M,    \
