@@ -96,14 +96,15 @@ def test_int4_dequant_tile_bit_exact(dev, act):
     assert torch.equal(got.cpu().view(torch.int16), ref.view(torch.int16))
 
 
-# (M, K) of each kernel kind: the stream kernel takes 1 < M <= 64 with
+# (M, K, N) of each kernel kind: the stream kernel takes 1 < M <= 64 with
 # K <= 4096; the GEMV M = 1 and K = 8192; skinny the remaining M <= 8 shapes
-# with K % 512 == 0; tiled M > 64.
-INT4_KINDS = {"skinny": (8, 5120), "gemv": (1, 4096), "gemv8k": (8, 8192),
-              "stream8": (8, 4096), "stream16": (16, 2048), "stream_multi": (40, 2048),
-              "tiled": (72, 512)}
-INT8_KINDS = {"skinny": (8, 768), "stream8": (8, 2048), "stream16": (16, 2048),
-              "stream_multi": (40, 1024), "tiled": (72, 512)}
+# with K % 512 == 0; wide M > 64 with fp16 activations and N % 128 == 0
+# (int8: no zero-points); tiled the other M > 64 shapes.
+INT4_KINDS = {"skinny": (8, 5120, 64), "gemv": (1, 4096, 64), "gemv8k": (8, 8192, 64),
+              "stream8": (8, 4096, 64), "stream16": (16, 2048, 64),
+              "stream_multi": (40, 2048, 64), "tiled": (72, 512, 64), "wide": (100, 1024, 256)}
+INT8_KINDS = {"skinny": (8, 768, 64), "stream8": (8, 2048, 64), "stream16": (16, 2048, 64),
+              "stream_multi": (40, 1024, 64), "tiled": (72, 512, 64), "wide": (100, 1024, 256)}
 
 
 @pytest.mark.parametrize("kind", list(INT4_KINDS))
@@ -111,8 +112,8 @@ INT8_KINDS = {"skinny": (8, 768), "stream8": (8, 2048), "stream16": (16, 2048),
 def test_int4_in_register_dequant_bit_exact(dev, kind, act):
     """One-hot activation rows make each output equal one dequantised weight,
     so the GEMM's in-register dequantisation is compared bit for bit."""
-    N, G = 64, 128
-    M, K = INT4_KINDS[kind]
+    G = 128
+    M, K, N = INT4_KINDS[kind]
     _, q, packed, s, z = make_int4_problem(M, N, K, G, seed=12, act=act)
     ks = torch.randperm(K, generator=_gen(3))[:M]
     x = torch.zeros(M, K, dtype=act)
@@ -125,8 +126,7 @@ def test_int4_in_register_dequant_bit_exact(dev, kind, act):
 
 @pytest.mark.parametrize("kind", list(INT8_KINDS))
 def test_int8_in_register_dequant_bit_exact(dev, kind):
-    N = 64
-    M, K = INT8_KINDS[kind]
+    M, K, N = INT8_KINDS[kind]
     _, w, s, _ = make_int8_problem(M, N, K, seed=13)
     ks = torch.randperm(K, generator=_gen(4))[:M]
     x = torch.zeros(M, K, dtype=torch.float16)
@@ -191,9 +191,11 @@ def test_int4_shapes_and_zero_types(dev, M, N, K, G, zeros):
     check_close(out.cpu(), ref)
 
 
-def test_int4_fractional_zero_points(dev):
-    """Non-integer zero-points take the fp32 formula path lane by lane."""
-    M, N, K, G = 4, 64, 1024, 128
+@pytest.mark.parametrize("M,N", [(4, 64), (80, 256)])
+def test_int4_fractional_zero_points(dev, M, N):
+    """Non-integer zero-points take the fp32 formula path (lane by lane in the
+    skinny kernels, per chunk in the wide kernel)."""
+    K, G = 1024, 128
     x, q, packed, s, _ = make_int4_problem(M, N, K, G, seed=21)
     z = (torch.rand(N, K // G, generator=_gen(22)) * 8).half()
     z[::2] = z[::2].round()  # mix integral and fractional rows
@@ -256,6 +258,29 @@ def test_int8_stream_shapes(dev, M, N, K, zeros, act):
                    M, N, K)
     ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
     check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(65, 128, 512), (128, 256, 4096), (200, 384, 2048),
+                                   (300, 128, 1024)])
+@pytest.mark.parametrize("zeros", ["f16", "u8", None])
+def test_int4_wide_shapes(dev, M, N, K, zeros):
+    G = 128
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 5 + N + K, zeros=zeros)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
+                   None if z is None else z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    check_close(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(65, 128, 256), (100, 256, 1024), (128, 128, 4096),
+                                   (257, 384, 768)])
+def test_int8_wide_shapes(dev, M, N, K):
+    x, w, s, _ = make_int8_problem(M, N, K, seed=M + 3 * N + K)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None, M, N, K)
+    ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), None, M, N, K)
+    check_close(out.cpu(), ref)
 
 
 def test_int8_stream_u8_zero_points(dev):

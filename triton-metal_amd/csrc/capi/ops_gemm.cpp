@@ -63,6 +63,24 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
               aligned16(W);
   const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
   const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
+  // wide kernel: fp16 activations, M > 64, 64 x 128 output blocks
+  if (fast && adt == TM_DT_F16 && M > 64 && N % 128 == 0 && aligned16(S) &&
+      (!Z || aligned16(Z)) &&
+      ((qbits == 4 && G == 128 && K % 512 == 0 && K <= 4096) ||
+       (qbits == 8 && zdt == TM_DT_NONE && K % 256 == 0))) {
+    const int ns = qbits == 4 ? 3 : 4, ck = qbits == 4 ? 64 : 32;
+    size_t wl = (size_t)ns * 4 * (64 * 2 * ck + 4096);  // ring stages
+    if (qbits == 4)  // scales and zero-points of the 128 columns
+      wl += (size_t)2 * K + (zdt == TM_DT_NONE ? 0 : zdt == TM_DT_U8 ? (size_t)K : (size_t)2 * K);
+    if (wl <= (size_t)max_dynamic_lds()) {
+      char name[64];
+      snprintf(name, sizeof name, "wq_wide_q%d_f16_z%c", qbits, zc);
+      const int mtl = (M + 63) / 64, ntl = N / 128;
+      const int grid = 8 * mtl * ((ntl + 7) / 8);
+      return launch(kernel(name), dim3(grid), dim3(512), (unsigned)wl, stream, X, W, Y, S, Z, M,
+                    N, K);
+    }
+  }
   // streaming kernel: 1 < M <= 64 (int4: 128), K-slices of 512 per wave (at
   // most 8); past 64 rows the int8 tiled kernel is the faster one
   const bool aligned4 = ((uintptr_t)S & 3u) == 0 && (!Z || ((uintptr_t)Z & 3u) == 0);
