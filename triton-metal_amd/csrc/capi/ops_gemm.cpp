@@ -67,7 +67,7 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
   if (fast && adt == TM_DT_F16 && M > 64 && N % 128 == 0 && aligned16(S) &&
       (!Z || aligned16(Z)) &&
       ((qbits == 4 && G == 128 && K % 512 == 0 && K <= 4096) ||
-       (qbits == 8 && zdt == TM_DT_NONE && K % 256 == 0))) {
+       (qbits == 8 && zdt == TM_DT_NONE && K % 128 == 0))) {
     const int ns = qbits == 4 ? 3 : 4, ck = qbits == 4 ? 64 : 32;
     size_t wl = (size_t)ns * 4 * (64 * 2 * ck + 4096);  // ring stages
     if (qbits == 4)  // scales and zero-points of the 128 columns

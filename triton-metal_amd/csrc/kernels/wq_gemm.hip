@@ -969,46 +969,47 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
 
 // ----------------------------------------------------------------------------
 // Wide kernel: fp16 activations, M > 64; int4 with G = 128 (K % 512 == 0,
-// K <= 4096) or int8 without zero-points (K % 256 == 0); N % 128 == 0.
+// K <= 4096) or int8 without zero-points (K % 128 == 0); N % 128 == 0.
 // A workgroup owns 64 rows x 128 columns.  Its 8 waves are 2 column halves
-// (64 columns) x 4 K-quarters; each wave accumulates a 64 x 64 block over its
-// K-quarter with v_mfma_f32_32x32x16_f16 (2 x 2 tiles of 32 x 32), and the
-// four K-quarter partials are summed through LDS at the end.
+// (64 columns) x 4 K-quarters; each wave accumulates a 64 x 64 block with
+// v_mfma_f32_32x32x16_f16 (2 x 2 tiles of 32 x 32), and the four K-quarter
+// partials are summed through LDS at the end.
 // The weight operand is the dequantised value itself, exactly rounded:
-//   int4: round_f16((q - z) * s) - the halves 64 + q are made by bit
-//         operations, then a packed fp16 subtraction of 64 + z (exact when
-//         64 + z is an fp16 value: integral zero-points, any uint8) and a
-//         packed multiplication by s (one rounding).  A chunk in which some
-//         lane's 64 + z is not exact builds its operands in fp32 instead.
+//   int4: round_f16((q - z) * s) - the halves 1024 + q (even k) and 64 + q
+//         (odd k) are made by bit operations, then a packed fp16 subtraction
+//         of (1024 + z, 64 + z) (exact for integral zero-points: every uint8,
+//         and fp16 ones without a fraction) and a packed multiplication by s
+//         (one rounding).  A chunk in which some lane's zero-point has a
+//         fraction (or exceeds 1000) builds its operands in fp32 instead.
 //   int8: q itself; the per-channel scale multiplies the fp32 sums.
 // So every product is x * (the dequantised weight tile entry), as in the
 // reference's dequantise-then-accumulate formula, with fp32 accumulation.
-// Data movement: per K-quarter and chunk of CK k, X [64 rows][CK] and the
-// weights [128 rows][32 bytes] are copied global -> LDS (4 consecutive lanes
-// per 64-byte segment for X) into a ring of NS stages; the two waves of a
-// K-quarter each copy half of X and their own weight rows, and one workgroup
-// barrier per chunk publishes the copies.  XOR swizzles keep the MFMA operand
-// reads free of bank conflicts:
-//   X piece p of tile row r at slot p ^ xw(r): int4 (r >> 1) & 7, int8 (r >> 2) & 3
-//   weight piece p of row r at slot p ^ ((r >> 3) & 1)
+// Data movement: K advances in stages of 4 CK k; K-quarter kq takes chunk kq
+// (CK k) of every stage, so one stage is a contiguous slice of every row:
+// X [64 rows][8 CK bytes] and weights [128 rows][128 bytes], copied global ->
+// LDS in whole lines into a ring of NS stages.  All 8 waves share the copies;
+// one workgroup barrier per stage publishes them.  XOR swizzles keep the MFMA
+// operand reads free of bank conflicts:
+//   X piece p of tile row r at slot p ^ (r & 15)
+//   weight piece p of row r at slot p ^ ((r >> 1) & 7)
 // Within a chunk, k-step s of lane half h uses the 8 k of X piece / weight
 // group 4 h + s (int4) or 2 h + s (int8), so that one 16-byte read gives a
 // lane the weights of all k-steps of the chunk.
 // int4 scales / zero-points of the workgroup's 128 rows are copied to LDS once.
-// Dynamic LDS: NS * 4 * (64 * 2 * CK + 4096) bytes, int4 plus 2 K (scales)
+// Dynamic LDS: NS * (64 * 8 * CK + 16384) bytes, int4 plus 2 K (scales)
 // and 2 K or K (fp16 / uint8 zero-points).
 // ----------------------------------------------------------------------------
 namespace {
-// int4 operand in k order, every value offset by 64: nibbles n0..n7 of w
-// (k = 8 j + i in nibble i) -> fp16 pairs [64+n0, 64+n1] .. [64+n6, 64+n7].
-// m = 0x00F000F0, g = 0x54005400 (held in VGPRs).
-TM_DEV u4_t w4_nat64(uint32_t w, uint32_t m, uint32_t g) {
-  const uint32_t w4 = w << 4;
+// int4 operand in k order: nibbles n0..n7 of w (k = 8 j + i in nibble i) ->
+// fp16 pairs [1024+n0, 64+n1] .. [1024+n6, 64+n7]: byte i of w goes to both
+// halves, the low nibble is kept under 0x6400 (ulp 1), the high one under
+// 0x5400 (ulp 1/16).  m = 0x00F0000F, g = 0x54006400 (held in VGPRs).
+TM_DEV u4_t w4_nat(uint32_t w, uint32_t m, uint32_t g) {
   u4_t r;
-  r.x = (perm_b32(w, w4, 0x0C040C00u) & m) | g;
-  r.y = (perm_b32(w, w4, 0x0C050C01u) & m) | g;
-  r.z = (perm_b32(w, w4, 0x0C060C02u) & m) | g;
-  r.w = (perm_b32(w, w4, 0x0C070C03u) & m) | g;
+  r.x = (perm_b32(w, w, 0x0C000C00u) & m) | g;
+  r.y = (perm_b32(w, w, 0x0C010C01u) & m) | g;
+  r.z = (perm_b32(w, w, 0x0C020C02u) & m) | g;
+  r.w = (perm_b32(w, w, 0x0C030C03u) & m) | g;
   return r;
 }
 TM_DEV uint32_t hmad_pair(uint32_t v, h2_t zz, h2_t ss) {
@@ -1033,17 +1034,16 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
                                              const uint8_t* __restrict__ W,
                                              uint16_t* __restrict__ Y, const uint16_t* S,
                                              const void* Z, int M, int N, int K) {
-  constexpr int CK = QB == 4 ? 64 : 32;  // k per chunk
+  constexpr int CK = QB == 4 ? 64 : 32;  // k per chunk and K-quarter
   constexpr int KS = CK / 16;            // MFMA k-steps per chunk
   constexpr int NS = QB == 4 ? 3 : 4;    // ring stages
-  constexpr int XRB = 2 * CK;            // X bytes per row per chunk
-  constexpr int XP = XRB / 16;           // 16-byte pieces per X row
-  constexpr int RPI = 1024 / XRB;        // X rows per 1 KB copy
+  constexpr int XRB = 8 * CK;            // X bytes per row per stage (4 quarters)
+  constexpr int XPQ = CK / 8;            // X pieces per row per quarter
   constexpr int XT = 64 * XRB;           // X tile bytes
-  constexpr int QT = XT + 128 * 32;      // X + weight tile per K-quarter
-  constexpr int ST = 4 * QT;             // stage bytes
-  constexpr int DX = 32 / RPI;           // X copies per wave per chunk
-  constexpr int D = DX + 2;              // copies per wave per chunk
+  constexpr int ST = XT + 128 * 128;     // stage: X tile, weight tile [128 rows][128 B]
+  constexpr int XLR = 64 / (XRB / 16);   // X rows per 1 KB copy
+  constexpr int DX = XT / 8192;          // X copies per wave per stage
+  constexpr int D = DX + 2;              // copies per wave per stage
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1057,18 +1057,18 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
   const int mb = j % mtl, nb = 8 * (j / mtl) + (blockIdx.x & 7);
   if (nb >= ntl) return;
   const int m0 = mb * 64, n0 = nb * 128;
-  const int KQ = K >> 2, NC = KQ / CK;
+  const int NC = K / (4 * CK);  // stages of 4 CK k
   const size_t wrow = QB == 4 ? (size_t)(K >> 1) : (size_t)K;
   const int ng = K >> 7;  // int4 groups per row
   const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_off(lds));
   const uint32_t sbase = lbase + NS * ST;  // int4 scales, then zero-points
   constexpr int ZRB = ZDT == 3 ? 1 : 2;    // zero-point bytes
 
-  // ---- int4 scales / zero-points of the 128 rows: contiguous blocks
+  // ---- int4 scales / zero-points of the 128 rows: contiguous blocks (lanes
+  // past the end of a block copy nothing: uint8 zero-point blocks are K bytes,
+  // a multiple of 512 only)
   if constexpr (QB == 4) {
     const int sb = 128 * ng * 2, zb = 128 * ng * ZRB;
-    // (lanes past the end of a block copy nothing: uint8 zero-point blocks
-    // are K bytes, a multiple of 512 only)
     for (int o = 1024 * wave; o < sb; o += 8192)
       if (o + 16 * lane < sb) dma16((const uint8_t*)(S + (size_t)n0 * ng) + o + 16 * lane, sbase + o);
     if constexpr (ZDT >= 0)
@@ -1077,52 +1077,56 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
           dma16((const uint8_t*)Z + (size_t)n0 * ng * ZRB + o + 16 * lane, sbase + sb + o);
   }
 
-  // ---- per-lane copy sources (chunk 0), destinations relative to a stage
+  // ---- copies of one stage (chunk c of every K-quarter: 4 CK consecutive k).
+  // Each copy moves whole lines: X rows of XRB bytes, weight rows of 128 B.
+  // X piece p of row r sits at slot p ^ (r & 15); weight piece p of row r at
+  // slot p ^ ((r >> 1) & 7).
   const uint8_t* xsrc[DX];
   uint32_t xdst[DX];
 #pragma unroll
   for (int i = 0; i < DX; ++i) {
-    const int rr = 32 * wn + RPI * i + lane / XP, sl = lane % XP;
-    const int p = sl ^ (QB == 4 ? (rr >> 1) & 7 : (rr >> 2) & 3);
-    xsrc[i] = (const uint8_t*)(X + (size_t)min(m0 + rr, M - 1) * K + kq * KQ + 8 * p);
-    xdst[i] = kq * QT + (32 * wn + RPI * i) * XRB;
+    const int rr = XLR * (DX * wave + i) + lane / (XRB / 16), sl = lane % (XRB / 16);
+    xsrc[i] = (const uint8_t*)(X + (size_t)min(m0 + rr, M - 1) * K) + 16 * (sl ^ (rr & 15));
+    xdst[i] = 1024 * (DX * wave + i);
   }
   const uint8_t* wsrc[2];
   uint32_t wdst[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int rr = 64 * wn + 32 * i + (lane >> 1);
-    const int p = (lane & 1) ^ ((rr >> 3) & 1);
-    wsrc[i] = W + (size_t)(n0 + rr) * wrow + (size_t)kq * KQ * QB / 8 + 16 * p;
-    wdst[i] = kq * QT + XT + (64 * wn + 32 * i) * 32;
+    const int rr = 8 * (2 * wave + i) + (lane >> 3), sl = lane & 7;
+    wsrc[i] = W + (size_t)(n0 + rr) * wrow + 16 * (sl ^ ((rr >> 1) & 7));
+    wdst[i] = XT + 1024 * (2 * wave + i);
   }
   auto issue = [&](int c) {
     const uint32_t st = lbase + (uint32_t)(c % NS) * ST;
 #pragma unroll
     for (int i = 0; i < DX; ++i) dma16(xsrc[i] + (size_t)c * XRB, st + xdst[i]);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dma16(wsrc[i] + (size_t)c * 32, st + wdst[i]);
+    for (int i = 0; i < 2; ++i) dma16(wsrc[i] + (size_t)c * 128, st + wdst[i]);
   };
 #pragma unroll
   for (int c = 0; c < NS - 1; ++c)
     if (c < NC) issue(c);
 
-  // ---- per-lane operand read offsets within a stage
+  // ---- per-lane operand read offsets within a stage: k-step s of lane half
+  // h reads X piece XPQ kq + g and weight group g, g = 4 h + s (int4) or
+  // 2 h + s (int8), of this wave's K-quarter
   uint32_t aoff[2][KS];
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const int row = 32 * mt + r32;
-      const int g = QB == 4 ? 4 * h + s : 2 * h + s;
-      const int sl = g ^ (QB == 4 ? (row >> 1) & 7 : (row >> 2) & 3);
-      aoff[mt][s] = kq * QT + row * XRB + 16 * sl;
+      const int pc = XPQ * kq + (QB == 4 ? 4 * h + s : 2 * h + s);
+      aoff[mt][s] = row * XRB + 16 * (pc ^ (row & 15));
     }
   uint32_t boff[2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-    boff[t] = kq * QT + XT + (64 * wn + 32 * t + r32) * 32 + 16 * (h ^ ((r32 >> 3) & 1));
-  const uint32_t vm = vgpr_const(0x00F000F0u), vg = vgpr_const(0x54005400u);
+  for (int t = 0; t < 2; ++t) {
+    const int row = 64 * wn + 32 * t + r32;
+    boff[t] = XT + row * 128 + 16 * ((2 * kq + h) ^ ((row >> 1) & 7));
+  }
+  const uint32_t vm = vgpr_const(0x00F0000Fu), vg = vgpr_const(0x54006400u);
 
   f16_t acc[2][2];
 #pragma unroll
@@ -1131,26 +1135,28 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
     for (int t = 0; t < 2; ++t) acc[mt][t] = f16_t{};
 
   for (int c = 0; c < NC; ++c) {
-    // this wave's copies of chunk c are complete once at most the copies of
-    // the later chunks already issued are outstanding
+    // this wave's copies of stage c are complete once at most the copies of
+    // the later stages already issued are outstanding
     const int later = min(NS - 2, NC - 1 - c);
     if (later >= 2) wait_vm<2 * D>();
     else if (later == 1) wait_vm<D>();
     else wait_vm<0>();
-    lds_barrier();  // all waves' copies of chunk c, and stage (c - 1) % NS is free
+    lds_barrier();  // all waves' copies of stage c, and stage (c - 1) % NS is free
     if (c + NS - 1 < NC) issue(c + NS - 1);
 
     const uint8_t* st = lds + (c % NS) * ST;
     u4_t braw[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) braw[t] = *(const u4_t*)(st + boff[t]);
-    // int4: this chunk's group (CK = 64: two chunks per group)
+    // int4: this chunk's group (k = (4 c + kq) CK; every chunk of a wave is
+    // in a group of its own); slow: some lane's zero-point has a fraction
     h2_t zz[2], ss[2];
     float zf[2], sf[2];
-    bool slow[2] = {false, false};
+    bool slow = false;
     if constexpr (QB == 4) {
-      const int gg = (kq * KQ + c * CK) >> 7;
+      const int gg = (4 * c + kq) >> 1;
       const uint8_t* sl = lds + NS * ST;
+      bool frac = false;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int gi = (64 * wn + 32 * t + r32) * ng + gg;
@@ -1159,36 +1165,45 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
         zf[t] = 0.0f;
         if constexpr (ZDT == 3) zf[t] = (float)(sl + 256 * ng)[gi];
         else if constexpr (ZDT >= 0) zf[t] = f16_bits_to_f32(((const uint16_t*)(sl + 256 * ng))[gi]);
-        const half_t zo = (half_t)(64.0f + zf[t]);
         if constexpr (ZDT == TM_DT_F16)
-          slow[t] = __builtin_amdgcn_ballot_w64((float)zo != 64.0f + zf[t]) != 0;
-        zz[t] = h2_t{-zo, -zo};
+          frac = frac || zf[t] != __builtin_rintf(zf[t]) || __builtin_fabsf(zf[t]) > 1000.0f;
+        // (1024 + z, 64 + z): exact for integral z, |z| <= 1000
+        zz[t] = h2_t{(half_t)(-1024.0f - zf[t]), (half_t)(-64.0f - zf[t])};
         const half_t sh = __builtin_bit_cast(half_t, sbits);
         ss[t] = h2_t{sh, sh};
       }
+      if constexpr (ZDT == TM_DT_F16) slow = __builtin_amdgcn_ballot_w64(frac) != 0;
     }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       u4_t a[2], b[2];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) a[mt] = *(const u4_t*)(st + aoff[mt][s]);
+      if constexpr (QB == 4) {
+        // one uniform branch per k-step that only chooses how the weight
+        // operands are made (the MFMAs below are shared)
+        if (slow) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if constexpr (QB == 4) {
-          const uint32_t wd = s == 0 ? braw[t].x : s == 1 ? braw[t].y : s == 2 ? braw[t].z : braw[t].w;
-          if (slow[t]) {
+          for (int t = 0; t < 2; ++t) {
+            const uint32_t wd = s == 0 ? braw[t].x : s == 1 ? braw[t].y : s == 2 ? braw[t].z : braw[t].w;
             b[t] = w4_exact(wd, zf[t], sf[t]);
-          } else {
-            const u4_t r = w4_nat64(wd, vm, vg);
+          }
+        } else {
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const uint32_t wd = s == 0 ? braw[t].x : s == 1 ? braw[t].y : s == 2 ? braw[t].z : braw[t].w;
+            const u4_t r = w4_nat(wd, vm, vg);
             b[t].x = hmad_pair(r.x, zz[t], ss[t]);
             b[t].y = hmad_pair(r.y, zz[t], ss[t]);
             b[t].z = hmad_pair(r.z, zz[t], ss[t]);
             b[t].w = hmad_pair(r.w, zz[t], ss[t]);
           }
-        } else {
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
           b[t] = s == 0 ? w8_operand<false>(braw[t].x, braw[t].y)
                         : w8_operand<false>(braw[t].z, braw[t].w);
-        }
       }
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
