@@ -103,6 +103,18 @@ int tm_int8_matmul(const void* input, const void* weight, void* output, const vo
 int tm_int4_matmul(const void* input, const void* weight, void* output, const void* scales,
                    const void* zeros, int M, int N, int K, int group_size, int act_dtype,
                    int scale_dtype, int zero_dtype, void* stream);
+/* Fused linear forms of the two: output[m, n] = (the sum above) + bias[n],
+ * the bias added to the fp32 sum before the output rounding, as
+ * make_fused_linear_kernel (_msl_templates.py:4013-4135) adds its bias to a
+ * dense product.  bias [N] in act_dtype; NULL gives the plain matmul.  The
+ * reference's quantized templates have no bias; these are the nn.Linear form
+ * of the same kernels. */
+int tm_int8_linear(const void* input, const void* weight, const void* bias, void* output,
+                   const void* scales, const void* zeros, int M, int N, int K, int act_dtype,
+                   int scale_dtype, int zero_dtype, void* stream);
+int tm_int4_linear(const void* input, const void* weight, const void* bias, void* output,
+                   const void* scales, const void* zeros, int M, int N, int K, int group_size,
+                   int act_dtype, int scale_dtype, int zero_dtype, void* stream);
 /* Dequantised weight tile out[n, k] = round_out((float(q) - z) * s), the
  * per-element arithmetic of _msl_templates.py:2671 (int8) / 2738-2739 (int4).
  * qbits 4 or 8; out_dtype F32/F16/BF16. */

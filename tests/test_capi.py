@@ -25,7 +25,8 @@ def declared_functions():
 def test_header_declares_entry_points():
     names = declared_functions()
     for n in ["tm_init", "tm_last_error", "tm_module_load", "tm_launch", "tm_int4_matmul",
-              "tm_int8_matmul", "tm_matmul", "tm_linear", "tm_wq_dequant"]:
+              "tm_int8_matmul", "tm_int4_linear", "tm_int8_linear", "tm_matmul", "tm_linear",
+              "tm_wq_dequant"]:
         assert n in names
 
 

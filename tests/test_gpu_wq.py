@@ -137,6 +137,60 @@ def test_int8_in_register_dequant_bit_exact(dev, kind):
     assert torch.equal(out.cpu().view(torch.int16), ref[:, ks].T.contiguous().view(torch.int16))
 
 
+# --- fused bias (nn.Linear form) on every kernel kind ------------------------------
+@pytest.mark.parametrize("kind", list(INT4_KINDS))
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int4_linear_bias(dev, kind, act):
+    G = 128
+    M, K, N = INT4_KINDS[kind]
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=40 + M, act=act)
+    bias = (torch.randn(N, generator=_gen(41)) * 4).to(act)
+    out = torch.empty(M, N, dtype=act, device=dev)
+    tm.int4_linear(x.to(dev), packed.to(dev), bias.to(dev), out, s.to(dev), z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    check_close(out.cpu(), ref + np32(bias)[None, :].astype(np.float64))
+    # without a bias the linear entry is the matmul, bit for bit
+    plain = torch.empty_like(out)
+    tm.int4_matmul(x.to(dev), packed.to(dev), plain, s.to(dev), z.to(dev), M, N, K, G)
+    tm.int4_linear(x.to(dev), packed.to(dev), None, out, s.to(dev), z.to(dev), M, N, K, G)
+    assert torch.equal(out.view(torch.int16), plain.view(torch.int16))
+
+
+@pytest.mark.parametrize("kind", list(INT8_KINDS))
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int8_linear_bias(dev, kind, act):
+    M, K, N = INT8_KINDS[kind]
+    x, w, s, _ = make_int8_problem(M, N, K, seed=50 + M, act=act)
+    bias = (torch.randn(N, generator=_gen(51)) * 4).to(act)
+    out = torch.empty(M, N, dtype=act, device=dev)
+    tm.int8_linear(x.to(dev), w.to(dev), bias.to(dev), out, s.to(dev), None, M, N, K)
+    ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), None, M, N, K)
+    check_close(out.cpu(), ref + np32(bias)[None, :].astype(np.float64))
+
+
+def test_int4_linear_fp32_general_kernel(dev):
+    """fp32 activations take the fp32 kernel; its bias is fp32 too."""
+    M, N, K, G = 3, 48, 256, 64
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=61, act=torch.float32)
+    bias = torch.randn(N, generator=_gen(62))
+    out = torch.empty(M, N, dtype=torch.float32, device=dev)
+    tm.int4_linear(x.to(dev), packed.to(dev), bias.to(dev), out, s.to(dev), z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    np.testing.assert_allclose(out.cpu().numpy(), ref + bias.numpy()[None, :], rtol=1e-4,
+                               atol=1e-4)
+
+
+def test_linear_bias_dtype_checked(dev):
+    x, q, packed, s, z = make_int4_problem(2, 64, 256, 128, seed=63)
+    out = torch.empty(2, 64, dtype=torch.float16, device=dev)
+    with pytest.raises(TypeError):
+        tm.int4_linear(x.to(dev), packed.to(dev), torch.zeros(64, device=dev), out, s.to(dev),
+                       z.to(dev), 2, 64, 256, 128)
+    with pytest.raises(ValueError):
+        tm.int4_linear(x.to(dev), packed.to(dev), torch.zeros(8, dtype=torch.float16, device=dev),
+                       out, s.to(dev), z.to(dev), 2, 64, 256, 128)
+
+
 # --- benchmark configurations (a column subset is checked against the oracle) ----
 def _cols(N, n=384, seed=0):
     return np.sort(np.random.default_rng(seed).choice(N, n, replace=False))

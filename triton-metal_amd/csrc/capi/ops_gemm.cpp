@@ -39,8 +39,10 @@ Kernel& kernel(const std::string& name) {
 }
 
 int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, const void* Z,
-              int M, int N, int K, int G, int adt, int sdt, int zdt, void* stream) {
-  const char* op = qbits == 4 ? "tm_int4_matmul" : "tm_int8_matmul";
+              int M, int N, int K, int G, int adt, int sdt, int zdt, const void* bias,
+              void* stream) {
+  const char* op = bias ? (qbits == 4 ? "tm_int4_linear" : "tm_int8_linear")
+                        : (qbits == 4 ? "tm_int4_matmul" : "tm_int8_matmul");
   if (M < 0 || N < 0 || K < 0) return fail(TM_ERR_INVALID_ARG, "%s: negative size", op);
   if (M == 0 || N == 0) return 0;
   if (!X || !W || !Y || !S) return fail(TM_ERR_INVALID_ARG, "%s: null buffer", op);
@@ -78,7 +80,7 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
       const int mtl = (M + 63) / 64, ntl = N / 128;
       const int grid = 8 * mtl * ((ntl + 7) / 8);
       return launch(kernel(name), dim3(grid), dim3(512), (unsigned)wl, stream, X, W, Y, S, Z, M,
-                    N, K);
+                    N, K, bias);
     }
   }
   // streaming kernel: 1 < M <= 64 (int4: 128), K-slices of 512 per wave (at
@@ -100,7 +102,7 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
                M <= 16 ? 's' : 'm');
       const int tiles = N / 16;
       return launch(kernel(name), dim3((tiles + nt - 1) / nt), dim3(64 * nwv), (unsigned)slds,
-                    stream, X, W, Y, S, Z, M, N, K);
+                    stream, X, W, Y, S, Z, M, N, K, bias);
     }
   }
   // exact-shape int4 GEMV: K = NW * PF * 128, G = 128
@@ -113,7 +115,7 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
       char name[64];
       snprintf(name, sizeof name, "wq_gemv4_%s_z%c_w8p%d", act, zc, pf);
       return launch(kernel(name), dim3(N / 16), dim3(512), (unsigned)glds, stream, X, W, Y, S,
-                    Z, M, N, K);
+                    Z, M, N, K, bias);
     }
   }
   size_t lds = (size_t)M * (K + 8) * 2 + (size_t)M * (K / 128) * 4;
@@ -122,18 +124,19 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
     const bool vs = qbits == 4 && G == 128 && K % 4096 == 0;
     snprintf(name, sizeof name, "wq_skinny_q%d_%s_z%c%s", qbits, act, zc, vs ? "_v" : "");
     return launch(kernel(name), dim3(N / 16), dim3(256), (unsigned)lds, stream, X, W, Y, S, Z, M,
-                  N, K, G);
+                  N, K, G, bias);
   }
   if (fast && K % 256 == 0 && N % 64 == 0) {
     char name[64];
     snprintf(name, sizeof name, "wq_tiled_q%d_%s_z%c", qbits, act, zc);
     int tiles = ((M + 63) / 64) * (N / 64);
     int grid = (tiles + 7) / 8 * 8;
-    return launch(kernel(name), dim3(grid), dim3(256), 0, stream, X, W, Y, S, Z, M, N, K, G);
+    return launch(kernel(name), dim3(grid), dim3(256), 0, stream, X, W, Y, S, Z, M, N, K, G,
+                  bias);
   }
   int Gg = qbits == 4 ? G : 1;
   return launch(kernel("wq_general"), dim3((N + 3) / 4), dim3(256), 0, stream, X,
-                (const uint8_t*)W, Y, S, Z, M, N, K, Gg, qbits, adt, sdt, zdt);
+                (const uint8_t*)W, Y, S, Z, M, N, K, Gg, qbits, adt, sdt, zdt, bias);
 }
 
 int dense(const void* A, const void* B, void* C, const void* bias, int M, int N, int K, int lda,
@@ -180,14 +183,28 @@ int tm_int8_matmul(const void* input, const void* weight, void* output, const vo
                    const void* zeros, int M, int N, int K, int act_dtype, int scale_dtype,
                    int zero_dtype, void* stream) {
   return wq_matmul(8, input, weight, output, scales, zeros, M, N, K, 1, act_dtype, scale_dtype,
-                   zero_dtype, stream);
+                   zero_dtype, nullptr, stream);
 }
 
 int tm_int4_matmul(const void* input, const void* weight, void* output, const void* scales,
                    const void* zeros, int M, int N, int K, int group_size, int act_dtype,
                    int scale_dtype, int zero_dtype, void* stream) {
   return wq_matmul(4, input, weight, output, scales, zeros, M, N, K, group_size, act_dtype,
-                   scale_dtype, zero_dtype, stream);
+                   scale_dtype, zero_dtype, nullptr, stream);
+}
+
+int tm_int8_linear(const void* input, const void* weight, const void* bias, void* output,
+                   const void* scales, const void* zeros, int M, int N, int K, int act_dtype,
+                   int scale_dtype, int zero_dtype, void* stream) {
+  return wq_matmul(8, input, weight, output, scales, zeros, M, N, K, 1, act_dtype, scale_dtype,
+                   zero_dtype, bias, stream);
+}
+
+int tm_int4_linear(const void* input, const void* weight, const void* bias, void* output,
+                   const void* scales, const void* zeros, int M, int N, int K, int group_size,
+                   int act_dtype, int scale_dtype, int zero_dtype, void* stream) {
+  return wq_matmul(4, input, weight, output, scales, zeros, M, N, K, group_size, act_dtype,
+                   scale_dtype, zero_dtype, bias, stream);
 }
 
 int tm_wq_dequant(const void* weight, const void* scales, const void* zeros, void* out, int N,

@@ -37,6 +37,10 @@
 //   wq_general   any shape / dtype: fp32 arithmetic exactly as the reference
 //                template, one wave per output column.
 //   wq_dequant   the dequantised weight tile round((float(q) - z) * s).
+// Every matmul kernel takes a trailing bias pointer (NULL: none) in the
+// activation dtype: Y[m, n] = round(acc + bias[n]), the fp32 epilogue of the
+// nn.Linear form X W^T + b (as make_fused_linear_kernel,
+// _msl_templates.py:4013-4135, adds its bias).
 #include "common.h"
 
 namespace {
@@ -186,6 +190,12 @@ template <bool BF16> TM_DEV float sum8(u4_t v) {
 // Sum over aligned groups of 16 lanes.
 TM_DEV float sum16(float v) { return row16_sum(v); }
 
+// bias[n] in the activation dtype (fp16 / bf16), 0 without a bias
+TM_DEV float bias_at(const uint16_t* bias, int n, bool bf16) {
+  if (!bias) return 0.0f;
+  return bf16 ? bf16_bits_to_f32(bias[n]) : f16_bits_to_f32(bias[n]);
+}
+
 TM_DEV void store_out(uint16_t* Y, size_t i, float v, bool bf16) {
   Y[i] = bf16 ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
 }
@@ -204,7 +214,7 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
                                                uint16_t* __restrict__ Y,
                                                const void* __restrict__ S,
                                                const void* __restrict__ Z, int M, int N, int K,
-                                               int G) {
+                                               int G, const uint16_t* bias) {
   extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8], then float xsum[M][K/128]
   __shared__ f4_t red[3][64];
   constexpr int CK = (QB == 4) ? 128 : 64;
@@ -376,7 +386,7 @@ __device__ __forceinline__ void wq_skinny_body(const uint16_t* __restrict__ X,
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       int row = 4 * q + e;
-      if (row < M) store_out(Y, (size_t)row * N + n, y[e], BF16);
+      if (row < M) store_out(Y, (size_t)row * N + n, y[e] + bias_at(bias, n, BF16), BF16);
     }
   }
 }
@@ -399,7 +409,8 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
                                               const uint8_t* __restrict__ W,
                                               uint16_t* __restrict__ Y,
                                               const uint16_t* __restrict__ S,
-                                              const void* __restrict__ Z, int M, int N, int K) {
+                                              const void* __restrict__ Z, int M, int N, int K,
+                                              const uint16_t* bias) {
   constexpr int NT = NW * 64;
   constexpr int SDT = BF16 ? TM_DT_BF16 : TM_DT_F16;
   extern __shared__ __align__(16) uint16_t xs[];
@@ -505,7 +516,7 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = 4 * q + e;
-      if (row < M) store_out(Y, (size_t)row * N + n, y[e], BF16);
+      if (row < M) store_out(Y, (size_t)row * N + n, y[e] + bias_at(bias, n, BF16), BF16);
     }
   }
 }
@@ -576,7 +587,8 @@ constexpr int stream_ahead(int rs, int nch, int c0, int c1, bool first, int i, b
 template <int QB, bool BF16, int SDT, int ZDT, int NT, int XR, bool MULTI>
 __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t* W,
                                                uint16_t* __restrict__ Y, const void* S,
-                                               const void* Z, int M, int N, int K) {
+                                               const void* Z, int M, int N, int K,
+                                               const uint16_t* bias) {
   constexpr int KS = 512;                 // k per wave
   constexpr int CK = QB == 4 ? 128 : 64;  // k per chunk: 64 weight bytes of a row
   constexpr int NCH = KS / CK;            // chunks per wave
@@ -789,7 +801,7 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
         for (int w2 = 0; w2 < nwv; ++w2) v += red[(w2 * 8 + f) * 64 + lane];
         const int F = 8 * r + f, t = F >> 2, e = F & 3;
         const int row = 16 * p + 4 * q + e, col = n0 + 16 * t + l16;
-        if (row < M && col < N) store_out(Y, (size_t)row * N + col, v, BF16);
+        if (row < M && col < N) store_out(Y, (size_t)row * N + col, v + bias_at(bias, col, BF16), BF16);
       }
     });
   };
@@ -813,7 +825,7 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
                                               uint16_t* __restrict__ Y,
                                               const void* __restrict__ S,
                                               const void* __restrict__ Z, int M, int N, int K,
-                                              int G) {
+                                              int G, const uint16_t* bias) {
   constexpr int BM = 64, KS = 256, LDX = KS + 8;
   __shared__ __align__(16) uint16_t xs[2][BM * LDX];
   __shared__ __align__(16) float xsm[2][2][BM];  // [buf][chunk][row]
@@ -963,7 +975,7 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
       int row = m0 + t * 16 + 4 * q + e;
       float v = y[t][e];
       if constexpr (QB == 8) v = sc * (v - z * xtot[t][e]);
-      if (row < M) store_out(Y, (size_t)row * N + n, v, BF16);
+      if (row < M) store_out(Y, (size_t)row * N + n, v + bias_at(bias, n, BF16), BF16);
     }
 }
 
@@ -1033,7 +1045,8 @@ template <int QB, int ZDT>
 __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
                                              const uint8_t* __restrict__ W,
                                              uint16_t* __restrict__ Y, const uint16_t* S,
-                                             const void* Z, int M, int N, int K) {
+                                             const void* Z, int M, int N, int K,
+                                             const uint16_t* bias) {
   constexpr int CK = QB == 4 ? 64 : 32;  // k per chunk and K-quarter
   constexpr int KS = CK / 16;            // MFMA k-steps per chunk
   constexpr int NS = QB == 4 ? 3 : 4;    // ring stages
@@ -1236,10 +1249,11 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
   const int col = n0 + 64 * wn + 32 * t + r32;
   float sc = 1.0f;
   if constexpr (QB == 8) sc = f16_bits_to_f32(S[col]);
+  const float bv = bias_at(bias, col, false);
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int row = m0 + 32 * mt + 8 * (e >> 2) + 4 * h + (e & 3);
-    if (row < M) Y[(size_t)row * N + col] = f32_to_f16_bits(y[e] * sc);
+    if (row < M) Y[(size_t)row * N + col] = f32_to_f16_bits(y[e] * sc + bv);
   }
 }
 
@@ -1259,7 +1273,7 @@ __device__ __forceinline__ void st_any(void* p, size_t i, int dt, float v) {
 extern "C" __global__ __launch_bounds__(256) void wq_general(
     const void* __restrict__ X, const uint8_t* __restrict__ W, void* __restrict__ Y,
     const void* __restrict__ S, const void* __restrict__ Z, int M, int N, int K, int G, int qbits,
-    int xdt, int sdt, int zdt) {
+    int xdt, int sdt, int zdt, const void* __restrict__ bias) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -1281,7 +1295,7 @@ extern "C" __global__ __launch_bounds__(256) void wq_general(
       acc += ld_scalar(X, (size_t)m * K + k, xdt) * w;
     }
     acc = wave_sum(acc);
-    if (lane == 0) st_any(Y, (size_t)m * N + n, xdt, acc);
+    if (lane == 0) st_any(Y, (size_t)m * N + n, xdt, acc + (bias ? ld_scalar(bias, n, xdt) : 0.0f));
   }
 }
 
@@ -1318,9 +1332,9 @@ extern "C" __global__ __launch_bounds__(256) void wq_dequant(
   extern "C" __global__ __launch_bounds__(256) TM_WQ_ATTR_##KIND void                           \
       wq_##KIND##_q##QB##_##ACT##_z##ZS##SUF(const uint16_t* X, const uint8_t* W, uint16_t* Y,   \
                                              const void* S, const void* Z, int M, int N, int K,  \
-                                             int G) {                                             \
+                                             int G, const uint16_t* bias) {                       \
     wq_##KIND##_body<QB, BF, (BF ? TM_DT_BF16 : TM_DT_F16), ZDT __VA_ARGS__>(X, W, Y, S, Z, M,   \
-                                                                              N, K, G);           \
+                                                                              N, K, G, bias);     \
   }
 // skinny: _v = vector scale loads (G == 128, K % 4096 == 0)
 #define TM_WQ_Z(KIND, QB, BF, ACT, SUF, ...)                                          \
@@ -1343,8 +1357,8 @@ TM_WQ_Z(tiled, 8, true, bf16, , )
 #define TM_WIDE(QB, ZS, ZDT)                                                                  \
   extern "C" __global__ __launch_bounds__(512) void wq_wide_q##QB##_f16_z##ZS(               \
       const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S, const void* Z,    \
-      int M, int N, int K) {                                                                  \
-    wq_wide_body<QB, ZDT>(X, W, Y, S, Z, M, N, K);                                            \
+      int M, int N, int K, const uint16_t* bias) {                                            \
+    wq_wide_body<QB, ZDT>(X, W, Y, S, Z, M, N, K, bias);                                      \
   }
 TM_WIDE(4, n, -1)
 TM_WIDE(4, s, TM_DT_F16)
@@ -1356,9 +1370,9 @@ TM_WIDE(8, n, -1)
 #define TM_STREAM(QB, BF, ACT, ZS, ZDT, NT, XR, MS, MULTI)                                     \
   extern "C" __global__ __launch_bounds__(512) void wq_stream_q##QB##_##ACT##_z##ZS##_x##XR##MS( \
       const uint16_t* X, const uint8_t* W, uint16_t* Y, const void* S, const void* Z, int M,    \
-      int N, int K) {                                                                          \
+      int N, int K, const uint16_t* bias) {                                                    \
     wq_stream_body<QB, BF, (BF ? TM_DT_BF16 : TM_DT_F16), ZDT, NT, XR, MULTI>(X, W, Y, S, Z, M, \
-                                                                              N, K);           \
+                                                                              N, K, bias);     \
   }
 #define TM_STREAM_V(QB, BF, ACT, ZS, ZDT, NT) \
   TM_STREAM(QB, BF, ACT, ZS, ZDT, NT, 8, s, false) \
@@ -1382,8 +1396,8 @@ TM_STREAM_Z(8, true, bf16, 3)
   __attribute__((amdgpu_waves_per_eu(NW == 8 && PF == 4 ? 8 : 1)))                             \
   void wq_gemv4_##ACT##_z##ZS##_w##NW##p##PF(                                                   \
       const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S, const void* Z, int M, \
-      int N, int K) {                                                                           \
-    wq_gemv4_body<BF, ZDT, NW, PF>(X, W, Y, S, Z, M, N, K);                                     \
+      int N, int K, const uint16_t* bias) {                                                     \
+    wq_gemv4_body<BF, ZDT, NW, PF>(X, W, Y, S, Z, M, N, K, bias);                               \
   }
 #define TM_GEMV4_Z(BF, ACT, NW, PF)                                   \
   TM_GEMV4(BF, ACT, n, -1, NW, PF)                                    \

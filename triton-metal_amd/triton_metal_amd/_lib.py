@@ -36,6 +36,8 @@ SIGNATURES = {
     "tm_synchronize": [vp],
     "tm_int8_matmul": [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp],
     "tm_int4_matmul": [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp],
+    "tm_int8_linear": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp],
+    "tm_int4_linear": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_wq_dequant": [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_matmul": [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_linear": [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp],

@@ -198,6 +198,48 @@ def int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size=128):
     return output
 
 
+def _linear_bias(base, bias, input, N, entry, what, stream):
+    """Rebind a validated weight-only matmul launch to its fused-bias entry."""
+    if bias is not None:
+        _device_of(input, bias)
+        _need_contig(bias, "bias")
+        if bias.dtype != input.dtype:
+            raise TypeError("bias dtype must equal input dtype")
+        _numel_at_least(bias, N, "bias")
+    a = base._args
+    return Launch(entry, (a[0], a[1], _ptr(bias)) + tuple(a[2:]), what, base.dev, stream)
+
+
+def plan_int8_linear(input, weight, bias, output, scales, zeros, M, N, K, stream=None) -> Launch:
+    """Validate and bind an int8_linear call (see int8_linear)."""
+    base = plan_int8_matmul(input, weight, output, scales, zeros, M, N, K, stream)
+    return _linear_bias(base, bias, input, N, _lib.lib().tm_int8_linear, "int8_linear", stream)
+
+
+def int8_linear(input, weight, bias, output, scales, zeros, M, N, K):
+    """int8_matmul in nn.Linear form: output = input @ dequant(weight)^T + bias[N].
+
+    The bias (input dtype, None for none) is added to the fp32 sum before the
+    output rounding, as make_fused_linear_kernel (_msl_templates.py:4013-4135)
+    adds its bias."""
+    _run(plan_int8_linear(input, weight, bias, output, scales, zeros, M, N, K))
+    return output
+
+
+def plan_int4_linear(input, weight, bias, output, scales, zeros, M, N, K, group_size=128,
+                     stream=None) -> Launch:
+    """Validate and bind an int4_linear call (see int4_linear)."""
+    base = plan_int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size, stream)
+    return _linear_bias(base, bias, input, N, _lib.lib().tm_int4_linear, "int4_linear", stream)
+
+
+def int4_linear(input, weight, bias, output, scales, zeros, M, N, K, group_size=128):
+    """int4_matmul in nn.Linear form: output = input @ dequant(weight)^T + bias[N]
+    (bias added in fp32 before the output rounding; None for none)."""
+    _run(plan_int4_linear(input, weight, bias, output, scales, zeros, M, N, K, group_size))
+    return output
+
+
 def wq_dequant(weight, scales, zeros, N, K, qbits, group_size=128, out_dtype=torch.float16,
                out=None):
     """Dequantised weight tile [N, K] = round((float(q) - z) * s) in out_dtype."""
