@@ -151,6 +151,34 @@ def kda(dev, B=1, H=16, T=8192, D=128, C=64):
                         "Dv": D, "chunk": C})
 
 
+def kda_decode(dev, B=16, H=16, D=128):
+    """One decoding step of KDA for B sequences x H heads (the token-by-token
+    form continuing from a state, updated in place); state sets rotated past
+    the Infinity Cache."""
+    import torch
+    import torch.nn.functional as F
+    import triton_metal_amd as tm
+    g = torch.Generator(device=dev).manual_seed(6)
+    per = 2 * B * H * D * D * 4
+    R = _nsets(per)
+    q = F.normalize(torch.randn(B, 1, H, D, device=dev, generator=g), dim=-1).bfloat16()
+    k = F.normalize(torch.randn(B, 1, H, D, device=dev, generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, 1, H, D, device=dev, generator=g).bfloat16()
+    beta = torch.sigmoid(torch.randn(B, 1, H, device=dev, generator=g))
+    gl = -F.softplus(torch.randn(B, 1, H, D, device=dev, generator=g))
+    o = torch.empty_like(v)
+    sts = [torch.randn(B, H, D, D, device=dev, generator=g) * 0.1 for _ in range(R)]
+    launches = [tm.plan_fused_recurrent_kda(q, k, v, gl, beta, o, initial_state=s, final_state=s)
+                for s in sts]
+    # state read + written (fp32), q, k, v, o bf16, g fp32, beta fp32
+    nbytes = 2 * B * H * D * D * 4 + 4 * B * H * D * 2 + B * H * D * 4 + B * H * 4
+    flops = B * H * 6 * D * D
+    return dict(launches=launches, keep=(q, k, v, beta, gl, o, sts), bytes=nbytes, flops=flops,
+                bound="hbm", dtype="fp32",
+                config={"workload": "kda_recurrent_decode", "B": B, "H": H, "T": 1, "Dk": D,
+                        "Dv": D, "state_sets_rotated": R})
+
+
 WORKLOADS = {
     "w4a16_m1": lambda d: w4a16(d, 1),
     "w4a16_m8": lambda d: w4a16(d, 8),
@@ -164,6 +192,7 @@ WORKLOADS = {
     "flash_causal": lambda d: flash(d, True),
     "flash_full": lambda d: flash(d, False),
     "kda": lambda d: kda(d),
+    "kda_decode": lambda d: kda_decode(d),
 }
 HEADLINE = "w4a16_m1"
 

@@ -174,6 +174,16 @@ int tm_kda_chunk_fwd(const void* q, const void* k, const void* v, const float* g
                      int batch, int seq_len, int heads, int key_dim, int value_dim,
                      int chunk_size, float scale, int beta_dtype, void* workspace,
                      size_t workspace_bytes, void* stream);
+/* The same rule token by token (the recurrent form; no counterpart in the
+ * reference either): for decoding one or a few tokens that continue from a
+ * state, e.g. the final_state of tm_kda_chunk_fwd.  Arguments as
+ * tm_kda_chunk_fwd without chunk size and workspace; the state lives in
+ * registers across the seq_len steps.  initial_state and final_state may be
+ * the same buffer (an in-place update).  key_dim = value_dim = 128. */
+int tm_kda_recurrent_fwd(const void* q, const void* k, const void* v, const float* g,
+                         const void* beta, const float* initial_state, void* o,
+                         float* final_state, int batch, int seq_len, int heads, int key_dim,
+                         int value_dim, float scale, int beta_dtype, void* stream);
 
 #if defined(__GNUC__)
 #pragma GCC visibility pop

@@ -172,3 +172,57 @@ def test_kda_config_c5_sampled_heads(dev):
         o_ref, st_ref = _ref(q[:, :, sl], k[:, :, sl], v[:, :, sl], g[:, :, sl], beta[:, :, sl])
         _close(o[:, :, sl], o_ref, f"o head {h}")
         _close(st[:, sl], st_ref, f"final state head {h}")
+
+
+# --- token-by-token (decoding) form -------------------------------------------------
+def _run_rec(dev, q, k, v, g, beta, s0=None, scale=None):
+    d = lambda t: None if t is None else t.to(dev)
+    o, st = tm.fused_recurrent_kda(d(q), d(k), d(v), d(g), d(beta), scale=scale,
+                                   initial_state=d(s0), output_final_state=True)
+    torch.cuda.synchronize()
+    return o.float().cpu().numpy(), st.cpu().numpy()
+
+
+@pytest.mark.parametrize("B,T,H", [(1, 1, 1), (2, 3, 3), (1, 40, 2), (4, 1, 16)])
+@pytest.mark.parametrize("beta_bf16", [False, True])
+def test_kda_recurrent_vs_recurrence(dev, B, T, H, beta_bf16):
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=70 + T + H, beta_bf16=beta_bf16)
+    s0 = torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(71)) * 0.5
+    o, st = _run_rec(dev, q, k, v, g, beta, s0=s0)
+    o_ref, st_ref = _ref(q, k, v, g, beta, s0=s0)
+    _close(o, o_ref, "o")
+    _close(st, st_ref, "final state")
+
+
+def test_kda_decode_continues_chunked_state(dev):
+    """Prefill 128 tokens with the chunked kernel, then decode 3 tokens one call
+    each, updating the state in place: outputs and state match one chunked pass
+    over all 131 tokens and the fp64 recurrence."""
+    B, T, H, P = 2, 131, 2, 128
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=72)
+    d = lambda t: t.to(dev).contiguous()
+    _, st = tm.chunk_kda(d(q[:, :P]), d(k[:, :P]), d(v[:, :P]), d(g[:, :P]), d(beta[:, :P]),
+                         output_final_state=True)
+    outs = []
+    for t in range(P, T):
+        sl = slice(t, t + 1)
+        o = torch.empty(B, 1, H, 128, dtype=torch.bfloat16, device=dev)
+        tm.plan_fused_recurrent_kda(d(q[:, sl]), d(k[:, sl]), d(v[:, sl]), d(g[:, sl]),
+                                    d(beta[:, sl]), o, initial_state=st, final_state=st)()
+        outs.append(o)
+    torch.cuda.synchronize()
+    o_dec = torch.cat(outs, 1).float().cpu().numpy()
+    o_ref, st_ref = _ref(q, k, v, g, beta)
+    _close(o_dec, o_ref[:, P:], "decoded o")
+    _close(st.cpu().numpy(), st_ref, "state after decoding")
+    o_all, st_all = _run(dev, q, k, v, g, beta)
+    _close(o_dec, o_all[:, P:], "decoded o vs chunked")
+
+
+def test_kda_recurrent_zero_steps_copies_state(dev):
+    B, H = 1, 2
+    q, k, v, g, beta = kda_inputs(B, 0, H, seed=73)
+    s0 = torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(74))
+    o, st = _run_rec(dev, q, k, v, g, beta, s0=s0)
+    assert o.shape == (B, 0, H, 128)
+    np.testing.assert_array_equal(st, s0.numpy())

@@ -1,4 +1,5 @@
-// Typed entry point for the KDA chunked forward (kda_intra + kda_state).
+// Typed entry points for KDA: the chunked forward (kda_intra + kda_state) and
+// the token-by-token recurrent form (kda_recurrent).
 #include <cmath>
 #include <cstring>
 
@@ -33,6 +34,10 @@ Kernel& intra_kernel() {
 }
 Kernel& state_kernel() {
   static Kernel k("kda_state");
+  return k;
+}
+Kernel& recurrent_kernel() {
+  static Kernel k("kda_recurrent");
   return k;
 }
 
@@ -96,4 +101,43 @@ extern "C" int tm_kda_chunk_fwd(const void* q, const void* k, const void* v, con
     if (rc) return rc;
   }
   return launch(state_kernel(), dim3((unsigned)(bh * (kValueDim / 16))), dim3(256), 0, stream, p);
+}
+
+extern "C" int tm_kda_recurrent_fwd(const void* q, const void* k, const void* v, const float* g,
+                                    const void* beta, const float* initial_state, void* o,
+                                    float* final_state, int batch, int seq_len, int heads,
+                                    int key_dim, int value_dim, float scale, int beta_dtype,
+                                    void* stream) {
+  if (batch < 0 || seq_len < 0 || heads < 0 || key_dim <= 0 || value_dim <= 0)
+    return fail(TM_ERR_INVALID_ARG, "tm_kda_recurrent_fwd: B=%d T=%d H=%d Dk=%d Dv=%d", batch,
+                seq_len, heads, key_dim, value_dim);
+  if (key_dim != kKeyDim || value_dim != kValueDim)
+    return fail(TM_ERR_UNSUPPORTED,
+                "tm_kda_recurrent_fwd: key_dim=%d value_dim=%d (supported: 128, 128)", key_dim,
+                value_dim);
+  if (beta_dtype != TM_DT_F32 && beta_dtype != TM_DT_BF16)
+    return fail(TM_ERR_INVALID_ARG, "tm_kda_recurrent_fwd: beta_dtype %d", beta_dtype);
+  if (!std::isfinite(scale)) return fail(TM_ERR_INVALID_ARG, "tm_kda_recurrent_fwd: scale");
+  if (batch == 0 || heads == 0) return 0;
+  if (seq_len > 0 && (!q || !k || !v || !g || !beta || !o))
+    return fail(TM_ERR_INVALID_ARG, "tm_kda_recurrent_fwd: null buffer");
+  if (seq_len == 0 && !final_state) return 0;
+  for (const void* ptr : {q, k, v, (const void*)g})
+    if (ptr && !aligned16(ptr))
+      return fail(TM_ERR_INVALID_ARG, "tm_kda_recurrent_fwd: q, k, v, g must be 16-byte aligned");
+  if ((long long)batch * seq_len * heads * kKeyDim > 0x7fffffffffffLL ||
+      (long long)batch * heads * (kValueDim / 16) > 0x7fffffffLL)
+    return fail(TM_ERR_UNSUPPORTED, "tm_kda_recurrent_fwd: problem too large");
+  if (!api()) return TM_ERR_NO_RUNTIME;
+  clear_error();
+  KdaParams p;
+  memset(&p, 0, sizeof p);
+  p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta;
+  p.s0 = initial_state; p.o = o; p.st = final_state;
+  p.B = batch; p.T = seq_len; p.H = heads;
+  p.scale = scale;
+  p.beta_bf16 = beta_dtype == TM_DT_BF16 ? 1 : 0;
+  // one wave per (head, 16 value columns)
+  return launch(recurrent_kernel(), dim3((unsigned)((long long)batch * heads * (kValueDim / 16))),
+                dim3(64), 0, stream, p);
 }

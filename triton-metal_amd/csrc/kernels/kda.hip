@@ -552,3 +552,64 @@ extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
       }
   }
 }
+
+// ----------------------------------------------------------------------------
+// kda_recurrent: the token-by-token form of the same rule (decode: one or a
+// few new tokens continuing from a state, e.g. the chunked kernel's final
+// state).  grid = B*H*(VD/16), block = 64 (one wave).  The wave owns value
+// columns v0 .. v0+15 of one head (64-byte pieces of each state row): lane
+// 16 rg + c holds S[32 rg + r][v0 + c] (r < 32) in registers for all steps,
+// so both reductions over the key dimension (S^T k and S^T q) are 32 in-lane
+// FMAs and two shuffles.
+// Per step t:  S <- diag(exp(g_t)) S;  u = beta_t (v_t - S^T k_t);
+//              S <- S + k_t u^T;       o_t = S^T (scale q_t).
+// ----------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(64) void kda_recurrent(KdaParams p) {
+  constexpr int CW = 16, RL = KD / (64 / CW);  // columns per wave, rows per lane
+  const int lane = threadIdx.x, c = lane & (CW - 1), rg = lane / CW;
+  const int vb = blockIdx.x % (VD / CW), bh = blockIdx.x / (VD / CW);
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int col = CW * vb + c, i0 = RL * rg;
+  const size_t sb = (size_t)bh * KD * VD;
+  float S[RL];
+#pragma unroll
+  for (int r = 0; r < RL; ++r) S[r] = p.s0 ? p.s0[sb + (size_t)(i0 + r) * VD + col] : 0.0f;
+  const long long rs = (long long)p.H * KD, rsv = (long long)p.H * VD;
+  for (int t = 0; t < p.T; ++t) {
+    const long long tk = ((long long)b * p.T + t) * rs + (long long)h * KD + i0;
+    const long long tv = ((long long)b * p.T + t) * rsv + (long long)h * VD;
+    float kf[RL], qf[RL], gd[RL];
+#pragma unroll
+    for (int j = 0; j < RL / 8; ++j) {
+      unpack8_bf16(ldg128(p.k + tk + 8 * j), kf + 8 * j);
+      unpack8_bf16(ldg128(p.q + tk + 8 * j), qf + 8 * j);
+      load8_f32(p.g + tk + 8 * j, gd + 8 * j);
+    }
+    const long long bi = ((long long)b * p.T + t) * p.H + h;
+    const float beta = p.beta_bf16 ? bf16_bits_to_f32(((const uint16_t*)p.beta)[bi])
+                                   : ((const float*)p.beta)[bi];
+    const float vj = bf16_bits_to_f32(p.v[tv + col]);
+    float dot = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RL; ++r) {
+      S[r] *= ex2(gd[r] * kLog2e);
+      dot = __builtin_fmaf(S[r], kf[r], dot);
+    }
+#pragma unroll
+    for (int o = CW; o < 64; o <<= 1) dot += __shfl_xor(dot, o, 64);
+    const float u = beta * (vj - dot);
+    float od = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RL; ++r) {
+      S[r] = __builtin_fmaf(kf[r], u, S[r]);
+      od = __builtin_fmaf(S[r], qf[r], od);
+    }
+#pragma unroll
+    for (int o = CW; o < 64; o <<= 1) od += __shfl_xor(od, o, 64);
+    if (rg == 0) p.o[tv + col] = f32_to_bf16_bits(od * p.scale);
+  }
+  if (p.st) {
+#pragma unroll
+    for (int r = 0; r < RL; ++r) p.st[sb + (size_t)(i0 + r) * VD + col] = S[r];
+  }
+}

@@ -46,6 +46,8 @@ SIGNATURES = {
     "tm_kda_workspace_size": [i32, i32, i32, i32, i32, i32],
     "tm_kda_chunk_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, C.c_float,
                          i32, vp, sz, vp],
+    "tm_kda_recurrent_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, C.c_float,
+                             i32, vp],
 }
 _RESTYPES = {
     "tm_last_error": C.c_char_p,

@@ -442,15 +442,9 @@ def kda_workspace_size(batch, seq_len, heads, key_dim=KDA_KEY_DIM, value_dim=KDA
                                                 chunk_size))
 
 
-def plan_chunk_kda(q, k, v, g, beta, o, scale=None, initial_state=None, final_state=None,
-                   workspace=None, chunk_size=KDA_CHUNK, stream=None) -> Launch:
-    """Validate and bind one KDA chunked forward.
-
-    q, k: bf16 [B, T, H, 128]; v, o: bf16 [B, T, H, 128]; g: fp32 [B, T, H, 128]
-    (log decay); beta: fp32 or bf16 [B, T, H]; initial_state / final_state:
-    fp32 [B, H, 128, 128] or None; workspace: a uint8 device tensor of at least
-    kda_workspace_size(B, T, H) bytes (allocated here when None)."""
-    dev = _device_of(q, k, v, g, beta, o, initial_state, final_state, workspace)
+def _kda_check(q, k, v, g, beta, o, initial_state, final_state, extra=None):
+    """Shared argument checks of the KDA operators; returns (dev, B, T, H, K, V)."""
+    dev = _device_of(q, k, v, g, beta, o, initial_state, final_state, extra)
     if q.dim() != 4 or k.shape != q.shape or g.shape != q.shape:
         raise ValueError(f"q, k, g must share a [B, T, H, K] shape: {q.shape} {k.shape} {g.shape}")
     B, T, H, Dk = q.shape
@@ -472,6 +466,19 @@ def plan_chunk_kda(q, k, v, g, beta, o, scale=None, initial_state=None, final_st
     for t, name in ((q, "q"), (k, "k"), (v, "v"), (g, "g"), (beta, "beta"), (o, "o"),
                     (initial_state, "initial_state"), (final_state, "final_state")):
         _need_contig(t, name)
+    return dev, B, T, H, Dk, Dv
+
+
+def plan_chunk_kda(q, k, v, g, beta, o, scale=None, initial_state=None, final_state=None,
+                   workspace=None, chunk_size=KDA_CHUNK, stream=None) -> Launch:
+    """Validate and bind one KDA chunked forward.
+
+    q, k: bf16 [B, T, H, 128]; v, o: bf16 [B, T, H, 128]; g: fp32 [B, T, H, 128]
+    (log decay); beta: fp32 or bf16 [B, T, H]; initial_state / final_state:
+    fp32 [B, H, 128, 128] or None; workspace: a uint8 device tensor of at least
+    kda_workspace_size(B, T, H) bytes (allocated here when None)."""
+    dev, B, T, H, Dk, Dv = _kda_check(q, k, v, g, beta, o, initial_state, final_state,
+                                      workspace)
     need = _lib.lib().tm_kda_workspace_size(B, T, H, Dk, Dv, chunk_size)
     if need == 0 and B * T * H > 0:
         raise ValueError(f"unsupported KDA shape: key_dim={Dk} value_dim={Dv} "
@@ -490,6 +497,39 @@ def plan_chunk_kda(q, k, v, g, beta, o, scale=None, initial_state=None, final_st
     launch = Launch(_lib.lib().tm_kda_chunk_fwd, args, "kda_chunk_fwd", dev, stream)
     launch._keep = workspace
     return launch
+
+
+def plan_fused_recurrent_kda(q, k, v, g, beta, o, scale=None, initial_state=None,
+                             final_state=None, stream=None) -> Launch:
+    """Validate and bind one token-by-token KDA forward (see fused_recurrent_kda).
+    Tensors as plan_chunk_kda; no workspace.  initial_state and final_state
+    may be the same tensor (in-place state update)."""
+    dev, B, T, H, Dk, Dv = _kda_check(q, k, v, g, beta, o, initial_state, final_state)
+    if (Dk, Dv) != (128, 128) and B * H > 0:
+        raise ValueError(f"unsupported KDA shape: key_dim={Dk} value_dim={Dv} (supported: 128, 128)")
+    if scale is None:
+        scale = Dk ** -0.5
+    bdt = TM_DT_BF16 if beta.dtype == torch.bfloat16 else TM_DT_F32
+    args = (_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(initial_state), _ptr(o),
+            _ptr(final_state), B, T, H, Dk, Dv, float(scale), bdt)
+    return Launch(_lib.lib().tm_kda_recurrent_fwd, args, "kda_recurrent_fwd", dev, stream)
+
+
+def fused_recurrent_kda(q, k, v, g, beta, scale=None, initial_state=None,
+                        output_final_state=False):
+    """Kimi Delta Attention, token by token, in the calling convention of the
+    published ``fused_recurrent_kda`` operator (the decoding counterpart of
+    chunk_kda): same tensors, same rule, one step per token.
+
+    Returns (o [B, T, H, V] bf16, final_state fp32 [B, H, K, V] or None)."""
+    B, T, H, Dk = q.shape
+    Dv = v.shape[-1]
+    o = torch.empty(B, T, H, Dv, dtype=torch.bfloat16, device=q.device)
+    st = (torch.empty(B, H, Dk, Dv, dtype=torch.float32, device=q.device)
+          if output_final_state else None)
+    _run(plan_fused_recurrent_kda(q, k, v, g, beta, o, scale=scale, initial_state=initial_state,
+                                  final_state=st))
+    return o, st
 
 
 def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
