@@ -122,6 +122,28 @@ int tm_wq_dequant(const void* weight, const void* scales, const void* zeros, voi
                   int K, int group_size, int qbits, int scale_dtype, int zero_dtype,
                   int out_dtype, void* stream);
 
+/* int4 checkpoints in the GPTQ and AWQ on-disk formats -> the int4 layout of
+ * tm_int4_matmul (weight [N, K/2] bytes, even k in the low nibble, as
+ * make_int4_matmul_kernel's layout, _msl_templates.py:2687-2697; scales /
+ * zeros [N, ceil(K/group_size)]).  No counterpart in the reference, which
+ * takes that layout as given; these load real checkpoints into it.
+ *   GPTQ: qweight int32 [K/8, N] (nibble i of word (j, n) = q[n, 8j+i]);
+ *         qzeros int32 [ngroups, N/8] (nibble i of word (g, b) =
+ *         z[8b+i, g] - zero_offset: 1 for the original format, 0 for v2).
+ *   AWQ:  qweight int32 [K, N/8] (nibble p of word (k, b) = q[8b + ORDER[p],
+ *         k], ORDER = 0 2 4 6 1 3 5 7); qzeros [ngroups, N/8] the same way.
+ *   scales: 16-bit [ngroups, N] (fp16 as stored) -> [N, ngroups].
+ * weight_out: N*K/2 bytes; zeros_out: uint8 [N, ngroups]; scales_out: 16-bit
+ * [N, ngroups].  qzeros / scales may be NULL together with their output.
+ * N and K multiples of 8; act-order (g_idx) checkpoints are not representable
+ * in this layout and are rejected by the Python layer. */
+int tm_wq_repack_gptq(const void* qweight, const void* qzeros, const void* scales, int N, int K,
+                      int group_size, int zero_offset, void* weight_out, void* scales_out,
+                      void* zeros_out, void* stream);
+int tm_wq_repack_awq(const void* qweight, const void* qzeros, const void* scales, int N, int K,
+                     int group_size, void* weight_out, void* scales_out, void* zeros_out,
+                     void* stream);
+
 /* ---- dense matmul -----------------------------------------------------------
  * C[M, N] = A[M, K] @ B[K, N], row-major with leading dimensions lda/ldb/ldc
  * (elements).  Replaces make_matmul_kernel (_msl_templates.py:447-585; buffer

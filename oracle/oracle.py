@@ -34,6 +34,12 @@ PINNING = {
                      "agreement with kda_chunked (parity unpinned by the reference)",
     "kda_chunked": "agreement with kda_recurrent; same closed forms (parity unpinned by "
                    "the reference)",
+    "pack_gptq": "round trip with the shift-table unpacking of the published format; "
+                 "dequant equivalence through gptq_to_ref (format not in the reference)",
+    "pack_awq": "inverse of the published reverse-order unpacking; identity-column word "
+                "0x75316420; dequant equivalence through awq_to_ref",
+    "gptq_to_ref": "dequant_int4 of the result equals (q - z) s of the unpacked checkpoint",
+    "awq_to_ref": "dequant_int4 of the result equals (q - z) s of the unpacked checkpoint",
 }
 
 
@@ -230,3 +236,70 @@ def kda_chunked(q, k, v, g, beta, scale=None, initial_state=None, chunk_size=64)
                 St = eG[-1][:, None] * St + (kc * np.exp(G[-1][None, :] - G)).T @ U
             S[b, h] = St
     return o, S
+
+
+# ---------------------------------------------------------------------------
+# On-disk int4 checkpoint formats -> the int4 layout of the reference template
+# (W [N, K/2] bytes, even k in the low nibble; scales / zeros [N, K/G]:
+# _msl_templates.py:2687-2697).  The formats themselves are not in the
+# reference; they are restated from their published definitions:
+#   GPTQ (AutoGPTQ checkpoints): qweight int32 [K/8, N], nibble i of word
+#     (j, n) = q[n, 8 j + i]; qzeros int32 [K/G, N/8], nibble i of word (g, b)
+#     = z[8 b + i, g] - zero_offset (1 in the original format, which stores
+#     zero-points minus one; 0 in its "v2" variant); scales fp16 [K/G, N].
+#   AWQ (AutoAWQ GEMM checkpoints): qweight int32 [K, N/8], nibble p of word
+#     (k, b) = q[8 b + AWQ_ORDER[p], k]; qzeros int32 [K/G, N/8] in the same
+#     order (no offset); scales fp16 [K/G, N].
+# ---------------------------------------------------------------------------
+AWQ_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def _pack_nibbles(vals: np.ndarray) -> np.ndarray:
+    """[..., 8] values 0..15 -> uint32 words, value i in nibble i."""
+    v = np.asarray(vals, np.uint32) & 0xF
+    return (v << (4 * np.arange(8, dtype=np.uint32))).sum(axis=-1, dtype=np.uint64).astype(
+        np.uint32)
+
+
+def pack_gptq(q: np.ndarray, zeros: np.ndarray, zero_offset: int = 1):
+    """q uint8 [N, K] (0..15), zeros int [N, ng] -> (qweight int32 [K/8, N],
+    qzeros int32 [ng, N/8])."""
+    N, K = q.shape
+    qw = _pack_nibbles(np.asarray(q).T.reshape(K // 8, 8, N).transpose(0, 2, 1))
+    zs = (np.asarray(zeros, np.int64).T - zero_offset) & 0xF          # [ng, N]
+    qz = _pack_nibbles(zs.reshape(zs.shape[0], N // 8, 8))
+    return np.ascontiguousarray(qw).view(np.int32), np.ascontiguousarray(qz).view(np.int32)
+
+
+def pack_awq(q: np.ndarray, zeros: np.ndarray):
+    """q uint8 [N, K], zeros int [N, ng] -> (qweight int32 [K, N/8],
+    qzeros int32 [ng, N/8]) in the AWQ column order."""
+    N, K = q.shape
+    order = np.array(AWQ_ORDER)
+    qt = np.asarray(q).T.reshape(K, N // 8, 8)[:, :, order]           # nibble p <- col ORDER[p]
+    zt = np.asarray(zeros, np.int64).T.reshape(-1, N // 8, 8)[:, :, order]
+    return (np.ascontiguousarray(_pack_nibbles(qt)).view(np.int32),
+            np.ascontiguousarray(_pack_nibbles(zt)).view(np.int32))
+
+
+def _unpack_words(w: np.ndarray) -> np.ndarray:
+    u = np.asarray(w).view(np.uint32)
+    return ((u[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).astype(np.uint8)
+
+
+def gptq_to_ref(qweight, qzeros, scales, N: int, K: int, group_size: int, zero_offset: int = 1):
+    """GPTQ checkpoint -> (packed [N, K/2] uint8, scales [N, ng] as given, zeros
+    [N, ng] as integers), the reference int4 layout."""
+    q = _unpack_words(qweight).transpose(0, 2, 1).reshape(K, N).T        # [N, K]
+    ng = (K + group_size - 1) // group_size
+    z = _unpack_words(qzeros).reshape(ng, N).T.astype(np.int64) + zero_offset
+    return pack_int4(q), np.asarray(scales).T.copy(), z
+
+
+def awq_to_ref(qweight, qzeros, scales, N: int, K: int, group_size: int):
+    """AWQ checkpoint -> (packed [N, K/2] uint8, scales [N, ng], zeros [N, ng])."""
+    inv = np.argsort(AWQ_ORDER)                                         # column i at nibble inv[i]
+    q = _unpack_words(qweight)[:, :, inv].reshape(K, N).T
+    ng = (K + group_size - 1) // group_size
+    z = _unpack_words(qzeros)[:, :, inv].reshape(ng, N).T.astype(np.int64)
+    return pack_int4(q), np.asarray(scales).T.copy(), z

@@ -358,3 +358,58 @@ def test_empty_and_errors(dev):
         tm.int4_matmul(x.float(), w, out, s, None, 0, 64, 512, 128)
     with pytest.raises(ValueError):
         tm.int4_matmul(x.cpu(), w, out, s, None, 0, 64, 512, 128)
+
+
+# --- GPTQ / AWQ checkpoints into the int4 layout -------------------------------------
+@pytest.mark.parametrize("fmt", ["gptq", "gptq_v2", "awq"])
+@pytest.mark.parametrize("N,K,G", [(64, 256, 128), (1000, 520, 8), (512, 4096, 128)])
+def test_checkpoint_repack_bit_exact(dev, fmt, N, K, G):
+    rng = np.random.default_rng(N + K)
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    ng = (K + G - 1) // G
+    z = rng.integers(1, 16, size=(N, ng))
+    s = (rng.random((ng, N)) * 0.02 + 0.001).astype(np.float16)
+    if fmt == "awq":
+        qw, qz = oracle.pack_awq(q, z)
+        ref = oracle.awq_to_ref(qw, qz, s, N, K, G)
+        got = tm.from_awq(torch.from_numpy(qw).to(dev), torch.from_numpy(qz).to(dev),
+                          torch.from_numpy(s).to(dev), group_size=G)
+    else:
+        off = 1 if fmt == "gptq" else 0
+        qw, qz = oracle.pack_gptq(q, z, zero_offset=off)
+        ref = oracle.gptq_to_ref(qw, qz, s, N, K, G, zero_offset=off)
+        got = tm.from_gptq(torch.from_numpy(qw).to(dev), torch.from_numpy(qz).to(dev),
+                           torch.from_numpy(s).to(dev), group_size=G, zero_offset=off)
+    torch.cuda.synchronize()
+    assert np.array_equal(got[0].cpu().numpy(), ref[0])
+    assert np.array_equal(got[1].cpu().numpy(), ref[1])
+    assert np.array_equal(got[2].cpu().numpy().astype(np.int64), ref[2])
+
+
+def test_gptq_checkpoint_through_the_gemv(dev):
+    """A GPTQ checkpoint loaded with from_gptq runs through the M = 1 GEMV and
+    matches (q - z) s of the checkpoint."""
+    N, K, G, M = 256, 4096, 128, 1
+    rng = np.random.default_rng(5)
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    z = rng.integers(1, 16, size=(N, K // G))
+    s = (rng.random((K // G, N)) * 0.019 + 0.001).astype(np.float16)
+    qw, qz = oracle.pack_gptq(q, z, zero_offset=1)
+    w, sc, zz = tm.from_gptq(torch.from_numpy(qw).to(dev), torch.from_numpy(qz).to(dev),
+                             torch.from_numpy(s).to(dev), group_size=G)
+    x = torch.randn(M, K, generator=_gen(6)).half()
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int4_matmul(x.to(dev), w, out, sc, zz, M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), oracle.pack_int4(q), s.T.astype(np.float32),
+                             z.astype(np.float32), M, N, K, G)
+    check_close(out.cpu(), ref)
+
+
+def test_act_order_checkpoint_rejected(dev):
+    N, K, G = 64, 256, 128
+    qw = torch.zeros(K // 8, N, dtype=torch.int32, device=dev)
+    s = torch.ones(K // G, N, dtype=torch.float16, device=dev)
+    trivial = torch.arange(K, dtype=torch.int32, device=dev) // G
+    tm.from_gptq(qw, None, s, group_size=G, g_idx=trivial)
+    with pytest.raises(ValueError):
+        tm.from_gptq(qw, None, s, group_size=G, g_idx=trivial.flip(0))

@@ -117,3 +117,80 @@ def test_planted_swapped_nibbles_fail_kat(kats):
         return out
     assert _kat_error(kats, "int4_seed44", oracle.unpack_int4) < 1e-6
     assert _kat_error(kats, "int4_seed44", swapped) > 0.1
+
+
+# --- GPTQ / AWQ checkpoint formats (restated; not in the reference) ------------------
+# Second, independent formulations of the published unpacking, written the way
+# the formats' own loaders state it (a shift table over the packed axis; for
+# AWQ a reverse-order column gather), so that a wrong nibble order, axis or
+# offset in the oracle's packers fails here.
+def _gptq_unpack_shift_table(qweight, K, N):
+    wf = np.arange(0, 32, 4, dtype=np.uint32)                    # [8]
+    u = qweight.view(np.uint32)                                  # [K/8, N]
+    t = (u[:, None, :] >> wf[None, :, None]) & 0xF               # [K/8, 8, N]
+    return t.reshape(K, N).astype(np.uint8)                      # q^T [K, N]
+
+
+def _awq_unpack_reverse_order(qweight, K, N):
+    rev = [0, 4, 1, 5, 2, 6, 3, 7]
+    u = qweight.view(np.uint32)                                  # [K, N/8]
+    t = (u[:, :, None] >> np.arange(0, 32, 4, dtype=np.uint32)) & 0xF   # [K, N/8, 8] nibble order
+    return t[:, :, rev].reshape(K, N).astype(np.uint8)           # q^T [K, N]
+
+
+def _problem(seed, N=32, K=64, G=16, zlo=0):
+    rng = np.random.default_rng(seed)
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    z = rng.integers(zlo, 16, size=(N, K // G))
+    s = (rng.random((K // G, N)) * 0.02 + 0.001).astype(np.float16)
+    return q, z, s
+
+
+def test_gptq_pack_matches_shift_table_unpacking():
+    q, z, _ = _problem(1, zlo=1)
+    qw, qz = oracle.pack_gptq(q, z, zero_offset=1)
+    assert qw.shape == (64 // 8, 32) and qz.shape == (4, 32 // 8)
+    assert np.array_equal(_gptq_unpack_shift_table(qw, 64, 32), q.T)
+    zt = ((qz.view(np.uint32)[:, :, None] >> np.arange(0, 32, 4, dtype=np.uint32)) & 0xF)
+    assert np.array_equal(zt.reshape(4, 32).T + 1, z)           # stored minus one
+
+
+def test_awq_pack_matches_reverse_order_unpacking():
+    q, z, _ = _problem(2)
+    qw, qz = oracle.pack_awq(q, z)
+    assert qw.shape == (64, 32 // 8)
+    assert np.array_equal(_awq_unpack_reverse_order(qw, 64, 32), q.T)
+    assert np.array_equal(_awq_unpack_reverse_order(qz, 4, 32), z.T)
+    # columns 0..7 holding their own index pack to the format's signature word
+    ident = np.repeat(np.arange(8, dtype=np.uint8)[:, None], 8, axis=1)
+    w, _ = oracle.pack_awq(ident, np.zeros((8, 1), int))
+    assert int(w.view(np.uint32)[0, 0]) == 0x75316420
+
+
+@pytest.mark.parametrize("fmt", ["gptq", "gptq_v2", "awq"])
+def test_checkpoint_to_ref_preserves_dequant(fmt):
+    N, K, G = 32, 64, 16
+    q, z, s = _problem(3, N, K, G, zlo=1)
+    if fmt == "awq":
+        qw, qz = oracle.pack_awq(q, z)
+        packed, s_ref, z_ref = oracle.awq_to_ref(qw, qz, s, N, K, G)
+        qt = _awq_unpack_reverse_order(qw, K, N)
+    else:
+        off = 1 if fmt == "gptq" else 0
+        qw, qz = oracle.pack_gptq(q, z, zero_offset=off)
+        packed, s_ref, z_ref = oracle.gptq_to_ref(qw, qz, s, N, K, G, zero_offset=off)
+        qt = _gptq_unpack_shift_table(qw, K, N)
+    # dequant through the reference layout == (q - z) s of the checkpoint
+    got = oracle.dequant_int4(packed, s_ref.astype(np.float32), z_ref.astype(np.float32), K, G)
+    gi = np.arange(K) // G
+    want = (qt.T.astype(np.float32) - z[:, gi]) * s.T.astype(np.float32)[:, gi]
+    np.testing.assert_array_equal(got, want)
+
+
+def test_gptq_original_format_cannot_hold_zero_point_zero():
+    # the original format stores z - 1 in 4 bits: z = 0 wraps to 16 (a property
+    # of the format the conversion reproduces, not a conversion error)
+    q = np.zeros((8, 8), np.uint8)
+    qw, qz = oracle.pack_gptq(q, np.zeros((8, 1), int), zero_offset=1)
+    _, _, z = oracle.gptq_to_ref(qw, qz, np.ones((1, 8)), 8, 8, 8, zero_offset=1)
+    assert (z == 16).all()

@@ -207,6 +207,57 @@ int tm_int4_linear(const void* input, const void* weight, const void* bias, void
                    scale_dtype, zero_dtype, bias, stream);
 }
 
+namespace {
+// GPTQ / AWQ int4 checkpoints -> the int4 layout of tm_int4_matmul.
+int repack(bool awq, const void* qweight, const void* qzeros, const void* scales, int N, int K,
+           int group_size, int zero_offset, void* weight_out, void* scales_out, void* zeros_out,
+           void* stream) {
+  const char* op = awq ? "tm_wq_repack_awq" : "tm_wq_repack_gptq";
+  if (N < 0 || K < 0 || group_size <= 0 || K % 8 || N % 8)
+    return fail(TM_ERR_INVALID_ARG, "%s: N=%d K=%d group_size=%d (N, K multiples of 8)", op, N,
+                K, group_size);
+  if (!qweight || !weight_out) return fail(TM_ERR_INVALID_ARG, "%s: null weight buffer", op);
+  if ((qzeros != nullptr) != (zeros_out != nullptr) ||
+      (scales != nullptr) != (scales_out != nullptr))
+    return fail(TM_ERR_INVALID_ARG, "%s: zeros / scales given without their output", op);
+  if (zero_offset < 0 || zero_offset > 240)
+    return fail(TM_ERR_INVALID_ARG, "%s: zero_offset=%d", op, zero_offset);
+  if (N == 0 || K == 0) return 0;
+  if (!api()) return TM_ERR_NO_RUNTIME;
+  clear_error();
+  static Kernel kg("wq_repack_gptq_weight"), ka("wq_repack_awq_weight"), kz("wq_repack_zeros"),
+      kt("wq_transpose16");
+  const int ng = (K + group_size - 1) / group_size;
+  int rc = launch(awq ? ka : kg, dim3((N + 63) / 64, (K / 8 + 63) / 64), dim3(256), 0, stream,
+                  qweight, weight_out, N, K);
+  if (rc) return rc;
+  if (qzeros) {
+    const long long total = (long long)N * ng;
+    rc = launch(kz, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, qzeros,
+                zeros_out, N, ng, awq ? 1 : 0, zero_offset);
+    if (rc) return rc;
+  }
+  if (scales)
+    rc = launch(kt, dim3((N + 63) / 64, (ng + 63) / 64), dim3(256), 0, stream, scales, scales_out,
+                ng, N);
+  return rc;
+}
+}  // namespace
+
+int tm_wq_repack_gptq(const void* qweight, const void* qzeros, const void* scales, int N, int K,
+                      int group_size, int zero_offset, void* weight_out, void* scales_out,
+                      void* zeros_out, void* stream) {
+  return repack(false, qweight, qzeros, scales, N, K, group_size, zero_offset, weight_out,
+                scales_out, zeros_out, stream);
+}
+
+int tm_wq_repack_awq(const void* qweight, const void* qzeros, const void* scales, int N, int K,
+                     int group_size, void* weight_out, void* scales_out, void* zeros_out,
+                     void* stream) {
+  return repack(true, qweight, qzeros, scales, N, K, group_size, 0, weight_out, scales_out,
+                zeros_out, stream);
+}
+
 int tm_wq_dequant(const void* weight, const void* scales, const void* zeros, void* out, int N,
                   int K, int group_size, int qbits, int scale_dtype, int zero_dtype,
                   int out_dtype, void* stream) {

@@ -24,6 +24,8 @@ from .ops import (
     plan_int8_linear,
     plan_int8_matmul,
     plan_matmul,
+    from_awq,
+    from_gptq,
     fused_linear,
     int4_linear,
     int4_matmul,
@@ -41,7 +43,7 @@ from .ops import (
 __all__ = [
     "errors", "HipLaunchError", "KernelLoadError", "NativeLibraryMissing", "NoDeviceError",
     "Kernel", "Launch", "attention", "chunk_kda", "fused_recurrent_kda", "kda_workspace_size", "plan_chunk_kda", "plan_fused_recurrent_kda", "flash_attention", "flash_attn_fwd",
-    "make_flash_attention_kernel", "plan_flash_attention", "plan_int4_linear", "plan_int4_matmul", "plan_int8_linear", "plan_int8_matmul", "plan_matmul", "fused_linear", "int4_linear", "int4_matmul", "int8_linear", "int8_matmul", "make_fused_linear_kernel",
+    "make_flash_attention_kernel", "plan_flash_attention", "plan_int4_linear", "plan_int4_matmul", "plan_int8_linear", "plan_int8_matmul", "plan_matmul", "from_awq", "from_gptq", "fused_linear", "int4_linear", "int4_matmul", "int8_linear", "int8_matmul", "make_fused_linear_kernel",
     "make_int4_matmul_kernel", "make_int8_matmul_kernel", "make_matmul_kernel",
     "make_simdgroup_matmul_kernel", "matmul", "wq_dequant",
 ]

@@ -39,6 +39,8 @@ SIGNATURES = {
     "tm_int8_linear": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp],
     "tm_int4_linear": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_wq_dequant": [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp],
+    "tm_wq_repack_gptq": [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp],
+    "tm_wq_repack_awq": [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp],
     "tm_matmul": [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_linear": [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp],
     "tm_flash_attention": [vp, vp, vp, vp, vp, i32, i32, i32, i32, C.POINTER(C.c_longlong),

@@ -253,6 +253,60 @@ def wq_dequant(weight, scales, zeros, N, K, qbits, group_size=128, out_dtype=tor
     return out
 
 
+def _repack(awq, qweight, qzeros, scales, group_size, zero_offset, g_idx):
+    if qweight.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"qweight must be int32, got {qweight.dtype}")
+    if awq:
+        K, N = qweight.shape[0], qweight.shape[1] * 8
+    else:
+        K, N = qweight.shape[0] * 8, qweight.shape[1]
+    ng = (K + group_size - 1) // group_size
+    if g_idx is not None:
+        want = torch.arange(K, device=g_idx.device, dtype=g_idx.dtype) // group_size
+        if g_idx.numel() != K or not torch.equal(g_idx, want):
+            raise ValueError("act-order checkpoints (a g_idx other than k // group_size) have no "
+                             "equivalent in the [N, K/2] layout")
+    dev = _device_of(qweight, qzeros, scales)
+    for t, w in ((qweight, "qweight"), (qzeros, "qzeros"), (scales, "scales")):
+        _need_contig(t, w)
+    if qzeros is not None and (qzeros.dtype not in (torch.int32, torch.uint32)
+                               or tuple(qzeros.shape) != (ng, N // 8)):
+        raise ValueError(f"qzeros must be int32 [{ng}, {N // 8}], got {qzeros.dtype} "
+                         f"{tuple(qzeros.shape)}")
+    if scales is not None and (scales.element_size() != 2 or tuple(scales.shape) != (ng, N)):
+        raise ValueError(f"scales must be 16-bit [{ng}, {N}], got {scales.dtype} "
+                         f"{tuple(scales.shape)}")
+    weight = torch.empty(N, K // 2, dtype=torch.uint8, device=dev)
+    s_out = None if scales is None else torch.empty(N, ng, dtype=scales.dtype, device=dev)
+    z_out = None if qzeros is None else torch.empty(N, ng, dtype=torch.uint8, device=dev)
+    L = _lib.lib()
+    if awq:
+        args = (_ptr(qweight), _ptr(qzeros), _ptr(scales), N, K, group_size, _ptr(weight),
+                _ptr(s_out), _ptr(z_out))
+        _run(Launch(L.tm_wq_repack_awq, args, "wq_repack_awq", dev))
+    else:
+        args = (_ptr(qweight), _ptr(qzeros), _ptr(scales), N, K, group_size, zero_offset,
+                _ptr(weight), _ptr(s_out), _ptr(z_out))
+        _run(Launch(L.tm_wq_repack_gptq, args, "wq_repack_gptq", dev))
+    return weight, s_out, z_out
+
+
+def from_gptq(qweight, qzeros, scales, group_size=128, zero_offset=1, g_idx=None):
+    """A GPTQ int4 checkpoint (qweight int32 [K/8, N], qzeros int32 [K/G, N/8],
+    scales [K/G, N]) in the int4 layout of int4_matmul: returns
+    (weight uint8 [N, K/2], scales [N, K/G], zeros uint8 [N, K/G]).
+    zero_offset: 1 for the original format (zero-points stored minus one), 0 for
+    its v2 variant.  g_idx, if given, must be the trivial k // group_size."""
+    return _repack(False, qweight, qzeros, scales, group_size, zero_offset, g_idx)
+
+
+def from_awq(qweight, qzeros, scales, group_size=128):
+    """An AWQ int4 checkpoint (qweight int32 [K, N/8] in AWQ column order,
+    qzeros int32 [K/G, N/8], scales [K/G, N]) in the int4 layout of
+    int4_matmul: returns (weight uint8 [N, K/2], scales [N, K/G], zeros uint8 [N, K/G])."""
+    return _repack(True, qweight, qzeros, scales, group_size, 0, None)
+
+
 def make_int8_matmul_kernel():
     return Kernel("int8_matmul", int8_matmul, {})
 
