@@ -179,6 +179,39 @@ def kda_decode(dev, B=16, H=16, D=128):
                         "Dv": D, "state_sets_rotated": R})
 
 
+def decode_attn(dev, paged=False, B=8, Hq=32, Hkv=8, D=128, S=8192, page_size=16):
+    """Decode attention over an fp16 KV cache (one query token per head);
+    caches rotated past the Infinity Cache."""
+    import torch
+    import triton_metal_amd as tm
+    g = torch.Generator(device=dev).manual_seed(7)
+    per = 2 * B * Hkv * S * D * 2
+    R = _nsets(per)
+    q = torch.randn(B, Hq, D, device=dev, generator=g).half()
+    o = torch.empty_like(q)
+    launches, keep = [], [q, o]
+    for _ in range(R):
+        if paged:
+            npb = S // page_size
+            kc = torch.randn(B * npb, page_size, Hkv, D, device=dev, generator=g).half()
+            vc = torch.randn(B * npb, page_size, Hkv, D, device=dev, generator=g).half()
+            table = torch.randperm(B * npb, device=dev, generator=g).int().reshape(B, npb)
+            launches.append(tm.plan_decode_attention(q, kc, vc, o, page_table=table))
+            keep += [kc, vc, table]
+        else:
+            kc = torch.randn(B, Hkv, S, D, device=dev, generator=g).half()
+            vc = torch.randn(B, Hkv, S, D, device=dev, generator=g).half()
+            launches.append(tm.plan_decode_attention(q, kc, vc, o))
+            keep += [kc, vc]
+    nbytes = 2 * B * Hkv * S * D * 2 + 2 * B * Hq * D * 2
+    flops = 4 * B * Hq * S * D
+    return dict(launches=launches, keep=keep, bytes=nbytes, flops=flops, bound="hbm",
+                dtype="fp16",
+                config={"workload": "decode_attention_paged" if paged else "decode_attention",
+                        "B": B, "q_heads": Hq, "kv_heads": Hkv, "D": D, "seq_len": S,
+                        "page_size": page_size if paged else None, "cache_sets_rotated": R})
+
+
 WORKLOADS = {
     "w4a16_m1": lambda d: w4a16(d, 1),
     "w4a16_m8": lambda d: w4a16(d, 8),
@@ -193,6 +226,8 @@ WORKLOADS = {
     "flash_full": lambda d: flash(d, False),
     "kda": lambda d: kda(d),
     "kda_decode": lambda d: kda_decode(d),
+    "decode_attn": lambda d: decode_attn(d),
+    "decode_attn_paged": lambda d: decode_attn(d, paged=True),
 }
 HEADLINE = "w4a16_m1"
 

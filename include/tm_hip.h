@@ -175,6 +175,40 @@ int tm_flash_attention(const void* q, const void* k, const void* v, void* o, flo
                        const long long* strides, float scale, int causal, int dtype,
                        void* stream);
 
+/* ---- decode attention ---------------------------------------------------------
+ * One query token per (batch, query head) over a KV cache:
+ *   o[b, h] = softmax_p(scale * q[b, h] . K[b, h / (q_heads / kv_heads), p]) V[...]
+ * over positions p < len(b), fp32 softmax; lse (may be NULL) receives the
+ * natural-log logsumexp [batch, q_heads].  A batch entry with no position
+ * gives o = 0, lse = -inf.  Replaces the reference's decode templates
+ * (_msl_templates.py): make_kv_cache_attention_kernel (1949-2048),
+ * make_gqa_attention_kernel (2049-2160), make_batched_kv_decode_kernel
+ * (2161-2278), make_paged_attention_kernel (2279-2404),
+ * make_multi_head_paged_attention_kernel (2405-2532) and
+ * make_fp16_kv_attention_kernel (2533-2629).
+ * q, o: [batch, q_heads, head_dim] in q_dtype / o_dtype; the cache in
+ * kv_dtype, head dim contiguous; kv_strides = {batch (paged: page), kv head,
+ * position (paged: slot)} in elements, NULL for
+ *   contiguous [batch][kv_heads][seq_len][head_dim], or
+ *   paged      [pages][page_size][kv_heads][head_dim].
+ * seq_lens: int32 [batch] on the device (clamped to seq_len) or NULL (every
+ * batch entry has seq_len positions); seq_len bounds the positions.
+ * page_table: int32 [batch, max_pages] on the device, or NULL (contiguous);
+ * position p sits in page page_table[b][p / page_size], slot p % page_size.
+ * workspace: scratch for per-slice partials of long sequences, at least
+ * tm_decode_attention_workspace_size(...) bytes (NULL or smaller: no slices).
+ * fp16 / bf16 caches with head_dim 64 or 128 run on MFMA kernels; everything
+ * else (head_dim <= 256) on an fp32 kernel.  With an fp32 query and a 16-bit
+ * cache the MFMA kernels round the query to the cache dtype. */
+size_t tm_decode_attention_workspace_size(int batch, int q_heads, int kv_heads, int head_dim,
+                                          int seq_len, int page_size);
+int tm_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,
+                        float* lse, int batch, int q_heads, int kv_heads, int head_dim,
+                        const int* seq_lens, int seq_len, const long long* kv_strides,
+                        const int* page_table, int page_size, int max_pages, float scale,
+                        int q_dtype, int kv_dtype, int o_dtype, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 /* ---- KDA chunked forward -----------------------------------------------------
  * No counterpart in the reference (it has no linear attention): the gated
  * delta rule of Kimi Delta Attention in the [B, T, H, D] layout of its chunked

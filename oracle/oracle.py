@@ -38,6 +38,9 @@ PINNING = {
                  "dequant equivalence through gptq_to_ref (format not in the reference)",
     "pack_awq": "inverse of the published reverse-order unpacking; identity-column word "
                 "0x75316420; dequant equivalence through awq_to_ref",
+    "decode_attention": "flash_attention on one query row (dense and gathered pages), "
+                        "brute-force phase loops, closed forms (one position -> V[0], "
+                        "zero query -> mean of V)",
     "gptq_to_ref": "dequant_int4 of the result equals (q - z) s of the unpacked checkpoint",
     "awq_to_ref": "dequant_int4 of the result equals (q - z) s of the unpacked checkpoint",
 }
@@ -155,6 +158,51 @@ def flash_attention(Q, K, V, scale: float, causal: bool):
     with np.errstate(divide="ignore"):
         lse = np.where(l[..., 0] > 0, m_safe[..., 0] + np.log(l[..., 0]), -np.inf)
     return o, lse
+
+
+# ---------------------------------------------------------------------------
+# decode attention (one query token per head over a KV cache)
+# ---------------------------------------------------------------------------
+def decode_attention(q, K, V, lens, scale: float, page_table=None):
+    """The reference's decode templates in float64; returns (O [B, Hq, D], LSE [B, Hq]).
+
+    Per (batch b, query head h): KV head kvh = h // (Hq // Hkv)
+    (make_gqa_attention_kernel _msl_templates.py:2098-2101); positions
+    p < lens[b] (make_batched_kv_decode_kernel 2201-2207); three phases as the
+    templates: max of scale * q.K[p] (1995-2004), sum of exp(score - max)
+    (2017-2026), weights * V (2039-2050).  Dense caches are [B, Hkv, S, D];
+    with page_table [B, max_pages] the caches are pages [n, page_size, Hkv, D]
+    and position p is slot p % page_size of page page_table[b][p // page_size]
+    (make_multi_head_paged_attention_kernel 2448-2455).  No position: O = 0,
+    LSE = -inf."""
+    q = np.asarray(q, np.float64)
+    K = np.asarray(K, np.float64)
+    V = np.asarray(V, np.float64)
+    B, Hq, D = q.shape
+    Hkv = K.shape[2] if page_table is not None else K.shape[1]
+    group = Hq // Hkv
+    O = np.zeros((B, Hq, D))
+    LSE = np.full((B, Hq), -np.inf)
+    for b in range(B):
+        n = int(lens[b])
+        if n == 0:
+            continue
+        pos = np.arange(n)
+        for h in range(Hq):
+            kvh = h // group
+            if page_table is not None:
+                ps = K.shape[1]
+                pages = np.asarray(page_table)[b][pos // ps]
+                kr, vr = K[pages, pos % ps, kvh], V[pages, pos % ps, kvh]
+            else:
+                kr, vr = K[b, kvh, :n], V[b, kvh, :n]
+            sc = kr @ q[b, h] * scale
+            m = sc.max()
+            e = np.exp(sc - m)
+            tot = e.sum()
+            O[b, h] = (e / tot) @ vr
+            LSE[b, h] = m + np.log(tot)
+    return O, LSE
 
 
 # ---------------------------------------------------------------------------

@@ -46,6 +46,10 @@ SIGNATURES = {
     "tm_flash_attention": [vp, vp, vp, vp, vp, i32, i32, i32, i32, C.POINTER(C.c_longlong),
                            C.c_float, i32, i32, vp],
     "tm_kda_workspace_size": [i32, i32, i32, i32, i32, i32],
+    "tm_decode_attention_workspace_size": [i32, i32, i32, i32, i32, i32],
+    "tm_decode_attention": [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32,
+                            C.POINTER(C.c_longlong), vp, i32, i32, C.c_float, i32, i32, i32, vp,
+                            sz, vp],
     "tm_kda_chunk_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, C.c_float,
                          i32, vp, sz, vp],
     "tm_kda_recurrent_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, C.c_float,
@@ -56,6 +60,7 @@ _RESTYPES = {
     "tm_version": C.c_char_p,
     "tm_builtin_module_name": C.c_char_p,
     "tm_kda_workspace_size": sz,
+    "tm_decode_attention_workspace_size": sz,
 }
 
 _lock = threading.Lock()

@@ -483,6 +483,196 @@ def make_flash_attention_kernel(head_dim=64, Br=16, Bc=16, block_size=256, causa
 
 
 # ---------------------------------------------------------------------------
+# decode attention (one query token per head over a KV cache)
+# ---------------------------------------------------------------------------
+def plan_decode_attention(q, k_cache, v_cache, o, seq_lens=None, seq_len=None, page_table=None,
+                          scale=None, lse=None, workspace=None, stream=None) -> Launch:
+    """Validate and bind one decode-attention call (see decode_attention)."""
+    dev = _device_of(q, k_cache, v_cache, o, seq_lens, page_table, lse, workspace)
+    if q.dim() != 3 or o.shape != q.shape:
+        raise ValueError(f"q and o must be [B, Hq, D]: {tuple(q.shape)} {tuple(o.shape)}")
+    B, Hq, D = q.shape
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise ValueError("k_cache and v_cache must share shape and strides")
+    if k_cache.dtype != v_cache.dtype:
+        raise TypeError("k_cache and v_cache must share a dtype")
+    if k_cache.dim() != 4 or k_cache.shape[-1] != D or k_cache.stride(-1) != 1:
+        raise ValueError("the cache must be 4-D with a contiguous head dim equal to q's")
+    for t, w in ((q, "q"), (o, "o"), (seq_lens, "seq_lens"), (page_table, "page_table"),
+                 (lse, "lse")):
+        _need_contig(t, w)
+    if page_table is not None:
+        # [pages, page_size, Hkv, D]
+        npages, page_size, Hkv = k_cache.shape[:3]
+        if page_table.dtype != torch.int32 or page_table.dim() != 2 or page_table.shape[0] != B:
+            raise ValueError("page_table must be int32 [B, max_pages]")
+        max_pages = page_table.shape[1]
+        strides = (k_cache.stride(0), k_cache.stride(2), k_cache.stride(1))
+        cap = page_size * max_pages
+    else:
+        # [B, Hkv, S, D]
+        if k_cache.shape[0] != B:
+            raise ValueError(f"cache batch {k_cache.shape[0]} != q batch {B}")
+        Hkv, cap = k_cache.shape[1], k_cache.shape[2]
+        page_size, max_pages = 0, 0
+        strides = (k_cache.stride(0), k_cache.stride(1), k_cache.stride(2))
+    if Hq % Hkv:
+        raise ValueError(f"q heads {Hq} not a multiple of kv heads {Hkv}")
+    if seq_len is None:
+        seq_len = cap
+    if seq_len > cap:
+        raise ValueError(f"seq_len {seq_len} exceeds the cache's {cap} positions")
+    if seq_lens is not None and (seq_lens.dtype != torch.int32 or seq_lens.shape != (B,)):
+        raise ValueError("seq_lens must be int32 [B]")
+    if lse is not None and (lse.dtype != torch.float32 or lse.shape != (B, Hq)):
+        raise ValueError("lse must be fp32 [B, Hq]")
+    if scale is None:
+        scale = D ** -0.5
+    need = _lib.lib().tm_decode_attention_workspace_size(B, Hq, Hkv, D, seq_len,
+                                                         page_size if page_table is not None else 0)
+    if workspace is None and need > 0:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    wbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    st = (C.c_longlong * 3)(*strides)
+    args = (_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(o), _ptr(lse), B, Hq, Hkv, D,
+            _ptr(seq_lens), int(seq_len), st, _ptr(page_table), page_size, max_pages,
+            float(scale), _dt(q, "q"), _dt(k_cache, "k_cache"), _dt(o, "o"), _ptr(workspace),
+            wbytes)
+    launch = Launch(_lib.lib().tm_decode_attention, args, "decode_attention", dev, stream)
+    launch._keep = (st, workspace)
+    return launch
+
+
+def decode_attention(q, k_cache, v_cache, seq_lens=None, seq_len=None, page_table=None,
+                     scale=None, o=None, lse=None):
+    """Attention of one query token per (batch, head) over a KV cache.
+
+    q [B, Hq, D]; cache [B, Hkv, S, D] (any strides, contiguous D), or paged
+    [pages, page_size, Hkv, D] with page_table int32 [B, max_pages];
+    seq_lens int32 [B] (positions per batch entry) or None for seq_len (default:
+    the cache's capacity) everywhere.  Query head h reads KV head
+    h // (Hq // Hkv).  scale defaults to D**-0.5.  Returns o (q's dtype unless
+    given)."""
+    if o is None:
+        o = torch.empty_like(q)
+    _run(plan_decode_attention(q, k_cache, v_cache, o, seq_lens=seq_lens, seq_len=seq_len,
+                               page_table=page_table, scale=scale, lse=lse))
+    return o
+
+
+# Wrappers with the buffer orders of the reference's decode templates.
+def kv_cache_attention(Q, K_cache, V_cache, O, seq_len, scale):
+    """make_kv_cache_attention_kernel (_msl_templates.py:1949-2048): Q, O
+    [n_heads, D]; K_cache, V_cache [n_heads, seq_len, D]."""
+    H, D = Q.shape
+    kc = K_cache.reshape(H, -1, D)[:, :seq_len].unsqueeze(0)
+    vc = V_cache.reshape(H, -1, D)[:, :seq_len].unsqueeze(0)
+    decode_attention(Q.unsqueeze(0), kc, vc, seq_len=seq_len, scale=scale, o=O.view(1, H, D))
+    return O
+
+
+def gqa_attention(Q, K_cache, V_cache, O, seq_len, scale, n_q_per_kv=None):
+    """make_gqa_attention_kernel (_msl_templates.py:2049-2160): Q, O
+    [n_q_heads, D]; K_cache, V_cache [n_kv_heads, seq_len, D]; query head h
+    reads KV head h // n_q_per_kv."""
+    Hq, D = Q.shape
+    Hkv = K_cache.numel() // (seq_len * D)
+    if n_q_per_kv is not None and n_q_per_kv * Hkv != Hq:
+        raise ValueError(f"n_q_per_kv={n_q_per_kv} does not match {Hq} / {Hkv} heads")
+    kc = K_cache.reshape(Hkv, seq_len, D).unsqueeze(0)
+    vc = V_cache.reshape(Hkv, seq_len, D).unsqueeze(0)
+    decode_attention(Q.unsqueeze(0), kc, vc, seq_len=seq_len, scale=scale, o=O.view(1, Hq, D))
+    return O
+
+
+def batched_kv_decode(Q, K_cache, V_cache, O, seq_lens, max_seq_len, batch_size=None):
+    """make_batched_kv_decode_kernel (_msl_templates.py:2161-2278): Q, O
+    [batch, n_heads, D]; caches [batch, n_heads, max_seq_len, D]; seq_lens
+    int32 [batch]; scale 1/sqrt(D)."""
+    B, H, D = Q.shape
+    if batch_size is not None and batch_size != B:
+        raise ValueError(f"batch_size={batch_size} but Q has {B} entries")
+    kc = K_cache.reshape(B, H, max_seq_len, D)
+    vc = V_cache.reshape(B, H, max_seq_len, D)
+    decode_attention(Q, kc, vc, seq_lens=seq_lens.to(torch.int32), seq_len=max_seq_len,
+                     scale=D ** -0.5, o=O)
+    return O
+
+
+def multi_head_paged_attention(Q, K_pages, V_pages, page_table, O, seq_len, n_pages,
+                               page_size=16):
+    """make_multi_head_paged_attention_kernel (_msl_templates.py:2405-2532):
+    Q, O [n_heads, D]; pages [n_physical_pages, page_size, n_heads, D];
+    page_table [>= n_pages] (logical -> physical); scale 1/sqrt(D)."""
+    H, D = Q.shape
+    kp = K_pages.reshape(-1, page_size, H, D)
+    vp = V_pages.reshape(-1, page_size, H, D)
+    pt = page_table[:n_pages].to(torch.int32).reshape(1, n_pages).contiguous()
+    decode_attention(Q.unsqueeze(0), kp, vp, seq_len=seq_len, page_table=pt, scale=D ** -0.5,
+                     o=O.view(1, H, D))
+    return O
+
+
+def paged_attention(Q, K_pages, V_pages, page_table, O, seq_len, n_pages, page_size=16):
+    """make_paged_attention_kernel (_msl_templates.py:2279-2404): one head;
+    Q, O [D]; pages [n_physical_pages, page_size, D]."""
+    D = Q.shape[-1]
+    multi_head_paged_attention(Q.reshape(1, D), K_pages.reshape(-1, page_size, 1, D),
+                               V_pages.reshape(-1, page_size, 1, D), page_table,
+                               O.view(1, D), seq_len, n_pages, page_size)
+    return O
+
+
+def fp16_kv_attention(Q, K_cache, V_cache, O, seq_len):
+    """make_fp16_kv_attention_kernel (_msl_templates.py:2533-2629): Q, O fp32
+    [D]; K_cache, V_cache fp16 [>= seq_len, D]; scale 1/sqrt(D)."""
+    D = Q.shape[-1]
+    kc = K_cache.reshape(1, 1, -1, D)
+    vc = V_cache.reshape(1, 1, -1, D)
+    decode_attention(Q.reshape(1, 1, D), kc, vc, seq_len=seq_len, scale=D ** -0.5,
+                     o=O.view(1, 1, D))
+    return O
+
+
+def make_kv_cache_attention_kernel(head_dim=64, block_size=256):
+    def run(Q, K_cache, V_cache, O, seq_len, scale):
+        return kv_cache_attention(Q, K_cache, V_cache, O, seq_len, scale)
+    return Kernel("kv_cache_attention", run, {"head_dim": head_dim})
+
+
+def make_gqa_attention_kernel(head_dim=64, n_q_per_kv=4, block_size=256):
+    def run(Q, K_cache, V_cache, O, seq_len, scale):
+        return gqa_attention(Q, K_cache, V_cache, O, seq_len, scale, n_q_per_kv)
+    return Kernel("gqa_attention", run, {"head_dim": head_dim, "n_q_per_kv": n_q_per_kv})
+
+
+def make_batched_kv_decode_kernel(n_heads=8, head_dim=64, block_size=256):
+    def run(Q, K_cache, V_cache, O, seq_lens, max_seq_len, batch_size):
+        return batched_kv_decode(Q, K_cache, V_cache, O, seq_lens, max_seq_len, batch_size)
+    return Kernel("batched_kv_decode", run, {"n_heads": n_heads, "head_dim": head_dim})
+
+
+def make_paged_attention_kernel(head_dim=64, page_size=16, block_size=256):
+    def run(Q, K_pages, V_pages, page_table, O, seq_len, n_pages):
+        return paged_attention(Q, K_pages, V_pages, page_table, O, seq_len, n_pages, page_size)
+    return Kernel("paged_attention", run, {"head_dim": head_dim, "page_size": page_size})
+
+
+def make_multi_head_paged_attention_kernel(n_heads=8, head_dim=64, page_size=16, block_size=256):
+    def run(Q, K_pages, V_pages, page_table, O, seq_len, n_pages):
+        return multi_head_paged_attention(Q, K_pages, V_pages, page_table, O, seq_len, n_pages,
+                                          page_size)
+    return Kernel("multi_head_paged_attention", run,
+                  {"n_heads": n_heads, "head_dim": head_dim, "page_size": page_size})
+
+
+def make_fp16_kv_attention_kernel(head_dim=64, block_size=256):
+    def run(Q, K_cache, V_cache, O, seq_len):
+        return fp16_kv_attention(Q, K_cache, V_cache, O, seq_len)
+    return Kernel("fp16_kv_attention", run, {"head_dim": head_dim})
+
+
+# ---------------------------------------------------------------------------
 # KDA chunked forward (no counterpart in the reference)
 # ---------------------------------------------------------------------------
 KDA_KEY_DIM = KDA_VALUE_DIM = 128
