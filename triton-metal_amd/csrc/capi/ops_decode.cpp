@@ -33,14 +33,15 @@ struct DecodeParams {
 
 bool is16(int dt) { return dt == TM_DT_F16 || dt == TM_DT_BF16; }
 
-// Slices of the positions for the MFMA kernel: enough waves to fill the chip
-// (B * kv_heads * head blocks * slices >= 2048) with at least 256 positions per
-// slice, a multiple of 32 (and, paged, whole pages, at most 64 of them).
+// Slices of the positions for the MFMA kernel: about one resident round of
+// waves (B * kv_heads * head blocks * slices ~ 768: three 48 KB rings per CU)
+// with at least 256 positions per slice, a multiple of 32 (and, paged, whole
+// pages, at most 64 of them).
 void plan_split(int batch, int q_heads, int kv_heads, int cap, int page_size, bool paged,
                 int* nsplit, int* split_len) {
   const int group = q_heads / kv_heads, hbn = (group + 15) / 16;
   const long long waves = (long long)batch * kv_heads * hbn;
-  int want = (int)std::max<long long>(1, (2048 + waves - 1) / waves);
+  int want = (int)std::max<long long>(1, (768 + waves - 1) / waves);
   int sl = std::max(256, (cap + want - 1) / want);
   sl = (sl + 31) / 32 * 32;
   if (paged) {

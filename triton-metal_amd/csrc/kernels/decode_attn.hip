@@ -152,13 +152,18 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
   };
   auto issue = [&](int t) {
     const uint32_t st = lbase + (uint32_t)((t % NST) * 2 * TB);
+    // all row offsets first (paged: the page fetches overlap), then the copies
+    long long e[NCP];
 #pragma unroll
     for (int i = 0; i < NCP; ++i) {
       const int r = RPC * i + lane / PR, sl = lane % PR;
       const int pos = min(p0 + 32 * t + r, len - 1);  // rows past the end are masked
-      const long long e = row_off(pos) + 8 * (sl ^ (r & (PR - 1)));
-      dma16(p.k + e, st + 1024 * i);
-      dma16(p.v + e, st + TB + 1024 * i);
+      e[i] = row_off(pos) + 8 * (sl ^ (r & (PR - 1)));
+    }
+#pragma unroll
+    for (int i = 0; i < NCP; ++i) {
+      dma16(p.k + e[i], st + 1024 * i);
+      dma16(p.v + e[i], st + TB + 1024 * i);
     }
   };
 #pragma unroll
