@@ -274,27 +274,45 @@ TM_DECODE(64, f16, false)
 TM_DECODE(64, bf16, true)
 
 // ----------------------------------------------------------------------------
-// Combine the slices: grid = B * Hq, block = 64 (D <= 256, 4 per lane).
+// Combine the slices: grid = B * Hq, block = 64 (D <= 256, 4 per lane).  The
+// lanes take the slices' maxima in parallel; the weighted sum runs 8 slices
+// per step so that their loads are in flight together.
 // ----------------------------------------------------------------------------
 extern "C" __global__ __launch_bounds__(64) void decode_attn_combine(DecodeParams p) {
   const int bh = blockIdx.x, lane = threadIdx.x;
-  const int D = p.D;
-  const float* w = p.ws + (long long)bh * p.nsplit * (D + 4);
+  const int D = p.D, ns = p.nsplit, RS = D + 4;
+  const float* w = p.ws + (long long)bh * ns * RS;
   float M = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, w[s * (D + 4) + D]);
+  for (int s = lane; s < ns; s += 64) M = fmaxf(M, w[s * RS + D]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
   const float mu = M == -INFINITY ? 0.0f : M;
   float L = 0.0f, acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < p.nsplit; ++s) {
-    const float* ws = w + s * (D + 4);
+  int s0 = 0;
+  for (; s0 + 8 <= ns; s0 += 8) {
+    float f[8], o[8][4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float* ws = w + (s0 + j) * RS;
+      const float ls = ws[D + 1];
+      f[j] = ls > 0.0f ? __builtin_amdgcn_exp2f(ws[D] - mu) : 0.0f;
+      L += ls * f[j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[j][i] = lane + 64 * i < D ? ws[lane + 64 * i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += o[j][i] * f[j];
+  }
+  for (; s0 < ns; ++s0) {
+    const float* ws = w + s0 * RS;
     const float ls = ws[D + 1];
-    if (ls == 0.0f) continue;  // empty slice
-    const float f = __builtin_amdgcn_exp2f(ws[D] - mu);
+    const float f = ls > 0.0f ? __builtin_amdgcn_exp2f(ws[D] - mu) : 0.0f;
     L += ls * f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d = lane + 64 * i;
-      if (d < D) acc[i] += ws[d] * f;
-    }
+    for (int i = 0; i < 4; ++i)
+      if (lane + 64 * i < D) acc[i] += ws[lane + 64 * i] * f;
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
 #pragma unroll
