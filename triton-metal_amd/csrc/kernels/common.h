@@ -150,6 +150,13 @@ TM_DEV void dma16(const void* g, uint32_t lds) {
                "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
+// The same copy from a wave-uniform base plus a 32-bit byte offset per lane
+// (one VGPR per copy instead of a 64-bit address pair).
+TM_DEV void dma16s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
 TM_DEV void dma4(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g),
                "s"(__builtin_amdgcn_readfirstlane(lds))

@@ -160,31 +160,32 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
   // lane % (D/8); its source offsets within a key block are fixed, only the
   // block base moves (32-bit offsets; the host checks 64 * stride < 2^31)
   const int prow = lane / (D / 8), pch = lane % (D / 8);
-  int koff[BPW], voff[BPW];
+  uint32_t koff[BPW], voff[BPW];  // byte offsets
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     const int r = (wave * BPW + i) * RPB + prow;
-    koff[i] = r * (int)p.sks + 8 * (pch ^ k_swz<D>(r));
-    voff[i] = r * (int)p.svs + 8 * (pch ^ v_swz<D>(r));
+    koff[i] = 2u * (uint32_t)(r * (int)p.sks + 8 * (pch ^ k_swz<D>(r)));
+    voff[i] = 2u * (uint32_t)(r * (int)p.svs + 8 * (pch ^ v_swz<D>(r)));
   }
   auto issue_kv = [&](uint16_t* kd, uint16_t* vd, int kv0) {
+    const uint16_t* kt = kg + (long long)kv0 * p.sks;
+    const uint16_t* vt = vg + (long long)kv0 * p.svs;
     if (kv0 + BN <= S) {
-      const uint16_t* kt = kg + (long long)kv0 * p.sks;
-      const uint16_t* vt = vg + (long long)kv0 * p.svs;
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int blk = wave * BPW + i;
-        g2lds16(kt + koff[i], kd + blk * 512);
-        g2lds16(vt + voff[i], vd + blk * 512);
+        dma16s(kt, koff[i], lds_off(kd + blk * 512));
+        dma16s(vt, voff[i], lds_off(vd + blk * 512));
       }
     } else {
+      // rows past the end re-read row S - 1 (their scores are masked)
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int blk = wave * BPW + i;
         const int r = blk * RPB + prow;
-        const int gr = min(kv0 + r, S - 1);  // rows past the end are masked later
-        g2lds16(kg + (long long)gr * p.sks + 8 * (pch ^ k_swz<D>(r)), kd + blk * 512);
-        g2lds16(vg + (long long)gr * p.svs + 8 * (pch ^ v_swz<D>(r)), vd + blk * 512);
+        const int back = r - min(r, S - 1 - kv0);
+        dma16s(kt, koff[i] - 2u * (uint32_t)(back * (int)p.sks), lds_off(kd + blk * 512));
+        dma16s(vt, voff[i] - 2u * (uint32_t)(back * (int)p.svs), lds_off(vd + blk * 512));
       }
     }
   };
@@ -224,14 +225,31 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
       __builtin_amdgcn_s_setprio(1);
       f16_t s[2];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        s[kt] = f16_t{};
-        const int r = kt * 32 + l32;
+      for (int kt = 0; kt < 2; ++kt) s[kt] = f16_t{};
+      // The two key halves alternate, so consecutive MFMAs are independent;
+      // the K operands of step c + KPD are read while step c multiplies.
+      constexpr int KPD = 2;
+      u4_t ka[DC][2];
+      auto kread = [&](int c) {
 #pragma unroll
-        for (int c = 0; c < DC; ++c) {
-          const u4_t a = *(const u4_t*)(ks + r * D + 8 * ((2 * c + h32) ^ k_swz<D>(r)));
-          s[kt] = mfma32<BF16>(a, qreg[c], s[kt]);
+        for (int kt = 0; kt < 2; ++kt) {
+          const int r = kt * 32 + l32;
+          ka[c][kt] = *(const u4_t*)(ks + r * D + 8 * ((2 * c + h32) ^ k_swz<D>(r)));
         }
+      };
+#pragma unroll
+      for (int c = 0; c < KPD; ++c) kread(c);
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        if (c + KPD < DC) kread(c + KPD);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s[kt] = mfma32<BF16>(ka[c][kt], qreg[c], s[kt]);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * KPD, 0);
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        if (c + KPD < DC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
       }
       __builtin_amdgcn_s_setprio(0);
       // raw scores sc[16 kt + i] of key kv0 + 32 kt + 8 (i / 4) + 4 h32 + i % 4
@@ -287,19 +305,31 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
       // O^T[d][q] += V^T[d][kv] P^T[kv][q]; MFMA u covers keys
       //   32 (u/2) + 16 (u%2) + 8 (e/4) + 4 h32 + e % 4
       __builtin_amdgcn_s_setprio(1);
+      // operand i = DT u + t; the V^T operands of i + VPD are read while i multiplies
+      constexpr int NVO = 4 * DT, VPD = 2;
+      u4_t va[NVO];
+      auto vread = [&](int i) {
+        const int u = i / DT, t = i % DT;
+        const int kb = 32 * (u >> 1) + 16 * (u & 1);
+        const int r0 = kb + tv_row, r1 = r0 + 8;
+        const int c = (32 * t + tv_d) >> 3, off = (32 * t + tv_d) & 7;
+        const u2_t lo = lds_tr16(vs + r0 * D + 8 * (c ^ v_swz<D>(r0)) + off);
+        const u2_t hi = lds_tr16(vs + r1 * D + 8 * (c ^ v_swz<D>(r1)) + off);
+        va[i].x = lo.x; va[i].y = lo.y; va[i].z = hi.x; va[i].w = hi.y;
+      };
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int i = 0; i < VPD; ++i) vread(i);
 #pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          const int kb = 32 * (u >> 1) + 16 * (u & 1);
-          const int r0 = kb + tv_row, r1 = r0 + 8;
-          const int c = (32 * t + tv_d) >> 3, off = (32 * t + tv_d) & 7;
-          const u2_t lo = lds_tr16(vs + r0 * D + 8 * (c ^ v_swz<D>(r0)) + off);
-          const u2_t hi = lds_tr16(vs + r1 * D + 8 * (c ^ v_swz<D>(r1)) + off);
-          u4_t a;
-          a.x = lo.x; a.y = lo.y; a.z = hi.x; a.w = hi.y;
-          oacc[t] = mfma32<BF16>(a, pop[u], oacc[t]);
-        }
+      for (int i = 0; i < NVO; ++i) {
+        if (i + VPD < NVO) vread(i + VPD);
+        oacc[i % DT] = mfma32<BF16>(va[i], pop[i / DT], oacc[i % DT]);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * VPD, 0);
+#pragma unroll
+      for (int i = 0; i < NVO; ++i) {
+        if (i + VPD < NVO) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
       __builtin_amdgcn_s_setprio(0);
     }
     if (more) {
