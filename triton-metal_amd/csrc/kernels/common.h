@@ -139,26 +139,28 @@ TM_DEV uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)(lds_void_t
 
 // Global -> LDS copies issued in asm: lane l deposits its 16 (4) bytes at LDS
 // byte offset lds + 16 l (4 l); lds must be wave-uniform.  The compiler does
-// not see these copies, so it adds no waits for them (given the builtin, it
-// waits for every outstanding copy before any LDS read).  The caller waits with
+// not see these copies, so it adds no waits for them (with the builtin in a
+// function, every LDS read there waits for all earlier LDS reads, lgkmcnt(0),
+// instead of only for its own).  The caller waits with
 // wait_vm<N>() - N = copies (and other vector memory operations) issued after
 // the awaited one - before reading the data, and must not overwrite LDS that
 // a copy still targets.  m0 is written here; the kernels that use these
-// helpers use m0 for nothing else.
+// helpers use m0 for nothing else.  A global load into LDS needs one wait
+// state after the write of m0 it reads (an s_nop 0 between the two).
 TM_DEV void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
                "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 // The same copy from a wave-uniform base plus a 32-bit byte offset per lane
 // (one VGPR per copy instead of a 64-bit address pair).
 TM_DEV void dma16s(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
                "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 TM_DEV void dma4(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g),
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
                "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }

@@ -116,7 +116,9 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
   __shared__ __align__(16) uint16_t Ks0[BN * D], Ks1[BN * D];
   __shared__ __align__(16) uint16_t Vs0[BN * D], Vs1[BN * D];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave index through readfirstlane: known uniform, so what derives from it
+  // (copy destinations, row ranges) stays in scalar registers
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h32 = lane >> 5, l32 = lane & 31;
   const int S = p.S;
   const int nqb = (S + BM - 1) / BM;
@@ -174,8 +176,8 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int blk = wave * BPW + i;
-        dma16s(kt, koff[i], lds_off(kd + blk * 512));
-        dma16s(vt, voff[i], lds_off(vd + blk * 512));
+        dma16s(kt, koff[i], lds_off(kd) + blk * 1024);
+        dma16s(vt, voff[i], lds_off(vd) + blk * 1024);
       }
     } else {
       // rows past the end re-read row S - 1 (their scores are masked)
@@ -184,8 +186,8 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
         const int blk = wave * BPW + i;
         const int r = blk * RPB + prow;
         const int back = r - min(r, S - 1 - kv0);
-        dma16s(kt, koff[i] - 2u * (uint32_t)(back * (int)p.sks), lds_off(kd + blk * 512));
-        dma16s(vt, voff[i] - 2u * (uint32_t)(back * (int)p.svs), lds_off(vd + blk * 512));
+        dma16s(kt, koff[i] - 2u * (uint32_t)(back * (int)p.sks), lds_off(kd) + blk * 1024);
+        dma16s(vt, voff[i] - 2u * (uint32_t)(back * (int)p.svs), lds_off(vd) + blk * 1024);
       }
     }
   };
