@@ -97,10 +97,12 @@ def test_int4_dequant_tile_bit_exact(dev, act):
 
 
 # (M, K, N) of each kernel kind: the stream kernel takes 1 < M <= 64 with
-# K <= 4096; the GEMV M = 1 and K = 8192; skinny the remaining M <= 8 shapes
-# with K % 512 == 0; wide M > 64 with fp16 activations and N % 128 == 0
-# (int8: no zero-points); tiled the other M > 64 shapes.
+# K <= 4096; the GEMV M = 1 and K = 8192; the two-tile GEMV int4 2 <= M <= 6
+# at K = 4096 with N % 32 == 0; skinny the remaining M <= 8 shapes with
+# K % 512 == 0; wide M > 64 with fp16 activations and N % 128 == 0 (int8: no
+# zero-points); tiled the other M > 64 shapes.
 INT4_KINDS = {"skinny": (8, 5120, 64), "gemv": (1, 4096, 64), "gemv8k": (8, 8192, 64),
+              "gemv2t": (4, 4096, 64),
               "stream8": (8, 4096, 64), "stream16": (16, 2048, 64),
               "stream_multi": (40, 2048, 64), "tiled": (72, 512, 64), "wide": (100, 1024, 256)}
 INT8_KINDS = {"skinny": (8, 768, 64), "stream8": (8, 2048, 64), "stream16": (16, 2048, 64),
@@ -280,6 +282,32 @@ def test_int8_shapes(dev, M, N, K, zeros):
     tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None if z is None else z.to(dev),
                    M, N, K)
     ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
+    check_close(out.cpu(), ref)
+
+
+# --- two-tile GEMV (int4, 2 <= M <= 6, K = 4096, N % 32 == 0) --------------------
+@pytest.mark.parametrize("M,N", [(2, 32), (3, 96), (5, 64), (6, 160)])
+@pytest.mark.parametrize("zeros", ["f16", "u8", None])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int4_two_tile_gemv_shapes(dev, M, N, zeros, act):
+    K, G = 4096, 128
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 17 + N, act=act, zeros=zeros)
+    out = torch.empty(M, N, dtype=act, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
+                   None if z is None else z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
+    check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
+
+
+def test_int4_two_tile_gemv_fractional_zero_points(dev):
+    """The zero-point enters the correction in fp32, so non-integer values
+    are exact as in the reference formula."""
+    M, N, K, G = 6, 64, 4096, 128
+    x, q, packed, s, _ = make_int4_problem(M, N, K, G, seed=23)
+    z = (torch.rand(N, K // G, generator=_gen(24)) * 8).half()
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev), z.to(dev), M, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
     check_close(out.cpu(), ref)
 
 

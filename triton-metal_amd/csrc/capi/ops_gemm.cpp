@@ -2,6 +2,7 @@
 // matmul, the dequantised weight tile, dense matmul and fused linear.
 // Each validates its arguments, picks a kernel variant from the shape and
 // dtypes and launches it asynchronously on the caller's stream.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <map>
@@ -81,6 +82,21 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
       const int grid = 8 * mtl * ((ntl + 7) / 8);
       return launch(kernel(name), dim3(grid), dim3(512), (unsigned)wl, stream, X, W, Y, S, Z, M,
                     N, K, bias);
+    }
+  }
+  // two-tile int4 GEMV: 2 <= M <= 6 at K = 4096 (from M = 7 on the streaming
+  // kernel is as fast or faster), 32 columns per workgroup
+  if (fast && qbits == 4 && M >= 2 && M <= 6 && G == 128 && K == 4096 && N % 32 == 0 &&
+      aligned16(S) && (!Z || aligned16(Z))) {
+    // X, then the scales and zero-points of 32 columns; at least the
+    // reduction's 7 waves x 2 tiles x 1 KB
+    size_t glds = (size_t)M * (K + 8) * 2 + (size_t)4 * 32 * (K / 128);
+    glds = std::max(glds, (size_t)7 * 2 * 1024);
+    if (glds <= (size_t)max_dynamic_lds()) {
+      char name[64];
+      snprintf(name, sizeof name, "wq_gemv4x2_%s_z%c_w8p4", act, zc);
+      return launch(kernel(name), dim3(N / 32), dim3(512), (unsigned)glds, stream, X, W, Y, S,
+                    Z, M, N, K, bias);
     }
   }
   // streaming kernel: 1 < M <= 64 (int4: 128), K-slices of 512 per wave (at

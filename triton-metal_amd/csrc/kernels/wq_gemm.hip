@@ -27,6 +27,8 @@
 // Kernels
 //   wq_gemv4_*   int4, M = 1 (and M <= 8 when K = 8192): GEMV, the whole grid
 //                resident, per-chunk MFMAs as the weights land.
+//   wq_gemv4x2_* int4, 2 <= M <= 6, K = 4096: the GEMV with two column tiles
+//                per workgroup and MFMA row sums.
 //   wq_stream_*  1 < M <= 64 (int4: 128), K <= 4096: weights and X streamed through LDS
 //                rings by global -> LDS copies, K split over the waves.
 //   wq_skinny_*  other M <= 8 shapes: the whole X[M, K] is staged once per
@@ -517,6 +519,157 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
     for (int e = 0; e < 4; ++e) {
       const int row = 4 * q + e;
       if (row < M) store_out(Y, (size_t)row * N + n, y[e] + bias_at(bias, n, BF16), BF16);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Multi-tile GEMV for 2 <= M <= 8 (int4, the exact shape K = NW * PF * 128,
+// G = 128): the GEMV above with NTL 16-column tiles per workgroup, so that the
+// M rows of X staged in LDS (M * (K + 8) * 2 bytes) serve NTL tiles and the
+// whole grid is resident (N = 14336, NTL = 2: 448 workgroups, two per CU).
+// All M rows of X are loaded before any is staged (one round trip, not M),
+// and staging is a permute and a store: the per-chunk row sums of the
+// zero-point correction (sum x and, for fp16, sum x * offset) come from
+// MFMAs of the X operands with constant B operands (ones; the operand's
+// offsets 1024 / 64 per position), already in the accumulator layout.
+// Wave w owns k = w*PF*128 .. +PF*128 of every tile; the waves' partial sums
+// are reduced through the X region of LDS once every wave is past its reads.
+// Dynamic LDS: max(M * (K + 8) * 2 bytes of X followed by the scales and
+// zero-points of the NTL * 16 columns (NTL * 16 rows x K / 128 each), the
+// (NW - 1) * NTL KB of the reduction).  S (and Z) must be 16-byte aligned.
+// ----------------------------------------------------------------------------
+template <bool BF16, int ZDT, int NW, int PF, int NTL>
+__device__ __forceinline__ void wq_gemv4x2_body(const uint16_t* __restrict__ X,
+                                                const uint8_t* __restrict__ W,
+                                                uint16_t* __restrict__ Y,
+                                                const uint16_t* __restrict__ S,
+                                                const void* __restrict__ Z, int M, int N, int K,
+                                                const uint16_t* bias) {
+  constexpr int NT = NW * 64;
+  constexpr int SDT = BF16 ? TM_DT_BF16 : TM_DT_F16;
+  constexpr int MX = 8;
+  extern __shared__ __align__(16) uint16_t xs[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ldx = K + 8;
+  const int nch = K >> 7;
+  uint16_t* sst = xs + (size_t)M * ldx;          // scales of the columns [16 NTL][nch]
+  uint16_t* zst = sst + 16 * NTL * nch;          // zero-points [16 NTL][nch] (bytes if uint8)
+  const int nb = blockIdx.x * 16 * NTL, q = lane >> 4;
+  const int m = min(lane & 15, M - 1);
+  const int kbeg = wave * (PF * 128);
+  const uint32_t vmask = vgpr_const(0x000F000Fu), vmagic = vgpr_const(w4_magic<BF16>());
+  const uint32_t vmask_hi = vgpr_const(0x00F000F0u), vmagic_hi = vgpr_const(0x54005400u);
+
+  // 1. every row of X, the scales and zero-points of the columns, 2. the
+  //    weights of every tile, 3. stage X.
+  constexpr int XP = PF / 4;  // pieces per thread per row: K / 8 / NT
+  u4_t xv[MX][XP];
+#pragma unroll
+  for (int r = 0; r < MX; ++r)
+#pragma unroll
+    for (int u = 0; u < XP; ++u)
+      xv[r][u] = r < M ? ldg128(X + (size_t)r * K + (size_t)(tid + NT * u) * 8)
+                       : u4_t{0u, 0u, 0u, 0u};
+  // (at most NT * 16 bytes of each: NTL * 32 * nch <= 8 KB)
+  const int sbytes = 32 * NTL * nch;
+  const int zbytes = ZDT == 3 ? 16 * NTL * nch : 32 * NTL * nch;
+  u4_t sv = {0u, 0u, 0u, 0u}, zv = {0u, 0u, 0u, 0u};
+  if (16 * tid < sbytes) sv = ldg128((const uint8_t*)S + (size_t)blockIdx.x * sbytes + 16 * tid);
+  if constexpr (ZDT >= 0)
+    if (16 * tid < zbytes) zv = ldg128((const uint8_t*)Z + (size_t)blockIdx.x * zbytes + 16 * tid);
+
+  u4_t wv[NTL][PF];
+#pragma unroll
+  for (int t = 0; t < NTL; ++t) {
+    const uint8_t* wrow =
+        W + (size_t)(nb + 16 * t + (lane & 15)) * (K >> 1) + (kbeg >> 1) + 16 * q;
+#pragma unroll
+    for (int i = 0; i < PF; ++i) wv[t][i] = ldg128(wrow + 64 * i);
+  }
+
+#pragma unroll
+  for (int r = 0; r < MX; ++r) {
+    if (r < M) {
+#pragma unroll
+      for (int u = 0; u < XP; ++u) {
+        const int p = tid + NT * u;
+        *(u4_t*)(xs + r * ldx + p * 8) = perm_x8(xv[r][u]);
+      }
+    }
+  }
+  if (16 * tid < sbytes) *(u4_t*)((uint8_t*)sst + 16 * tid) = sv;
+  if constexpr (ZDT >= 0)
+    if (16 * tid < zbytes) *(u4_t*)((uint8_t*)zst + 16 * tid) = zv;
+  __syncthreads();
+
+  const uint16_t* xa = xs + m * ldx + kbeg + 32 * q;
+  // constant B operands: ones, and (fp16) the operand's offset per position
+  const uint32_t one2 = vgpr_const(BF16 ? 0x3F803F80u : 0x3C003C00u);
+  const u4_t ones = {one2, one2, one2, one2};
+  const uint32_t o_lo = vgpr_const(0x64006400u), o_hi = vgpr_const(0x54005400u);
+  const u4_t offs = {o_lo, o_hi, o_lo, o_hi};
+  f4_t y[NTL];
+#pragma unroll
+  for (int t = 0; t < NTL; ++t) y[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    u4_t xo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xo[j] = *(const u4_t*)(xa + 128 * i + 8 * j);
+    // this chunk's row sums, sum x and (fp16) sum x * offset, for rows 4 q + e
+    f4_t xv4 = {0.f, 0.f, 0.f, 0.f}, xo4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xv4 = mfma16<BF16>(xo[j], ones, xv4);
+      if constexpr (!BF16) xo4 = mfma16<BF16>(xo[j], offs, xo4);
+    }
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) {
+      f4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u4_t w = wv[t][i];
+        const uint32_t wj = j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w;
+        const u4_t wop = BF16 ? w4_operand(wj, vmask, vmagic)
+                              : w4_operand_h(wj, vmask, vmask_hi, vmagic, vmagic_hi);
+        a = mfma16<BF16>(xo[j], wop, a);
+      }
+      const int gi = (16 * t + (lane & 15)) * nch + (kbeg >> 7) + i;
+      const float sc = raw_to_f32<SDT>(sst[gi]);
+      float z = 0.0f;
+      if constexpr (ZDT == 3) z = (float)((const uint8_t*)zst)[gi];
+      else if constexpr (ZDT >= 0) z = raw_to_f32<ZDT>(zst[gi]);
+      if constexpr (BF16) {
+        const float zb = w4_offset<BF16>() + z;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[t][e] += sc * (a[e] - zb * xv4[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[t][e] += sc * (a[e] - xo4[e] - z * xv4[e]);
+      }
+    }
+  }
+
+  // reduction over the waves through the X region ((NW - 1) * NTL KB <= M * ldx * 2)
+  __syncthreads();
+  f4_t* red = (f4_t*)xs;  // [NW - 1][NTL][64]
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) red[((wave - 1) * NTL + t) * 64 + lane] = y[t];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) {
+#pragma unroll
+      for (int w = 0; w < NW - 1; ++w) y[t] += red[(w * NTL + t) * 64 + lane];
+      const int n = nb + 16 * t + (lane & 15);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = 4 * q + e;
+        if (row < M) store_out(Y, (size_t)row * N + n, y[t][e] + bias_at(bias, n, BF16), BF16);
+      }
     }
   }
 }
@@ -1409,3 +1562,19 @@ TM_GEMV4_Z(false, f16, 4, 8)
 TM_GEMV4_Z(true, bf16, 4, 8)
 TM_GEMV4_Z(false, f16, 8, 8)
 TM_GEMV4_Z(true, bf16, 8, 8)
+
+// Two-tile GEMV (2 <= M <= 8, K = 4096, G = 128): wq_gemv4x2_<act>_z<zs>_w8p4,
+// 8 waves, two workgroups per CU (<= 128 VGPRs).
+#define TM_GEMV4XN(BF, ACT, ZS, ZDT, NTL, WPE)                                                  \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(WPE))) void   \
+      wq_gemv4x##NTL##_##ACT##_z##ZS##_w8p4(const uint16_t* X, const uint8_t* W, uint16_t* Y,   \
+                                            const uint16_t* S, const void* Z, int M, int N,     \
+                                            int K, const uint16_t* bias) {                      \
+    wq_gemv4x2_body<BF, ZDT, 8, 4, NTL>(X, W, Y, S, Z, M, N, K, bias);                          \
+  }
+#define TM_GEMV4XN_Z(BF, ACT, NTL, WPE)                              \
+  TM_GEMV4XN(BF, ACT, n, -1, NTL, WPE)                               \
+  TM_GEMV4XN(BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), NTL, WPE)    \
+  TM_GEMV4XN(BF, ACT, u, 3, NTL, WPE)
+TM_GEMV4XN_Z(false, f16, 2, 4)
+TM_GEMV4XN_Z(true, bf16, 2, 4)
