@@ -1,5 +1,6 @@
 // Typed entry points for KDA: the chunked forward (kda_intra + kda_state) and
 // the token-by-token recurrent form (kda_recurrent).
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -97,7 +98,10 @@ extern "C" int tm_kda_chunk_fwd(const void* q, const void* k, const void* v, con
   p.beta_bf16 = beta_dtype == TM_DT_BF16 ? 1 : 0;
 
   if (nc > 0) {
-    const int rc = launch(intra_kernel(), dim3((unsigned)(bh * nc)), dim3(256), 0, stream, p);
+    // one workgroup per CU (its LDS admits no second), each walking its share of
+    // the chunks
+    const long long grid = std::min<long long>(bh * nc, (long long)cu_count());
+    const int rc = launch(intra_kernel(), dim3((unsigned)grid), dim3(256), 0, stream, p);
     if (rc) return rc;
   }
   return launch(state_kernel(), dim3((unsigned)(bh * (kValueDim / 16))), dim3(256), 0, stream, p);

@@ -174,6 +174,22 @@ int max_dynamic_lds() {
   return attr;
 }
 
+int cu_count() {
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (current_device(&dev)) return 256;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int attr = 0;
+  if (g_api.DeviceGetAttribute(&attr, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      attr <= 0) {
+    g_api.GetLastError();
+    attr = 256;
+  }
+  cache[dev].store(attr, std::memory_order_relaxed);
+  return attr;
+}
+
 int Kernel::get(hipFunction_t* out) {
   int dev = 0;
   int rc = current_device(&dev);

@@ -62,6 +62,8 @@ class Kernel {
 int current_device(int* dev);
 // Largest dynamic LDS allocation per workgroup on the current device (bytes).
 int max_dynamic_lds();
+// Compute units of the current device (256 if the query fails).
+int cu_count();
 
 // Launch helper: args are passed by value and forwarded as kernelParams.
 template <class... Args>

@@ -105,7 +105,12 @@ struct KdaParams {
 };
 
 // ----------------------------------------------------------------------------
-// kda_intra: grid = B*H*NC (block index = bh * NC + chunk), block = 256.
+// kda_intra: chunk index = bh * NC + chunk; block = 256; any grid (at most one
+// workgroup fits a CU, so the host launches one per CU).  Each workgroup takes
+// chunks blockIdx.x, blockIdx.x + gridDim.x, ... and loads the next chunk's
+// g, k, v (after the current ones are staged in LDS) and q, beta (after the
+// current q is used) into registers while the current chunk computes, so the
+// loads, and the workspace stores of the chunk before, overlap its work.
 // MFMA 16x16x32 bf16 layouts (lane l, q = l/16): A[l%16][8q+e], B[8q+e][l%16],
 // D[4q+e][l%16].  MFMA 16x16x4 fp32: A[l%16][l/16], B[l/16][l%16], same D.
 // ----------------------------------------------------------------------------
@@ -129,47 +134,75 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, q4 = lane >> 4;
-  const int chunk = blockIdx.x % p.NC, bh = blockIdx.x / p.NC;
-  const int b = bh / p.H, h = bh - b * p.H;
-  const int t0 = chunk * KC;
-  const int nt = min(KC, p.T - t0);  // valid steps in this chunk
   const long long rs = (long long)p.H * KD;
   const long long rsv = (long long)p.H * VD;
-  const long long base_k = ((long long)b * p.T + t0) * rs + (long long)h * KD;
-  const long long base_v = ((long long)b * p.T + t0) * rsv + (long long)h * VD;
-  uint8_t* ws = p.ws + (size_t)blockIdx.x * WS_CHUNK;
   const u4_t z4 = {0u, 0u, 0u, 0u};
-
-  // ---- 1. loads: g (cumulative sum), k and v to LDS, q rows, beta ---------
   const int c4 = tid & 31, seg = tid >> 5;  // channels 4c4.., rows 8seg..8seg+7
-  f4_t gv[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int t = 8 * seg + e;
-    gv[e] = t < nt ? *(const f4_t*)(p.g + base_k + t * rs + 4 * c4) : f4_t{0.f, 0.f, 0.f, 0.f};
-  }
-  u4_t kr[4], vr[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = tid + 256 * j, row = i >> 4, c8 = i & 15;
-    kr[j] = row < nt ? ldg128(p.k + base_k + row * rs + 8 * c8) : z4;
-    vr[j] = row < nt ? ldg128(p.v + base_v + row * rsv + 8 * c8) : z4;
-  }
   const int r0 = 16 * wave;     // first row of this wave's 16-row block
   const int trow = r0 + l16;    // A-operand row of this lane
-  u4_t qr[4];
+  const int total = p.B * p.H * p.NC;
+
+  struct Chunk {
+    int b, h, t0, nt;
+    long long base_k, base_v;
+  };
+  auto locate = [&](int idx) {
+    Chunk c;
+    const int chunk = idx % p.NC, bh = idx / p.NC;
+    c.b = bh / p.H;
+    c.h = bh - c.b * p.H;
+    c.t0 = chunk * KC;
+    c.nt = min(KC, p.T - c.t0);  // valid steps in this chunk
+    c.base_k = ((long long)c.b * p.T + c.t0) * rs + (long long)c.h * KD;
+    c.base_v = ((long long)c.b * p.T + c.t0) * rsv + (long long)c.h * VD;
+    return c;
+  };
+  // input registers: g (this thread's 8 rows x 4 channels), k and v pieces,
+  // this lane's q row, beta of step tid
+  f4_t gv[8];
+  u4_t kr[4], vr[4], qr[4];
+  float bv = 0.0f;
+  auto load_gkv = [&](const Chunk& c) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-    qr[ks] = trow < nt ? ldg128(p.q + base_k + trow * rs + 32 * ks + 8 * q4) : z4;
-  if (tid < KC) {
-    float bv = 0.0f;
-    if (tid < nt) {
-      const long long bi = ((long long)b * p.T + t0 + tid) * p.H + h;
+    for (int e = 0; e < 8; ++e) {
+      const int t = 8 * seg + e;
+      gv[e] = t < c.nt ? *(const f4_t*)(p.g + c.base_k + t * rs + 4 * c4)
+                       : f4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid + 256 * j, row = i >> 4, c8 = i & 15;
+      kr[j] = row < c.nt ? ldg128(p.k + c.base_k + row * rs + 8 * c8) : z4;
+      vr[j] = row < c.nt ? ldg128(p.v + c.base_v + row * rsv + 8 * c8) : z4;
+    }
+  };
+  auto load_qb = [&](const Chunk& c) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qr[ks] = trow < c.nt ? ldg128(p.q + c.base_k + trow * rs + 32 * ks + 8 * q4) : z4;
+    bv = 0.0f;
+    if (tid < c.nt) {
+      const long long bi = ((long long)c.b * p.T + c.t0 + tid) * p.H + c.h;
       bv = p.beta_bf16 ? bf16_bits_to_f32(((const uint16_t*)p.beta)[bi])
                        : ((const float*)p.beta)[bi];
     }
-    bet[tid] = bv;
-  }
+  };
+
+  int idx = blockIdx.x;
+  if (idx >= total) return;
+  Chunk cur = locate(idx);
+  load_gkv(cur);
+  load_qb(cur);
+  for (;;) {
+  const int nidx = idx + (int)gridDim.x;
+  const bool has_next = nidx < total;
+  const Chunk nxt = locate(has_next ? nidx : idx);
+  const int nt = cur.nt;
+  const long long base_k = cur.base_k;
+  uint8_t* ws = p.ws + (size_t)idx * WS_CHUNK;
+
+  // ---- 1. g (cumulative sum), k and v to LDS, beta ---------------------------
+  if (tid < KC) bet[tid] = bv;
 #pragma unroll
   for (int e = 1; e < 8; ++e) gv[e] += gv[e - 1];
   *(f4_t*)&tot[seg][4 * c4] = gv[7];
@@ -186,6 +219,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) *(f4_t*)&Gs[8 * seg + e][4 * c4] = (gv[e] + pre) * kLog2e;
   }
+  if (has_next) load_gkv(nxt);  // g, k, v are in LDS now
   lds_barrier();
 
   // ---- 2. t-side operands, Qd, K_end^T, B^T, exp(G_C) ----------------------
@@ -212,6 +246,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
     qt_op[ks] = pack8_bf16(qt);
     *(u4_t*)(ws + WS_QD + frag_off(trow, 4 * ks + q4, 4)) = pack8_bf16(qd);
   }
+  if (has_next) load_qb(nxt);  // q and beta of this chunk are used
   // (c, 8-step group) tasks: K_end^T to the workspace, B^T to LDS
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -380,6 +415,11 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
         *(u2_t*)(ws + WS_WV + 8 * (tq * VD + cv)) = w;
       }
     }
+  }
+  if (!has_next) break;
+  idx = nidx;
+  cur = nxt;
+  __syncthreads();  // every wave is done with this chunk's LDS
   }
 }
 
