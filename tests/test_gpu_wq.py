@@ -105,7 +105,8 @@ INT4_KINDS = {"skinny": (8, 5120, 64), "gemv": (1, 4096, 64), "gemv8k": (8, 8192
               "gemv2t": (4, 4096, 64),
               "stream8": (8, 4096, 64), "stream16": (16, 2048, 64),
               "stream_multi": (40, 2048, 64), "tiled": (72, 512, 64), "wide": (100, 1024, 256)}
-INT8_KINDS = {"skinny": (8, 768, 64), "stream8": (8, 2048, 64), "stream16": (16, 2048, 64),
+INT8_KINDS = {"skinny": (8, 768, 64), "gemv": (1, 4096, 64), "stream8": (8, 2048, 64),
+              "stream16": (16, 2048, 64),
               "stream_multi": (40, 1024, 64), "tiled": (72, 512, 64), "wide": (100, 1024, 256)}
 
 
@@ -363,6 +364,20 @@ def test_int8_wide_shapes(dev, M, N, K):
     tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None, M, N, K)
     ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), None, M, N, K)
     check_close(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("N", [16, 208])
+@pytest.mark.parametrize("zeros", [False, True])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int8_gemv_shapes(dev, N, zeros, act):
+    """The int8 GEMV (M = 1, K = 4096), with and without per-channel zero-points."""
+    M, K = 1, 4096
+    x, w, s, z = make_int8_problem(M, N, K, seed=N + 7 * zeros, act=act, zeros=zeros or None)
+    out = torch.empty(M, N, dtype=act, device=dev)
+    tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None if z is None else z.to(dev),
+                   M, N, K)
+    ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
+    check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
 
 
 def test_int8_stream_u8_zero_points(dev):

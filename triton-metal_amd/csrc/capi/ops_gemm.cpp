@@ -134,6 +134,13 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
                     Z, M, N, K, bias);
     }
   }
+  // int8 GEMV: M = 1, K = 4096 (8 waves x 8 loads of 16 bytes per lane)
+  if (fast && qbits == 8 && M == 1 && K == 4096) {
+    char name[64];
+    snprintf(name, sizeof name, "wq_gemv8_%s_z%c_w8p8", act, zc);
+    return launch(kernel(name), dim3(N / 16), dim3(512), (unsigned)((K + 8) * 2), stream, X, W,
+                  Y, S, Z, M, N, K, bias);
+  }
   size_t lds = (size_t)M * (K + 8) * 2 + (size_t)M * (K / 128) * 4;
   if (fast && M <= 8 && K % (4 * CK) == 0 && lds <= (size_t)max_dynamic_lds()) {
     char name[64];

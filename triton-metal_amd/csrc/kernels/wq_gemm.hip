@@ -29,6 +29,7 @@
 //                resident, per-chunk MFMAs as the weights land.
 //   wq_gemv4x2_* int4, 2 <= M <= 6, K = 4096: the GEMV with two column tiles
 //                per workgroup and MFMA row sums.
+//   wq_gemv8_*   int8, M = 1, K = 4096: the GEMV layout for int8 weights.
 //   wq_stream_*  1 < M <= 64 (int4: 128), K <= 4096: weights and X streamed through LDS
 //                rings by global -> LDS copies, K split over the waves.
 //   wq_skinny_*  other M <= 8 shapes: the whole X[M, K] is staged once per
@@ -519,6 +520,89 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
     for (int e = 0; e < 4; ++e) {
       const int row = 4 * q + e;
       if (row < M) store_out(Y, (size_t)row * N + n, y[e] + bias_at(bias, n, BF16), BF16);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// int8 GEMV, M <= 8 (the exact shape K = NW * PF * 64): the int4 GEMV's layout
+// for int8 weights.  grid.x = N / 16, block = NW waves; wave w owns
+// k = w*PF*64 .. +PF*64 of the workgroup's 16 columns.  Lane (n, q) loads
+// 16 bytes at byte 64 i + 16 q of its column's segment (i < PF), so its MFMA
+// steps (i, h) cover k = 64 i + 16 q + 8 h + e in natural order - the order in
+// which X is staged and read.  Per-channel scale (and zero-point) once at the
+// end: Y = s * (sum x q - z * sum x), sum x from MFMAs of the X operands with
+// a ones operand.  Dynamic LDS: M * (K + 8) * 2 bytes of X.
+// ----------------------------------------------------------------------------
+template <bool BF16, int ZDT, int NW, int PF>
+__device__ __forceinline__ void wq_gemv8_body(const uint16_t* __restrict__ X,
+                                              const uint8_t* __restrict__ W,
+                                              uint16_t* __restrict__ Y,
+                                              const uint16_t* __restrict__ S,
+                                              const void* __restrict__ Z, int M, int N, int K,
+                                              const uint16_t* bias) {
+  constexpr int NT = NW * 64;
+  constexpr int SDT = BF16 ? TM_DT_BF16 : TM_DT_F16;
+  extern __shared__ __align__(16) uint16_t xs[];
+  __shared__ f4_t red[NW - 1][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ldx = K + 8;
+  const int n = blockIdx.x * 16 + (lane & 15), q = lane >> 4;
+  const int m = min(lane & 15, M - 1);
+  const int kbeg = wave * (PF * 64);
+
+  // 1. row 0 of X, this lane's channel scale / zero-point, 2. the weights,
+  // 3. stage X (later rows one at a time)
+  constexpr int XP = PF / 8;  // pieces per thread per row: K / 8 / NT
+  u4_t xv[XP];
+#pragma unroll
+  for (int u = 0; u < XP; ++u) xv[u] = ldg128(X + (size_t)(tid + NT * u) * 8);
+  const float sc = ld_typed<SDT>(S, (size_t)n);
+  const float z = ld_typed<ZDT>(Z, (size_t)n);
+  const uint8_t* wrow = W + (size_t)n * K + kbeg + 16 * q;
+  u4_t wv[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) wv[i] = ldg128(wrow + 64 * i);
+#pragma unroll
+  for (int u = 0; u < XP; ++u) *(u4_t*)(xs + (tid + NT * u) * 8) = xv[u];
+  for (int r = 1; r < M; ++r) {
+#pragma unroll
+    for (int u = 0; u < XP; ++u)
+      xv[u] = ldg128(X + (size_t)r * K + (size_t)(tid + NT * u) * 8);
+#pragma unroll
+    for (int u = 0; u < XP; ++u) *(u4_t*)(xs + r * ldx + (tid + NT * u) * 8) = xv[u];
+  }
+  __syncthreads();
+
+  const uint16_t* xa = xs + m * ldx + kbeg + 16 * q;
+  const uint32_t one2 = vgpr_const(BF16 ? 0x3F803F80u : 0x3C003C00u);
+  const u4_t ones = {one2, one2, one2, one2};
+  f4_t y = {0.f, 0.f, 0.f, 0.f}, xsum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u4_t xo = *(const u4_t*)(xa + 64 * i + 8 * h);
+      const u4_t w = wv[i];
+      y = mfma16<BF16>(xo, w8_operand<BF16>(h ? w.z : w.x, h ? w.w : w.y), y);
+      if constexpr (ZDT >= 0) xsum = mfma16<BF16>(xo, ones, xsum);
+    }
+  }
+  if constexpr (ZDT >= 0) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] -= z * xsum[e];
+  }
+
+  if (wave > 0) red[wave - 1][lane] = y;
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 0; w < NW - 1; ++w) y += red[w][lane];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = 4 * q + e;
+      if (row < M)
+        store_out(Y, (size_t)row * N + n, sc * y[e] + bias_at(bias, n, BF16), BF16);
     }
   }
 }
@@ -1578,3 +1662,19 @@ TM_GEMV4_Z(true, bf16, 8, 8)
   TM_GEMV4XN(BF, ACT, u, 3, NTL, WPE)
 TM_GEMV4XN_Z(false, f16, 2, 4)
 TM_GEMV4XN_Z(true, bf16, 2, 4)
+
+// int8 GEMV (K = 4096): wq_gemv8_<act>_z<zs>_w8p8; 8 waves per SIMD (<= 64
+// VGPRs), so the whole grid is resident.
+#define TM_GEMV8(BF, ACT, ZS, ZDT)                                                              \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8))) void     \
+      wq_gemv8_##ACT##_z##ZS##_w8p8(const uint16_t* X, const uint8_t* W, uint16_t* Y,           \
+                                    const uint16_t* S, const void* Z, int M, int N, int K,      \
+                                    const uint16_t* bias) {                                     \
+    wq_gemv8_body<BF, ZDT, 8, 8>(X, W, Y, S, Z, M, N, K, bias);                                 \
+  }
+#define TM_GEMV8_Z(BF, ACT)                              \
+  TM_GEMV8(BF, ACT, n, -1)                               \
+  TM_GEMV8(BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16))    \
+  TM_GEMV8(BF, ACT, u, 3)
+TM_GEMV8_Z(false, f16)
+TM_GEMV8_Z(true, bf16)
