@@ -109,6 +109,41 @@ def test_linear_shapes(dev, M, N, K, bias):
                                rtol=RTOL)
 
 
+# --- 256 x 256 tiles (M, N multiples of 256 with at least 192 tiles, K % 64 == 0) ----
+def _sample(n, k, seed):
+    return np.sort(np.random.default_rng(seed).choice(n, k, replace=False))
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 128), (3072, 4096, 192)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("out32", [False, True])
+def test_matmul_large_tiles(dev, M, N, K, dt, out32):
+    A, B = _rand((M, K), 11, dt), _rand((K, N), 12, dt)
+    C = torch.empty(M, N, dtype=torch.float32 if out32 else dt, device=dev)
+    tm.matmul(A.to(dev), B.to(dev), C, M, N, K)
+    rows, cols = _sample(M, 256, 1), _sample(N, 256, 2)
+    ref = oracle.matmul(A.float().numpy()[rows], B.float().numpy()[:, cols])
+    got = C.float().cpu().numpy()[np.ix_(rows, cols)]
+    atol = 1e-3 if out32 else ATOL * np.sqrt(K / 64)
+    np.testing.assert_allclose(got, ref, atol=atol, rtol=1e-4 if out32 else RTOL)
+
+
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_linear_large_tiles(dev, bias, dt):
+    M, N, K = 3072, 4096, 256
+    x, W = _rand((M, K), 13, dt), _rand((N, K), 14, dt)
+    b = _rand((N,), 15, dt) if bias else None
+    C = torch.empty(M, N, dtype=dt, device=dev)
+    tm.fused_linear(x.to(dev), W.to(dev), C, None if b is None else b.to(dev), M, N, K)
+    rows, cols = _sample(M, 256, 3), _sample(N, 256, 4)
+    ref = oracle.linear(x.float().numpy()[rows], W.float().numpy()[cols],
+                        None if b is None else b.float().numpy()[cols])
+    got = C.float().cpu().numpy()[np.ix_(rows, cols)]
+    np.testing.assert_allclose(got, ref, atol=ATOL * np.sqrt(K / 64) + (2e-2 if dt == torch.bfloat16 else 0),
+                               rtol=RTOL)
+
+
 def test_fp32_general_path(dev):
     M, N, K = 13, 17, 19
     A, B = _rand((M, K), 8, torch.float32), _rand((K, N), 9, torch.float32)

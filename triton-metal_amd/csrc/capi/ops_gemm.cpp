@@ -177,6 +177,19 @@ int dense(const void* A, const void* B, void* C, const void* bias, int M, int N,
   bool mfma = is_half(idt) && (odt == idt || odt == TM_DT_F32) && K % 8 == 0 && lda % 8 == 0 &&
               ldb % 8 == 0 && aligned16(A) && aligned16(B) && (bt || N % 8 == 0);
   if (mfma) {
+    // 256 x 256 tiles (gemm_big.hip) for large aligned problems: at least 192
+    // tiles, so that most CUs get one; the 32-bit copy offsets of a tile
+    // (up to 256 rows of A / B^T, 64 rows of B) must fit
+    const long t256 = (M % 256 == 0 && N % 256 == 0) ? (long)(M / 256) * (N / 256) : 0;
+    if (t256 >= 192 && K % 64 == 0 && 256LL * lda * 2 < (1LL << 32) &&
+        (bt ? 256LL : 64LL) * ldb * 2 < (1LL << 32)) {
+      char name[96];
+      snprintf(name, sizeof name, "gemm_t256_%s_%s_%s%s", bt ? "nt" : "nn",
+               idt == TM_DT_BF16 ? "bf16" : "f16", odt == TM_DT_F32 ? "f32" : "same",
+               (bt && bias) ? "_bias" : "");
+      return launch(kernel(name), dim3((unsigned)t256), dim3(512), 0, stream, A, B, C, bias, M,
+                    N, K, lda, ldb, ldc);
+    }
     const char* tile;
     long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
     long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
