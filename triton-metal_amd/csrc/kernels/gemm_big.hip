@@ -98,32 +98,49 @@ __device__ __forceinline__ void gemm_big_body(const uint16_t* __restrict__ A,
   const int tr_k = 8 * (tg >> 1) + (tj >> 2);        // + 16 kk (+ 4 for elements 4..7)
   const int tr_c = 16 * (tg & 1) + 4 * (tj & 3);     // + 64 wn + 32 ct
 
+  // operands of one 16-k substep: 4 A row tiles, 2 B column tiles
+  auto read_ops = [&](const uint16_t* as, const uint16_t* bs, int kk, u4_t* ao, u4_t* bo) {
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const int r = 128 * wm + 32 * rt + l32, p = 2 * kk + h32;
+      ao[rt] = *(const u4_t*)(as + r * GB_BK + 8 * (p ^ (r & 7)));
+    }
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      if constexpr (BT) {
+        const int r = 64 * wn + 32 * ct + l32, p = 2 * kk + h32;
+        bo[ct] = *(const u4_t*)(bs + r * GB_BK + 8 * (p ^ (r & 7)));
+      } else {
+        const int c = 64 * wn + 32 * ct + tr_c, pc = c >> 3, co = c & 7;
+        const int k0 = 16 * kk + tr_k, k1 = k0 + 4;
+        const u2_t lo = gb_tr16(bs + k0 * GB_BN + 8 * (pc ^ (4 * (k0 & 3))) + co);
+        const u2_t hi = gb_tr16(bs + k1 * GB_BN + 8 * (pc ^ (4 * (k1 & 3))) + co);
+        bo[ct] = u4_t{lo.x, lo.y, hi.x, hi.y};
+      }
+    }
+  };
+  // the operands of substep kk + 1 are read while substep kk multiplies
+  constexpr int NRD = BT ? 6 : 8;  // LDS reads per substep
   auto compute = [&](const uint16_t* as, const uint16_t* bs) {
+    u4_t ao[2][4], bo[2][2];
+    read_ops(as, bs, 0, ao[0], bo[0]);
 #pragma unroll
     for (int kk = 0; kk < GB_BK / 16; ++kk) {
-      u4_t ao[4], bo[2];
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        const int r = 128 * wm + 32 * rt + l32, p = 2 * kk + h32;
-        ao[rt] = *(const u4_t*)(as + r * GB_BK + 8 * (p ^ (r & 7)));
-      }
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        if constexpr (BT) {
-          const int r = 64 * wn + 32 * ct + l32, p = 2 * kk + h32;
-          bo[ct] = *(const u4_t*)(bs + r * GB_BK + 8 * (p ^ (r & 7)));
-        } else {
-          const int c = 64 * wn + 32 * ct + tr_c, pc = c >> 3, co = c & 7;
-          const int k0 = 16 * kk + tr_k, k1 = k0 + 4;
-          const u2_t lo = gb_tr16(bs + k0 * GB_BN + 8 * (pc ^ (4 * (k0 & 3))) + co);
-          const u2_t hi = gb_tr16(bs + k1 * GB_BN + 8 * (pc ^ (4 * (k1 & 3))) + co);
-          bo[ct] = u4_t{lo.x, lo.y, hi.x, hi.y};
-        }
-      }
+      if (kk + 1 < GB_BK / 16) read_ops(as, bs, kk + 1, ao[(kk + 1) & 1], bo[(kk + 1) & 1]);
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = mfma32<BF16>(ao[rt], bo[ct], acc[rt][ct]);
+        for (int ct = 0; ct < 2; ++ct)
+          acc[rt][ct] = mfma32<BF16>(ao[kk & 1][rt], bo[kk & 1][ct], acc[rt][ct]);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
+#pragma unroll
+    for (int kk = 0; kk < GB_BK / 16; ++kk) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (kk + 1 < GB_BK / 16 && j < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
     }
   };
 
