@@ -82,13 +82,6 @@ TM_DEV void store_as_f32_rt(void* p, long long i, int dt, float v) {
 
 // ---- MFMA wrappers ------------------------------------------------------------
 // The 8 x 16-bit operand of a 16x16x32 / 32x32x16 MFMA travels as 4 dwords.
-TM_DEV f4_t mfma16x16x32(u4_t a, u4_t b, f4_t c, bool bf16) {
-  if (bf16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a),
-                                                   __builtin_bit_cast(b8_t, b), c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
-                                                __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
-}
 template <bool BF16> TM_DEV f4_t mfma16(u4_t a, u4_t b, f4_t c) {
   if constexpr (BF16)
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8_t, a),
@@ -117,31 +110,25 @@ TM_DEV uint32_t h2_bits(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
 // Buffer-free 16-byte global load that the compiler keeps as one dwordx4.
 TM_DEV u4_t ldg128(const void* p) { return *(const u4_t*)p; }
 
-// Direct global -> LDS copy (global_load_lds_dwordx4): lane l of the wave
-// deposits the 16 bytes at g at LDS address lds_base + 16 l (lds_base must be
-// wave-uniform).  The copy is counted by vmcnt like a load.
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef const __attribute__((address_space(1))) void glb_void_t;
-TM_DEV void g2lds16(const void* g, void* lds_base) {
-  __builtin_amdgcn_global_load_lds((glb_void_t*)g, (lds_void_t*)lds_base, 16, 0, 0);
-}
 
 // Workgroup barrier for data exchanged through LDS alone: waits for this
 // wave's LDS operations (lgkmcnt) and meets the other waves, without draining
 // outstanding global loads, stores or global -> LDS copies as the fence of
 // __syncthreads() does.  The asm's memory clobber keeps the compiler from
-// moving memory accesses across it; reads of LDS filled by global -> LDS
-// copies still get their vmcnt wait from the compiler.
+// moving memory accesses across it; LDS filled by global -> LDS copies needs
+// the copying waves' own wait_vm before the barrier.
 TM_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Byte offset of an LDS location (the address a global -> LDS copy takes).
 TM_DEV uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)(lds_void_t*)p; }
 
-// Global -> LDS copies issued in asm: lane l deposits its 16 (4) bytes at LDS
-// byte offset lds + 16 l (4 l); lds must be wave-uniform.  The compiler does
-// not see these copies, so it adds no waits for them (with the builtin in a
-// function, every LDS read there waits for all earlier LDS reads, lgkmcnt(0),
-// instead of only for its own).  The caller waits with
+// Global -> LDS copies (global_load_lds_dwordx4 / _dword) issued in asm: lane
+// l deposits its 16 (4) bytes at LDS byte offset lds + 16 l (4 l); lds must be
+// wave-uniform.  The copies count in vmcnt like loads.  The compiler does not
+// see them, so it adds no waits for them (with the global_load_lds builtin in
+// a function, every LDS read there waits for all earlier LDS reads,
+// lgkmcnt(0), instead of only for its own).  The caller waits with
 // wait_vm<N>() - N = copies (and other vector memory operations) issued after
 // the awaited one - before reading the data, and must not overwrite LDS that
 // a copy still targets.  m0 is written here; the kernels that use these
