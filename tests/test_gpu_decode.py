@@ -55,10 +55,11 @@ def _check(dev, q, k, v, lens, scale, dtype, page_table=None, kp=None, vp=None, 
 
 
 # (B, Hq, Hkv, D, S): MFMA kernels (D 64/128, 16-bit caches) with one slice and
-# with many slices (long S, few heads), GQA groups below / above 16, and the
-# general kernel (other head dims)
+# with many slices (long S, few heads: up to 32 slices merge in one round of
+# loads, (1, 2, 1, 128, 9000) makes 36 and takes the looped merge), GQA groups
+# below / above 16, and the general kernel (other head dims)
 SHAPES = [(1, 8, 8, 128, 1000), (2, 32, 8, 128, 4096), (3, 12, 4, 64, 300),
-          (1, 40, 2, 128, 700), (2, 4, 4, 96, 100), (1, 2, 1, 64, 17)]
+          (1, 40, 2, 128, 700), (2, 4, 4, 96, 100), (1, 2, 1, 64, 17), (1, 2, 1, 128, 9000)]
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[str(s) for s in SHAPES])

@@ -282,6 +282,46 @@ extern "C" __global__ __launch_bounds__(64) void decode_attn_combine(DecodeParam
   const int bh = blockIdx.x, lane = threadIdx.x;
   const int D = p.D, ns = p.nsplit, RS = D + 4;
   const float* w = p.ws + (long long)bh * ns * RS;
+  if (ns <= 32 && D <= 128) {
+    // one round of loads: every slice's (max, sum) (the same address in every
+    // lane) and this lane's output elements, then the merge in registers
+    constexpr int MS = 32;
+    float mj[MS], lj[MS], oj[MS][2];
+#pragma unroll
+    for (int j = 0; j < MS; ++j) {
+      mj[j] = -INFINITY;
+      lj[j] = 0.0f;
+      oj[j][0] = oj[j][1] = 0.0f;
+      if (j < ns) {
+        const float* ws = w + j * RS;
+        mj[j] = ws[D];
+        lj[j] = ws[D + 1];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          if (lane + 64 * i < D) oj[j][i] = ws[lane + 64 * i];
+      }
+    }
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < MS; ++j) Mx = fmaxf(Mx, mj[j]);
+    const float mu = Mx == -INFINITY ? 0.0f : Mx;
+    float L = 0.0f, acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < MS; ++j) {
+      const float f = lj[j] > 0.0f ? __builtin_amdgcn_exp2f(mj[j] - mu) : 0.0f;
+      L += lj[j] * f;
+      acc[0] += oj[j][0] * f;
+      acc[1] += oj[j][1] * f;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int d = lane + 64 * i;
+      if (d < D) st_any(p.o, (long long)bh * D + d, p.o_dt, acc[i] * inv);
+    }
+    if (p.lse && lane == 0) p.lse[bh] = L > 0.0f ? (Mx + __log2f(L)) * kLn2f : -INFINITY;
+    return;
+  }
   float M = -INFINITY;
   for (int s = lane; s < ns; s += 64) M = fmaxf(M, w[s * RS + D]);
 #pragma unroll
