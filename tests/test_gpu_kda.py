@@ -174,6 +174,23 @@ def test_kda_config_c5_sampled_heads(dev):
         _close(st[:, sl], st_ref, f"final state head {h}")
 
 
+def test_kda_many_chunks_per_workgroup_partial_last_chunk(dev):
+    """More chunks than CUs (B=2, H=2, T=8300: 520 chunks, each head ending in
+    a 44-step chunk), so the intra-chunk workgroups walk several chunks each,
+    across head and batch boundaries: every (batch, head) against the fp64
+    recurrence."""
+    B, T, H = 2, 8300, 2
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=4)
+    o, st = _run(dev, q, k, v, g, beta)
+    for b in range(B):
+        for h in range(H):
+            bs, hs = slice(b, b + 1), slice(h, h + 1)
+            o_ref, st_ref = _ref(q[bs, :, hs], k[bs, :, hs], v[bs, :, hs], g[bs, :, hs],
+                                 beta[bs, :, hs])
+            _close(o[bs, :, hs], o_ref, f"o batch {b} head {h}")
+            _close(st[bs, hs], st_ref, f"final state batch {b} head {h}")
+
+
 # --- token-by-token (decoding) form -------------------------------------------------
 def _run_rec(dev, q, k, v, g, beta, s0=None, scale=None):
     d = lambda t: None if t is None else t.to(dev)
