@@ -144,6 +144,30 @@ def test_linear_large_tiles(dev, bias, dt):
                                rtol=RTOL)
 
 
+def test_matmul_large_tiles_padded_leading_dims(dev):
+    """The C ABI with row strides above the logical widths (lda > K, ldb > N,
+    ldc > N) on the 256 x 256-tile kernel: views into padded buffers."""
+    import ctypes
+    from triton_metal_amd import _lib
+    M, N, K = 4096, 3072, 128
+    lda, ldb, ldc = K + 64, N + 256, N + 128
+    Ap, Bp = _rand((M, lda), 16, torch.float16), _rand((K, ldb), 17, torch.float16)
+    Cp = torch.zeros(M, ldc, dtype=torch.float16, device=dev)
+    Ad, Bd = Ap.to(dev), Bp.to(dev)
+    L = _lib.lib()
+    rc = L.tm_matmul(ctypes.c_void_p(Ad.data_ptr()), ctypes.c_void_p(Bd.data_ptr()),
+                     ctypes.c_void_p(Cp.data_ptr()), M, N, K, lda, ldb, ldc,
+                     _lib.TM_DT_F16, _lib.TM_DT_F16, None)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    rows, cols = _sample(M, 256, 5), _sample(N, 256, 6)
+    ref = oracle.matmul(Ap[:, :K].float().numpy()[rows], Bp[:, :N].float().numpy()[:, cols])
+    got = Cp.float().cpu().numpy()
+    np.testing.assert_allclose(got[np.ix_(rows, cols)], ref, atol=ATOL * np.sqrt(K / 64),
+                               rtol=RTOL)
+    assert (got[:, N:] == 0).all()  # the padding columns of C are untouched
+
+
 def test_fp32_general_path(dev):
     M, N, K = 13, 17, 19
     A, B = _rand((M, K), 8, torch.float32), _rand((K, N), 9, torch.float32)
