@@ -369,7 +369,8 @@ def main():
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(every kernel here runs on one GPU's share; see DESIGN.md for sharding)",
+              "(every kernel here runs on one GPU's share of a sharded problem: W-only and "
+              "dense matmuls split over N, attention over batch x heads, KDA over heads)",
               file=sys.stderr)
         return 2
 
