@@ -126,13 +126,23 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
   // Work order.  Consecutive workgroups go round-robin to the 8 XCDs
   // (blockIdx % 8), each with its own L2.  When B*H % 8 == 0, every query
   // block of head bh runs on XCD bh % 8 and the heads of one XCD are taken
-  // one after another, so a head's K and V are fetched into that L2 once.
-  // Within a head the heaviest (causal) query blocks go first.
+  // two at a time, their query blocks alternating, so two heads' K and V are
+  // live in that L2 at once.  Within a pair the heaviest (causal) query blocks
+  // of both heads go first: taking one head at a time would start the next
+  // head's heaviest blocks while the last light blocks of the previous one
+  // run, and the causal grid would end with long blocks on a few CUs.
   int qslot, bh;
   if ((BH & 7) == 0) {
     const int x = blockIdx.x & 7, sl = blockIdx.x >> 3;
-    bh = x + 8 * (sl / nqb);
-    qslot = sl % nqb;
+    const int hpx = BH >> 3;  // heads per XCD
+    const int pair = sl / (2 * nqb), r = sl - pair * (2 * nqb);
+    if (2 * pair + 1 < hpx) {
+      bh = x + 8 * (2 * pair + (r & 1));
+      qslot = r >> 1;
+    } else {  // an odd count leaves the last head alone: r < nqb
+      bh = x + 8 * (2 * pair);
+      qslot = r;
+    }
   } else {
     bh = blockIdx.x % BH;
     qslot = blockIdx.x / BH;
