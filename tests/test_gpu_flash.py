@@ -118,6 +118,20 @@ def test_flash_custom_scale_and_closed_forms(dev):
     assert torch.equal(o[:, :, 0], v[:, :, 0])    # row 0 sees only key 0
 
 
+@pytest.mark.parametrize("B,H", [(1, 24), (2, 8), (1, 40)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_every_head_xcd_pairing(dev, B, H, causal):
+    """B*H a multiple of 8 takes the work order that gives each XCD its heads
+    two at a time (3 and 5 heads per XCD leave the last one alone, 2 pairs
+    them): every (batch, head) and every query block against the oracle."""
+    S, D = 300, 128
+    q, k, v = (_rand((B, H, S, D), s, torch.bfloat16, dev) for s in (31, 32, 33))
+    o, lse = tm.attention(q, k, v, causal=causal, return_lse=True)
+    ref, ref_lse = _ref(q, k, v, causal)
+    np.testing.assert_allclose(o.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
+
+
 # --- benchmark configuration C4 (sampled rows against the oracle) -----------------
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_config_c4(dev, causal):
