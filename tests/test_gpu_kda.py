@@ -243,3 +243,26 @@ def test_kda_recurrent_zero_steps_copies_state(dev):
     o, st = _run_rec(dev, q, k, v, g, beta, s0=s0)
     assert o.shape == (B, 0, H, 128)
     np.testing.assert_array_equal(st, s0.numpy())
+
+
+def test_kda_recurrent_unaligned_state_buffers(dev):
+    """State buffers 16-byte aligned take the kernel with 16-byte state
+    accesses, buffers at a 4-byte offset the one with 4-byte accesses: both,
+    updating the state in place, against the fp64 recurrence."""
+    B, T, H = 2, 3, 3
+    q, k, v, g, beta = kda_inputs(B, T, H, seed=75)
+    s0 = torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(76)) * 0.5
+    o_ref, st_ref = _ref(q, k, v, g, beta, s0=s0)
+    n = B * H * 128 * 128
+    d = lambda t: t.to(dev).contiguous()
+    for off in (0, 1):
+        buf = torch.zeros(n + 4, device=dev)
+        st = buf[off:off + n].view(B, H, 128, 128)
+        st.copy_(s0.to(dev))
+        assert (st.data_ptr() % 16 == 0) == (off == 0)
+        o = torch.empty(B, T, H, 128, dtype=torch.bfloat16, device=dev)
+        tm.plan_fused_recurrent_kda(d(q), d(k), d(v), d(g), d(beta), o, initial_state=st,
+                                    final_state=st)()
+        torch.cuda.synchronize()
+        _close(o.float().cpu().numpy(), o_ref, f"o, state offset {off}")
+        _close(st.cpu().numpy(), st_ref, f"final state, state offset {off}")

@@ -41,6 +41,10 @@ Kernel& recurrent_kernel() {
   static Kernel k("kda_recurrent");
   return k;
 }
+Kernel& recurrent_v4_kernel() {
+  static Kernel k("kda_recurrent_v4");
+  return k;
+}
 
 }  // namespace
 
@@ -141,7 +145,10 @@ extern "C" int tm_kda_recurrent_fwd(const void* q, const void* k, const void* v,
   p.B = batch; p.T = seq_len; p.H = heads;
   p.scale = scale;
   p.beta_bf16 = beta_dtype == TM_DT_BF16 ? 1 : 0;
-  // one wave per (head, 16 value columns)
-  return launch(recurrent_kernel(), dim3((unsigned)((long long)batch * heads * (kValueDim / 16))),
-                dim3(64), 0, stream, p);
+  // one wave per (head, 16 value columns); 16-byte state accesses when both
+  // state buffers (or null) are 16-byte aligned
+  const bool v4 = ((reinterpret_cast<uintptr_t>(initial_state) |
+                    reinterpret_cast<uintptr_t>(final_state)) & 15) == 0;
+  return launch(v4 ? recurrent_v4_kernel() : recurrent_kernel(),
+                dim3((unsigned)((long long)batch * heads * (kValueDim / 16))), dim3(64), 0, stream, p);
 }
