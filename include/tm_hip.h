@@ -198,8 +198,11 @@ int tm_flash_attention(const void* q, const void* k, const void* v, void* o, flo
  * workspace: scratch for per-slice partials of long sequences, at least
  * tm_decode_attention_workspace_size(...) bytes (NULL or smaller: no slices).
  * fp16 / bf16 caches with head_dim 64 or 128 run on MFMA kernels; everything
- * else (head_dim <= 256) on an fp32 kernel.  With an fp32 query and a 16-bit
- * cache the MFMA kernels round the query to the cache dtype. */
+ * else (head_dim <= 256) on an fp32 kernel.  With a query dtype other than
+ * the cache's (an fp32 query over a 16-bit cache, as
+ * make_fp16_kv_attention_kernel, _msl_templates.py:2558-2576, computes it) the
+ * MFMA kernels carry the query and the softmax weights as hi + lo pairs of
+ * cache-dtype operands, keeping fp32-level accuracy. */
 size_t tm_decode_attention_workspace_size(int batch, int q_heads, int kv_heads, int head_dim,
                                           int seq_len, int page_size);
 int tm_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,

@@ -97,3 +97,15 @@ def test_kda_workspace_and_validation():
     # no heads: nothing to do
     assert lib.tm_kda_chunk_fwd(*args, 1, 64, 0, 128, 128, 64, 0.1, L.TM_DT_F32, p, 0,
                                 None) == 0
+
+
+def test_int8_matmul_rejects_uint8_weights():
+    """The kernels read the weight bytes as signed int8 (the reference's
+    `device const char*`); uint8 storage is refused rather than misread."""
+    import torch
+    import triton_metal_amd as tm
+    x = torch.zeros(1, 64, dtype=torch.float16)
+    w = torch.zeros(16, 64, dtype=torch.uint8)
+    with pytest.raises(TypeError, match="int8"):
+        tm.int8_matmul(x, w, torch.zeros(1, 16, dtype=torch.float16),
+                       torch.ones(16, dtype=torch.float16), None, 1, 16, 64)

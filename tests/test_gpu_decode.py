@@ -184,4 +184,54 @@ def test_reference_template_wrappers(dev):
     tm.make_fp16_kv_attention_kernel(D)(Q.to(dev), Kc.to(dev), Vc.to(dev), O, 150)
     ref, _ = oracle.decode_attention(Q[None, None].numpy(), Kc[None, None].float().numpy(),
                                      Vc[None, None].float().numpy(), [150], D ** -0.5)
-    np.testing.assert_allclose(O.cpu().numpy(), ref[0, 0], atol=2e-2, rtol=1e-2)
+    # the reference computes in fp32 throughout (an fp32 query against float(half K))
+    np.testing.assert_allclose(O.cpu().numpy(), ref[0, 0], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D,S", [(64, 150), (128, 3000)])
+def test_decode_fp32_query_exact(dev, kv_dtype, D, S):
+    """fp32 queries and outputs over a 16-bit cache (the fp16_kv_attention
+    contract) keep fp32 accuracy on the MFMA path, one slice and many, GQA."""
+    g = _gen(21)
+    B, Hq, Hkv = 2, 8, 2
+    q = torch.randn(B, Hq, D, generator=g) * 2.0
+    k = torch.randn(B, Hkv, S, D, generator=g).to(kv_dtype)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(kv_dtype)
+    lens = torch.tensor([S, S // 3], dtype=torch.int32)
+    o = torch.empty(B, Hq, D, dtype=torch.float32, device=dev)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=dev)
+    tm.decode_attention(q.to(dev), k.to(dev), v.to(dev), seq_lens=lens.to(dev), o=o, lse=lse)
+    ref, ref_l = oracle.decode_attention(q.numpy(), k.float().numpy(), v.float().numpy(),
+                                         lens.tolist(), D ** -0.5)
+    np.testing.assert_allclose(o.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_l, atol=1e-4, rtol=1e-5)
+
+
+def test_reference_wrappers_capacity_beyond_seq_len(dev):
+    """kv_cache_attention / gqa_attention space heads by seq_len as the
+    reference does (head_offset_kv = pid * seq_len * D), also when the buffers
+    hold more positions than seq_len."""
+    D, S, cap = 64, 100, 160
+    g = _gen(23)
+    H = 4
+    Q = torch.randn(H, D, generator=g).half()
+    flatK = torch.randn(H * cap * D, generator=g).half()
+    flatV = torch.randn(H * cap * D, generator=g).half()
+    O = torch.empty(H, D, dtype=torch.float16, device=dev)
+    tm.make_kv_cache_attention_kernel(D)(Q.to(dev), flatK.to(dev), flatV.to(dev), O, S, 0.2)
+    Kr = flatK[:H * S * D].view(H, S, D)
+    Vr = flatV[:H * S * D].view(H, S, D)
+    ref, _ = oracle.decode_attention(Q[None].float().numpy(), Kr[None].float().numpy(),
+                                     Vr[None].float().numpy(), [S], 0.2)
+    np.testing.assert_allclose(O.float().cpu().numpy(), ref[0], atol=2e-2, rtol=1e-2)
+    Hq, n = 8, 4
+    Q = torch.randn(Hq, D, generator=g).half()
+    O = torch.empty(Hq, D, dtype=torch.float16, device=dev)
+    tm.make_gqa_attention_kernel(D, n_q_per_kv=n)(Q.to(dev), flatK.to(dev), flatV.to(dev), O, S,
+                                                  0.2)
+    Kr = flatK[:(Hq // n) * S * D].view(Hq // n, S, D)
+    Vr = flatV[:(Hq // n) * S * D].view(Hq // n, S, D)
+    ref, _ = oracle.decode_attention(Q[None].float().numpy(), Kr[None].float().numpy(),
+                                     Vr[None].float().numpy(), [S], 0.2)
+    np.testing.assert_allclose(O.float().cpu().numpy(), ref[0], atol=2e-2, rtol=1e-2)

@@ -83,8 +83,7 @@ def test_matmul_shapes(dev, M, N, K, dt):
     C = torch.empty(M, N, dtype=dt, device=dev)
     tm.matmul(A.to(dev), B.to(dev), C, M, N, K)
     ref = oracle.matmul(A.float().numpy(), B.float().numpy())
-    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=ATOL * np.sqrt(K / 64),
-                               rtol=RTOL)
+    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
 
 
 def test_matmul_c1_fp16_fp32_out(dev):
@@ -105,8 +104,7 @@ def test_linear_shapes(dev, M, N, K, bias):
     tm.fused_linear(x.to(dev), W.to(dev), C, None if b is None else b.to(dev), M, N, K)
     ref = oracle.linear(x.float().numpy(), W.float().numpy(),
                         None if b is None else b.float().numpy())
-    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=ATOL * np.sqrt(K / 64),
-                               rtol=RTOL)
+    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
 
 
 # --- 256 x 256 tiles (M, N multiples of 256 with at least 192 tiles, K % 64 == 0) ----
@@ -124,7 +122,7 @@ def test_matmul_large_tiles(dev, M, N, K, dt, out32):
     rows, cols = _sample(M, 256, 1), _sample(N, 256, 2)
     ref = oracle.matmul(A.float().numpy()[rows], B.float().numpy()[:, cols])
     got = C.float().cpu().numpy()[np.ix_(rows, cols)]
-    atol = 1e-3 if out32 else ATOL * np.sqrt(K / 64)
+    atol = 1e-3 if out32 else ATOL
     np.testing.assert_allclose(got, ref, atol=atol, rtol=1e-4 if out32 else RTOL)
 
 
@@ -140,8 +138,7 @@ def test_linear_large_tiles(dev, bias, dt):
     ref = oracle.linear(x.float().numpy()[rows], W.float().numpy()[cols],
                         None if b is None else b.float().numpy()[cols])
     got = C.float().cpu().numpy()[np.ix_(rows, cols)]
-    np.testing.assert_allclose(got, ref, atol=ATOL * np.sqrt(K / 64) + (2e-2 if dt == torch.bfloat16 else 0),
-                               rtol=RTOL)
+    np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
 
 
 def test_matmul_large_tiles_padded_leading_dims(dev):
@@ -163,8 +160,7 @@ def test_matmul_large_tiles_padded_leading_dims(dev):
     rows, cols = _sample(M, 256, 5), _sample(N, 256, 6)
     ref = oracle.matmul(Ap[:, :K].float().numpy()[rows], Bp[:, :N].float().numpy()[:, cols])
     got = Cp.float().cpu().numpy()
-    np.testing.assert_allclose(got[np.ix_(rows, cols)], ref, atol=ATOL * np.sqrt(K / 64),
-                               rtol=RTOL)
+    np.testing.assert_allclose(got[np.ix_(rows, cols)], ref, atol=ATOL, rtol=RTOL)
     assert (got[:, N:] == 0).all()  # the padding columns of C are untouched
 
 

@@ -4,11 +4,22 @@ The reference has no linear attention, so KDA parity is pinned by the oracle's
 own checks (recurrent vs chunked restatements and closed forms) and, here, by
 the kernel against the fp64 token-by-token recurrence on the same bf16 inputs.
 
-Tolerance (rtol 2e-2 for outputs and final state), written per element as
-    |got - ref| <= 2e-2 * |ref| + 2e-2 * max|ref|
-over each compared tensor: the kernel computes in bf16 MFMA operands with
-fp32 accumulation and an fp32 state, so near-zero entries carry an error set
-by the tensor's scale rather than their own.
+Tolerance (rtol 2e-2 for outputs and final state), per element:
+    |got - ref| <= 2e-2 * |ref| + 4u * max|ref|,   u = 2^-9 (bf16 unit roundoff)
+over each compared tensor, plus an aggregate bound on the relative RMS error
+    ||got - ref||_2 / ||ref||_2 <= 3u.
+The kernels round their MFMA operands to bf16 and accumulate in fp32.  An
+output entry is a signed sum of rounded products, so its error scales with the
+magnitude of the terms, not with the entry itself, which can be near zero
+after cancellation: a purely relative bound means nothing there.  The
+chunked form passes o through four bf16 roundings in sequence (the operands
+and result of Aqk, W_v = T beta v, U = W_v - W_k S), each worth about u of
+the terms' magnitude, which the tensor's largest entry bounds: hence the 4u
+floor.  A CPU model of exactly these roundings, run against the fp64
+recurrence on the C5 recipe, gives a relative RMS error of 4.1e-3 and a worst
+element at 1.9x a 1e-3 * max|ref| floor, which is what the GPU shows; the RMS
+bound keeps the typical error at that level.  Every comparison prints its
+worst error/tolerance ratio and its relative RMS error.
 """
 import numpy as np
 import pytest
@@ -20,15 +31,26 @@ import triton_metal_amd as tm
 
 pytestmark = pytest.mark.gpu
 RTOL = 2e-2
+U_BF16 = 2.0 ** -9
 
 
 def _close(got, ref, what):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
-    tol = RTOL * np.abs(ref) + RTOL * np.abs(ref).max()
-    bad = np.abs(got - ref) > tol
+    if ref.ndim == 0 or ref.size == 0:
+        ref, got = ref.reshape(1, -1), got.reshape(1, -1)
+    tol = RTOL * np.abs(ref) + 4 * U_BF16 * np.abs(ref).max()
+    err = np.abs(got - ref)
+    ratio = float((err / np.maximum(tol, 1e-300)).max())
+    nref = np.sqrt((ref ** 2).sum())
+    rms = float(np.sqrt((err ** 2).sum()) / nref) if nref > 0 else float(np.sqrt((err ** 2).sum()))
+    print(f"[kda tol] {what}: worst err/tol {ratio:.3f}, rel rms {rms:.2e}, "
+          f"max err {err.max():.3e}, max|ref| {np.abs(ref).max():.3e}", flush=True)
+    bad = err > tol
     assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside tolerance, "
-                           f"max err {np.abs(got - ref).max():.3e}, max|ref| {np.abs(ref).max():.3e}")
+                           f"worst err/tol {ratio:.3f}, max err {err.max():.3e}, "
+                           f"max|ref| {np.abs(ref).max():.3e}")
+    assert rms <= 3 * U_BF16, f"{what}: relative RMS error {rms:.2e} > {3 * U_BF16:.2e}"
 
 
 def kda_inputs(B, T, H, seed=0, gscale=1.0, beta_bf16=False):

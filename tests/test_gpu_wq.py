@@ -272,7 +272,7 @@ def test_int4_bf16_activations(dev, M):
     out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev), z.to(dev), M, N, K, G)
     ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
-    check_close(out.cpu(), ref, atol=3e-2, rtol=1e-2)
+    check_close(out.cpu(), ref, atol=ATOL, rtol=RTOL)
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (16, 128, 512), (3, 40, 100), (70, 64, 256)])
@@ -297,7 +297,7 @@ def test_int4_two_tile_gemv_shapes(dev, M, N, zeros, act):
     tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
                    None if z is None else z.to(dev), M, N, K, G)
     ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
-    check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
+    check_close(out.cpu(), ref, atol=ATOL)
 
 
 def test_int4_two_tile_gemv_fractional_zero_points(dev):
@@ -327,7 +327,7 @@ def test_int4_stream_shapes(dev, M, N, K, zeros, act):
     tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
                    None if z is None else z.to(dev), M, N, K, G)
     ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)
-    check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
+    check_close(out.cpu(), ref, atol=ATOL)
 
 
 @pytest.mark.parametrize("M,N,K", [(2, 48, 512), (8, 208, 4096), (9, 32, 1024), (16, 96, 4096),
@@ -340,7 +340,7 @@ def test_int8_stream_shapes(dev, M, N, K, zeros, act):
     tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None if z is None else z.to(dev),
                    M, N, K)
     ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
-    check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
+    check_close(out.cpu(), ref, atol=ATOL)
 
 
 @pytest.mark.parametrize("M,N,K", [(65, 128, 512), (128, 256, 4096), (200, 384, 2048),
@@ -377,7 +377,7 @@ def test_int8_gemv_shapes(dev, N, zeros, act):
     tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None if z is None else z.to(dev),
                    M, N, K)
     ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
-    check_close(out.cpu(), ref, atol=3e-2 if act == torch.bfloat16 else ATOL)
+    check_close(out.cpu(), ref, atol=ATOL)
 
 
 def test_int8_stream_u8_zero_points(dev):

@@ -139,9 +139,13 @@ extern "C" int tm_decode_attention(const void* q, const void* k_cache, const voi
       p.nsplit = ns; p.split_len = sl;
       p.ws = (float*)workspace;
       const int group = q_heads / kv_heads, hbn = (group + 15) / 16;
-      static Kernel* k128[2] = {new Kernel("decode_attn_d128_f16"), new Kernel("decode_attn_d128_bf16")};
-      static Kernel* k64[2] = {new Kernel("decode_attn_d64_f16"), new Kernel("decode_attn_d64_bf16")};
-      Kernel& kk = *(head_dim == 128 ? k128 : k64)[kv_dtype == TM_DT_BF16 ? 1 : 0];
+      // [head dim][cache dtype][query dtype other than the cache's: hi + lo split]
+      static Kernel* kd[2][2][2] = {
+          {{new Kernel("decode_attn_d64_f16"), new Kernel("decode_attn_d64_f16_x")},
+           {new Kernel("decode_attn_d64_bf16"), new Kernel("decode_attn_d64_bf16_x")}},
+          {{new Kernel("decode_attn_d128_f16"), new Kernel("decode_attn_d128_f16_x")},
+           {new Kernel("decode_attn_d128_bf16"), new Kernel("decode_attn_d128_bf16_x")}}};
+      Kernel& kk = *kd[head_dim == 128][kv_dtype == TM_DT_BF16][q_dtype != kv_dtype];
       const unsigned lds = 3u * 2u * 32u * (unsigned)head_dim * 2u;
       int rc = launch(kk, dim3(ns, kv_heads * hbn, batch), dim3(64), lds, stream, p);
       if (rc || ns == 1) return rc;

@@ -131,25 +131,25 @@ TM_DEV uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)(lds_void_t
 // lgkmcnt(0), instead of only for its own).  The caller waits with
 // wait_vm<N>() - N = copies (and other vector memory operations) issued after
 // the awaited one - before reading the data, and must not overwrite LDS that
-// a copy still targets.  m0 is written here; the kernels that use these
-// helpers use m0 for nothing else.  A global load into LDS needs one wait
+// a copy still targets.  m0 is written here and declared clobbered, so the
+// compiler keeps none of its own values in m0 across a copy.  A global load into LDS needs one wait
 // state after the write of m0 it reads (an s_nop 0 between the two).
 TM_DEV void dma16(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g),
                "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
+               : "memory", "m0");
 }
 // The same copy from a wave-uniform base plus a 32-bit byte offset per lane
 // (one VGPR per copy instead of a 64-bit address pair).
 TM_DEV void dma16s(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base),
                "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
+               : "memory", "m0");
 }
 TM_DEV void dma4(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g),
                "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
+               : "memory", "m0");
 }
 // Wait until at most N vector memory operations of this wave are outstanding
 // (they complete in issue order).

@@ -65,6 +65,24 @@ TM_DEV u2_t tr16(const uint16_t* p) {
   return __builtin_bit_cast(u2_t, v);
 }
 
+// Eight fp32 values as hi + lo pairs of 16-bit operands: hi = round(f),
+// lo = round(f - hi) (f - hi is exact in fp32).
+template <bool BF16> TM_DEV void split_pack(const float* f, u4_t& hi, u4_t& lo) {
+  float r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    r[e] = BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(f[e])) : f16_bits_to_f32(f32_to_f16_bits(f[e]));
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = BF16 ? pack_bf16x2(f[2 * i], f[2 * i + 1]) : pack_f16x2(f[2 * i], f[2 * i + 1]);
+    const float d0 = f[2 * i] - r[2 * i], d1 = f[2 * i + 1] - r[2 * i + 1];
+    l[i] = BF16 ? pack_bf16x2(d0, d1) : pack_f16x2(d0, d1);
+  }
+  hi = u4_t{h[0], h[1], h[2], h[3]};
+  lo = u4_t{l[0], l[1], l[2], l[3]};
+}
+
 TM_DEV int seq_len_of(const DecodeParams& p, int b) {
   return p.seq_lens ? min(p.seq_lens[b], p.seq_len) : p.seq_len;
 }
@@ -86,7 +104,14 @@ TM_DEV void st_any(void* ptr, long long i, int dt, float v) {
 // Per-wave LDS ring of NST stages, each [32 positions][D] of K then of V, row
 // piece c (16 bytes) of position row r stored at slot c ^ (r & (D / 8 - 1)).
 // ----------------------------------------------------------------------------
-template <int D, bool BF16>
+// SPLIT (a query dtype other than the cache's, e.g. fp32 queries over a
+// 16-bit cache as make_fp16_kv_attention_kernel takes them): the query and the
+// probabilities each travel as a pair hi + lo of cache-dtype operands,
+// hi = round(x), lo = round(x - hi), and every product is two MFMAs.  The
+// pair carries 22 (fp16) or 16 (bf16) significant bits, so scores and the
+// weighted sum keep fp32-level accuracy against the fp32 computation of the
+// reference template instead of one 16-bit rounding of q and P.
+template <int D, bool BF16, bool SPLIT>
 __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
   constexpr int NST = 3;
   constexpr int PR = D / 8;             // 16-byte pieces per row
@@ -105,23 +130,22 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
   const int hq = kvh * group + 16 * hb + l16;    // this lane's query head
   const bool hvalid = 16 * hb + l16 < group;
 
-  // Q^T operand: q[b, hq, 32 ks + 8 q4 .. +8] in the cache dtype
-  u4_t qop[KS];
+  // Q^T operand: q[b, hq, 32 ks + 8 q4 .. +8] in the cache dtype (SPLIT: its
+  // hi and lo parts)
+  u4_t qop[KS], qlo[SPLIT ? KS : 1];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     qop[ks] = u4_t{0u, 0u, 0u, 0u};
+    if constexpr (SPLIT) qlo[ks] = u4_t{0u, 0u, 0u, 0u};
     if (hvalid) {
       const long long qi = ((long long)b * p.Hq + hq) * D + 32 * ks + 8 * q4;
-      if (p.q_dt == p.kv_dt) {
+      if constexpr (!SPLIT) {
         qop[ks] = ldg128((const uint16_t*)p.q + qi);
       } else {
         float f[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) f[e] = ld_any(p.q, qi + e, p.q_dt);
-        qop[ks].x = BF16 ? pack_bf16x2(f[0], f[1]) : pack_f16x2(f[0], f[1]);
-        qop[ks].y = BF16 ? pack_bf16x2(f[2], f[3]) : pack_f16x2(f[2], f[3]);
-        qop[ks].z = BF16 ? pack_bf16x2(f[4], f[5]) : pack_f16x2(f[4], f[5]);
-        qop[ks].w = BF16 ? pack_bf16x2(f[6], f[7]) : pack_f16x2(f[6], f[7]);
+        split_pack<BF16>(f, qop[ks], qlo[ks]);
       }
     }
   }
@@ -192,6 +216,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
       for (int ks = 0; ks < KS; ++ks) {
         const u4_t a = *(const u4_t*)(ks_ + r * D + 8 * ((4 * ks + q4) ^ (r & (PR - 1))));
         s[kb] = mfma16<BF16>(a, qop[ks], s[kb]);
+        if constexpr (SPLIT) s[kb] = mfma16<BF16>(a, qlo[ks], s[kb]);
       }
     }
     // positions of this lane's scores: 32 t + 16 kb + 4 q4 + e
@@ -220,11 +245,15 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
       ps += pv[i];
     }
     l_run = l_run * alpha + ps;
-    u4_t pop;
-    pop.x = BF16 ? pack_bf16x2(pv[0], pv[1]) : pack_f16x2(pv[0], pv[1]);
-    pop.y = BF16 ? pack_bf16x2(pv[2], pv[3]) : pack_f16x2(pv[2], pv[3]);
-    pop.z = BF16 ? pack_bf16x2(pv[4], pv[5]) : pack_f16x2(pv[4], pv[5]);
-    pop.w = BF16 ? pack_bf16x2(pv[6], pv[7]) : pack_f16x2(pv[6], pv[7]);
+    u4_t pop, plo;
+    if constexpr (SPLIT) {
+      split_pack<BF16>(pv, pop, plo);
+    } else {
+      pop.x = BF16 ? pack_bf16x2(pv[0], pv[1]) : pack_f16x2(pv[0], pv[1]);
+      pop.y = BF16 ? pack_bf16x2(pv[2], pv[3]) : pack_f16x2(pv[2], pv[3]);
+      pop.z = BF16 ? pack_bf16x2(pv[4], pv[5]) : pack_f16x2(pv[4], pv[5]);
+      pop.w = BF16 ? pack_bf16x2(pv[6], pv[7]) : pack_f16x2(pv[6], pv[7]);
+    }
     // O^T += V^T P^T: lane j of 16-lane group q4 addresses row 4 q4 + j / 4
     // (+16 for the second half), d chunk 16 dt + 4 (j % 4)
 #pragma unroll
@@ -237,6 +266,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
       u4_t a;
       a.x = lo.x; a.y = lo.y; a.z = hi.x; a.w = hi.y;
       oacc[dt] = mfma16<BF16>(a, pop, oacc[dt]);
+      if constexpr (SPLIT) oacc[dt] = mfma16<BF16>(a, plo, oacc[dt]);
     }
   }
   wait_vm<0>();
@@ -264,9 +294,12 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
   }
 }
 
-#define TM_DECODE(D, DT, BF)                                                                 \
-  extern "C" __global__ __launch_bounds__(64) void decode_attn_d##D##_##DT(DecodeParams p) { \
-    decode_mfma_body<D, BF>(p);                                                              \
+#define TM_DECODE(D, DT, BF)                                                                   \
+  extern "C" __global__ __launch_bounds__(64) void decode_attn_d##D##_##DT(DecodeParams p) {   \
+    decode_mfma_body<D, BF, false>(p);                                                         \
+  }                                                                                            \
+  extern "C" __global__ __launch_bounds__(64) void decode_attn_d##D##_##DT##_x(DecodeParams p) { \
+    decode_mfma_body<D, BF, true>(p);                                                          \
   }
 TM_DECODE(128, f16, false)
 TM_DECODE(128, bf16, true)

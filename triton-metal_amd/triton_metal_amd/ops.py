@@ -131,12 +131,14 @@ class Kernel:
 # ---------------------------------------------------------------------------
 def plan_int8_matmul(input, weight, output, scales, zeros, M, N, K, stream=None) -> Launch:
     """Validate and bind an int8_matmul call (see int8_matmul)."""
+    if weight.dtype != torch.int8:
+        # the kernels read signed bytes (the reference's `device const char*`);
+        # uint8 storage of the same bytes must be passed as weight.view(torch.int8)
+        raise TypeError(f"weight must be int8, got {weight.dtype}")
     dev = _device_of(input, weight, output, scales, zeros)
     for t, w in ((input, "input"), (weight, "weight"), (output, "output"), (scales, "scales"),
                  (zeros, "zeros")):
         _need_contig(t, w)
-    if weight.dtype not in (torch.int8, torch.uint8):
-        raise TypeError(f"weight must be int8, got {weight.dtype}")
     adt = _dt(input, "input")
     if output.dtype != input.dtype:
         raise TypeError("output dtype must equal input dtype")
@@ -563,24 +565,30 @@ def decode_attention(q, k_cache, v_cache, seq_lens=None, seq_len=None, page_tabl
 # Wrappers with the buffer orders of the reference's decode templates.
 def kv_cache_attention(Q, K_cache, V_cache, O, seq_len, scale):
     """make_kv_cache_attention_kernel (_msl_templates.py:1949-2048): Q, O
-    [n_heads, D]; K_cache, V_cache [n_heads, seq_len, D]."""
+    [n_heads, D]; K_cache, V_cache hold [n_heads, seq_len, D] in their first
+    n_heads * seq_len * D elements: head h starts at element h * seq_len * D
+    (head_offset_kv = pid * seq_len * D, line 1988), whatever capacity the
+    buffers have beyond that."""
     H, D = Q.shape
-    kc = K_cache.reshape(H, -1, D)[:, :seq_len].unsqueeze(0)
-    vc = V_cache.reshape(H, -1, D)[:, :seq_len].unsqueeze(0)
+    n = H * seq_len * D
+    kc = K_cache.reshape(-1)[:n].view(1, H, seq_len, D)
+    vc = V_cache.reshape(-1)[:n].view(1, H, seq_len, D)
     decode_attention(Q.unsqueeze(0), kc, vc, seq_len=seq_len, scale=scale, o=O.view(1, H, D))
     return O
 
 
-def gqa_attention(Q, K_cache, V_cache, O, seq_len, scale, n_q_per_kv=None):
+def gqa_attention(Q, K_cache, V_cache, O, seq_len, scale, n_q_per_kv):
     """make_gqa_attention_kernel (_msl_templates.py:2049-2160): Q, O
-    [n_q_heads, D]; K_cache, V_cache [n_kv_heads, seq_len, D]; query head h
-    reads KV head h // n_q_per_kv."""
+    [n_q_heads, D]; K_cache, V_cache hold [n_kv_heads, seq_len, D] in their
+    first elements, n_kv_heads = n_q_heads / n_q_per_kv (KV head h starts at
+    element h * seq_len * D); query head h reads KV head h // n_q_per_kv."""
     Hq, D = Q.shape
-    Hkv = K_cache.numel() // (seq_len * D)
-    if n_q_per_kv is not None and n_q_per_kv * Hkv != Hq:
-        raise ValueError(f"n_q_per_kv={n_q_per_kv} does not match {Hq} / {Hkv} heads")
-    kc = K_cache.reshape(Hkv, seq_len, D).unsqueeze(0)
-    vc = V_cache.reshape(Hkv, seq_len, D).unsqueeze(0)
+    if n_q_per_kv <= 0 or Hq % n_q_per_kv:
+        raise ValueError(f"n_q_per_kv={n_q_per_kv} does not divide {Hq} query heads")
+    Hkv = Hq // n_q_per_kv
+    n = Hkv * seq_len * D
+    kc = K_cache.reshape(-1)[:n].view(1, Hkv, seq_len, D)
+    vc = V_cache.reshape(-1)[:n].view(1, Hkv, seq_len, D)
     decode_attention(Q.unsqueeze(0), kc, vc, seq_len=seq_len, scale=scale, o=O.view(1, Hq, D))
     return O
 
