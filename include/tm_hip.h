@@ -212,6 +212,25 @@ int tm_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                         int q_dtype, int kv_dtype, int o_dtype, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* tm_decode_attention without the workspace arguments, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation).  It has no counterpart in the
+ * reference.  It allocates nothing: the per-slice partials go to a static
+ * device array of TM_DECODE_SCRATCH_BYTES, one per device, held from the
+ * library's first use on that device until the process ends.  A call whose
+ * slice plan needs more (tm_decode_attention_workspace_size(...) bytes) fails
+ * with TM_ERR_INVALID_ARG before launching anything.  Every call on a device
+ * shares that device's array: calls that overlap on one device (other
+ * streams, other threads) race and must be serialised by the caller.  Nothing
+ * in the array needs clearing between calls; each call writes every partial
+ * it reads. */
+#define TM_DECODE_SCRATCH_BYTES (8u << 20)
+int tm_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache, void* o,
+                                float* lse, int batch, int q_heads, int kv_heads, int head_dim,
+                                const int* seq_lens, int seq_len, const long long* kv_strides,
+                                const int* page_table, int page_size, int max_pages, float scale,
+                                int q_dtype, int kv_dtype, int o_dtype, void* stream);
+
 /* ---- KDA chunked forward -----------------------------------------------------
  * No counterpart in the reference (it has no linear attention): the gated
  * delta rule of Kimi Delta Attention in the [B, T, H, D] layout of its chunked

@@ -70,14 +70,15 @@ extern "C" size_t tm_decode_attention_workspace_size(int batch, int q_heads, int
   return ns > 1 ? (size_t)batch * q_heads * ns * (head_dim + 4) * sizeof(float) : 0;
 }
 
-extern "C" int tm_decode_attention(const void* q, const void* k_cache, const void* v_cache,
-                                   void* o, float* lse, int batch, int q_heads, int kv_heads,
-                                   int head_dim, const int* seq_lens, int seq_len,
-                                   const long long* kv_strides, const int* page_table,
-                                   int page_size, int max_pages, float scale, int q_dtype,
-                                   int kv_dtype, int o_dtype, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
-  const char* op = "tm_decode_attention";
+// Both entry points.  noalloc: the slice partials go to the device's
+// tm_decode_scratch array (no workspace argument); a plan that needs more than
+// it holds is rejected instead of falling back to one slice per wave.
+static int decode_attention(const char* op, bool noalloc, const void* q, const void* k_cache,
+                            const void* v_cache, void* o, float* lse, int batch, int q_heads,
+                            int kv_heads, int head_dim, const int* seq_lens, int seq_len,
+                            const long long* kv_strides, const int* page_table, int page_size,
+                            int max_pages, float scale, int q_dtype, int kv_dtype, int o_dtype,
+                            void* workspace, size_t workspace_bytes, void* stream) {
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || seq_len < 0)
     return fail(TM_ERR_INVALID_ARG, "%s: batch=%d q_heads=%d kv_heads=%d head_dim=%d seq_len=%d",
                 op, batch, q_heads, kv_heads, head_dim, seq_len);
@@ -128,6 +129,20 @@ extern "C" int tm_decode_attention(const void* q, const void* k_cache, const voi
     int ns = 1, sl = 0;
     plan_split(batch, q_heads, kv_heads, seq_len, p.page_size, paged, &ns, &sl);
     const size_t need = (size_t)batch * q_heads * ns * (head_dim + 4) * sizeof(float);
+    if (noalloc && ns > 1) {
+      static DeviceGlobal scratch("tm_decode_scratch");
+      void* ptr = nullptr;
+      size_t bytes = 0;
+      int rc = scratch.get(&ptr, &bytes);
+      if (rc) return rc;
+      if (need > bytes)
+        return fail(TM_ERR_INVALID_ARG,
+                    "%s: this call needs %zu bytes of slice scratch, more than the %zu bytes "
+                    "of the static scratch array; use tm_decode_attention with a workspace",
+                    op, need, bytes);
+      workspace = ptr;
+      workspace_bytes = bytes;
+    }
     if (ns > 1 && (!workspace || workspace_bytes < need || !aligned16(workspace))) {
       // no room for slice partials: one slice per wave (paged: only while it
       // spans at most 64 pages)
@@ -156,4 +171,30 @@ extern "C" int tm_decode_attention(const void* q, const void* k_cache, const voi
   static Kernel gen("decode_attn_general");
   p.nsplit = 1; p.split_len = seq_len;
   return launch(gen, dim3((unsigned)((long long)batch * q_heads)), dim3(256), 0, stream, p);
+}
+
+extern "C" int tm_decode_attention(const void* q, const void* k_cache, const void* v_cache,
+                                   void* o, float* lse, int batch, int q_heads, int kv_heads,
+                                   int head_dim, const int* seq_lens, int seq_len,
+                                   const long long* kv_strides, const int* page_table,
+                                   int page_size, int max_pages, float scale, int q_dtype,
+                                   int kv_dtype, int o_dtype, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  return decode_attention("tm_decode_attention", false, q, k_cache, v_cache, o, lse, batch,
+                          q_heads, kv_heads, head_dim, seq_lens, seq_len, kv_strides, page_table,
+                          page_size, max_pages, scale, q_dtype, kv_dtype, o_dtype, workspace,
+                          workspace_bytes, stream);
+}
+
+extern "C" int tm_decode_attention_noalloc(const void* q, const void* k_cache,
+                                           const void* v_cache, void* o, float* lse, int batch,
+                                           int q_heads, int kv_heads, int head_dim,
+                                           const int* seq_lens, int seq_len,
+                                           const long long* kv_strides, const int* page_table,
+                                           int page_size, int max_pages, float scale,
+                                           int q_dtype, int kv_dtype, int o_dtype, void* stream) {
+  return decode_attention("tm_decode_attention_noalloc", true, q, k_cache, v_cache, o, lse,
+                          batch, q_heads, kv_heads, head_dim, seq_lens, seq_len, kv_strides,
+                          page_table, page_size, max_pages, scale, q_dtype, kv_dtype, o_dtype,
+                          nullptr, 0, stream);
 }

@@ -90,6 +90,7 @@ bool resolve_api() {
   ok &= sym(h, g_api.ModuleLoadData, "hipModuleLoadData");
   ok &= sym(h, g_api.ModuleUnload, "hipModuleUnload");
   ok &= sym(h, g_api.ModuleGetFunction, "hipModuleGetFunction");
+  ok &= sym(h, g_api.ModuleGetGlobal, "hipModuleGetGlobal");
   ok &= sym(h, g_api.FuncGetAttribute, "hipFuncGetAttribute");
   ok &= sym(h, g_api.ModuleLaunchKernel, "hipModuleLaunchKernel");
   ok &= sym(h, g_api.StreamSynchronize, "hipStreamSynchronize");
@@ -218,6 +219,37 @@ int Kernel::get(hipFunction_t* out) {
     }
   }
   return fail(TM_ERR_NOT_FOUND, "kernel '%s' not found in the embedded code objects", name_);
+}
+
+int DeviceGlobal::get(void** ptr, size_t* bytes) {
+  int dev = 0;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  void* a = addr_[dev].load(std::memory_order_acquire);
+  if (a) {
+    *ptr = a;
+    if (bytes) *bytes = bytes_[dev];
+    return 0;
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  rc = load_modules_locked(dev);
+  if (rc) return rc;
+  for (int i = 0; i < kNumModules; ++i) {
+    hipDeviceptr_t d = nullptr;
+    size_t n = 0;
+    hipError_t e = g_api.ModuleGetGlobal(&d, &n, g_mods[dev][i], name_);
+    if (e != hipSuccess || !d) {
+      g_api.GetLastError();  // an expected miss in this module
+      continue;
+    }
+    bytes_[dev] = n;
+    addr_[dev].store((void*)d, std::memory_order_release);
+    *ptr = (void*)d;
+    if (bytes) *bytes = n;
+    return 0;
+  }
+  return fail(TM_ERR_NOT_FOUND, "device global '%s' not found in the embedded code objects",
+              name_);
 }
 
 }  // namespace tmhip

@@ -26,6 +26,7 @@ struct HipApi {
   hipError_t (*ModuleLoadData)(hipModule_t*, const void*);
   hipError_t (*ModuleUnload)(hipModule_t);
   hipError_t (*ModuleGetFunction)(hipFunction_t*, hipModule_t, const char*);
+  hipError_t (*ModuleGetGlobal)(hipDeviceptr_t*, size_t*, hipModule_t, const char*);
   hipError_t (*FuncGetAttribute)(int*, hipFunction_attribute, hipFunction_t);
   hipError_t (*ModuleLaunchKernel)(hipFunction_t, unsigned, unsigned, unsigned, unsigned,
                                    unsigned, unsigned, unsigned, hipStream_t, void**, void**);
@@ -57,6 +58,24 @@ class Kernel {
  private:
   const char* name_;
   std::atomic<hipFunction_t> fn_[kMaxDevices];
+};
+
+// A __device__ global of one of the embedded code objects: its address on
+// each device, resolved once per device (with that device current) through
+// hipModuleGetGlobal on the module loaded there, the module-API counterpart
+// of hipGetSymbolAddress.  Host code holds only the returned device address.
+class DeviceGlobal {
+ public:
+  explicit DeviceGlobal(const char* name) : name_(name) {
+    for (auto& a : addr_) a.store(nullptr, std::memory_order_relaxed);
+  }
+  // Address and size on the current device; returns 0 or an error code.
+  int get(void** ptr, size_t* bytes);
+
+ private:
+  const char* name_;
+  std::atomic<void*> addr_[kMaxDevices];
+  size_t bytes_[kMaxDevices] = {};
 };
 
 int current_device(int* dev);

@@ -55,6 +55,14 @@ struct DecodeParams {
   int q_dt, kv_dt, o_dt;    // TM_DT_* codes
 };
 
+// Scratch of tm_decode_attention_noalloc: the per-slice partials (O, max,
+// sum) live here instead of in a caller's workspace.  One copy per device,
+// allocated when this code object is loaded there and held until the process
+// ends; its device address is looked up by name (hipModuleGetGlobal), so it
+// has external linkage (a static array would not be in the module's symbol
+// table).  Size: TM_DECODE_SCRATCH_BYTES of include/tm_hip.h.
+__device__ __align__(256) unsigned char tm_decode_scratch[8u << 20];
+
 namespace {
 constexpr float kLn2f = 0.69314718055994530942f;
 

@@ -50,6 +50,9 @@ SIGNATURES = {
     "tm_decode_attention": [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32,
                             C.POINTER(C.c_longlong), vp, i32, i32, C.c_float, i32, i32, i32, vp,
                             sz, vp],
+    "tm_decode_attention_noalloc": [vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32,
+                                    C.POINTER(C.c_longlong), vp, i32, i32, C.c_float, i32, i32,
+                                    i32, vp],
     "tm_kda_chunk_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, C.c_float,
                          i32, vp, sz, vp],
     "tm_kda_recurrent_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, C.c_float,
