@@ -41,6 +41,23 @@ extern "C" {
 #define TM_DT_F16 1
 #define TM_DT_BF16 2
 #define TM_DT_U8 3
+/* FP8 inputs of the dot / matmul entry points, decoded as the reference's
+ * converters (triton_metal/codegen/msl_builtins.py, dtype map 264-272):
+ * Triton's fp8e4nv (OCP E4M3, bias 7, 0x7F/0xFF NaN), fp8e5 (E5M2, bias 15,
+ * inf and NaN), fp8e4b15, fp8e4b8 and fp8e5b16 (bias 15 / 8 / 16). */
+#define TM_DT_FP8_E4M3 4
+#define TM_DT_FP8_E5M2 5
+#define TM_DT_FP8_E4M3B15 6
+#define TM_DT_FP8_E4M3B8 7
+#define TM_DT_FP8_E5M2B16 8
+
+/* ---- dot epilogues (tm_dot) --------------------------------------------- */
+#define TM_EPI_NONE 0
+#define TM_EPI_ADD_MATRIX 1 /* C = A@B + Z[b, m, n]                      */
+#define TM_EPI_ADD_ROWS 2   /* C = A@B + Z[b, m, 0]                      */
+#define TM_EPI_ADD_COLS 3   /* C = A@B + Z[b, 0, n]                      */
+#define TM_EPI_SOFTMAX 4    /* C = softmax over n of A@B                 */
+#define TM_EPI_CHAIN_DOT 5  /* C = (A@B) @ W, W [N, L]                   */
 
 /* ---- library / device ------------------------------------------------------ */
 /* Resolve the HIP runtime.  Called implicitly by every entry point. */
@@ -148,9 +165,33 @@ int tm_wq_repack_awq(const void* qweight, const void* qzeros, const void* scales
  * C[M, N] = A[M, K] @ B[K, N], row-major with leading dimensions lda/ldb/ldc
  * (elements).  Replaces make_matmul_kernel (_msl_templates.py:447-585; buffer
  * order A, B, C, M, N, K) and make_simdgroup_matmul_kernel (3501-3667; fp16
- * in, fp32 out).  in_dtype F16/BF16 (MFMA) or F32; out_dtype F32/F16/BF16. */
+ * in, fp32 out).  in_dtype F16/BF16 (MFMA), an FP8 code (MFMA on the exact
+ * fp16 values; the reference's FP8 matmul writes fp32, _msl_templates.py:
+ * 475-476) or F32; out_dtype F32/F16/BF16. */
 int tm_matmul(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb,
               int ldc, int in_dtype, int out_dtype, void* stream);
+/* tl.dot in general form: the strided dot template of the reference,
+ * _lower_dot_via_prebuilt_template (triton_metal/codegen/_lowerer_templates.py:
+ * 1116-1540), with the epilogue detection of _detect_dot_epilogue
+ * (_lowerer_detection.py:763-805).  For b < batch, m < M, n < N:
+ *   P[b, m, n] = sum_k A[b, m, k] * B[b, k, n]      (fp32 accumulation)
+ *   C[b, m, n] = P + Z[b, m, n] | P + Z[b, m, 0] | P + Z[b, 0, n]
+ *                | exp(P - max_n P) / sum_n exp(P - max_n P)
+ *   C[b, m, l] = sum_n P[b, m, n] * W[n, l]         (chain-dot, l < L)
+ * Every operand is addressed by element strides, so transposed and
+ * column-major views need no copy:
+ *   strides[14] = {A: batch, m, k;  B: batch, k, n;  C: batch, m, n (l);
+ *                  Z: batch, m, n;  W: n, l}   (non-negative).
+ * in_dtype F16 / BF16 / FP8 (MFMA; FP8 decoded exactly to fp16) or F32
+ * (fp32 FMA); out_dtype F32 / F16 / BF16 (the reference writes FP8 products
+ * as fp32).  z_dtype / w_dtype: the dtypes of Z / W (any input dtype), or
+ * TM_DT_NONE when unused.  Z may be C itself (the reference reads the bias
+ * from the output buffer): add-matrix and add-rows are defined in place;
+ * add-cols in place only for batch * M == 1.  Softmax and chain-dot keep a
+ * product row on chip: N <= 8192. */
+int tm_dot(const void* A, const void* B, void* C, const void* Z, const void* W, int batch, int M,
+           int N, int K, int L, const long long* strides, int epilogue, int in_dtype,
+           int out_dtype, int z_dtype, int w_dtype, void* stream);
 /* output[M, N] = input[M, K] @ weight[N, K]^T (+ bias[N]); bias may be NULL.
  * Replaces make_fused_linear_kernel (_msl_templates.py:4013-4135; buffer order
  * input, weight, C, [bias], M, N, K). */

@@ -42,6 +42,13 @@ PINNING = {
                         "brute-force phase loops, closed forms (one position -> V[0], "
                         "zero query -> mean of V)",
     "gptq_to_ref": "dequant_int4 of the result equals (q - z) s of the unpacked checkpoint",
+    "fp8_decode": "every one of the 256 codes of each format against an independent "
+                  "bit-field formula, torch's float8_e4m3fn / float8_e5m2 decoders, the "
+                  "formats' closed-form extremes (max normal, min subnormal, NaN / inf codes)",
+    "dot": "brute-force loops over (b, m, n, k) for every epilogue, strided and transposed "
+           "views equal to the contiguous product of the same matrices, softmax rows sum "
+           "to one, chain-dot equal to two plain products, add-* equal to the plain "
+           "product plus the broadcast bias",
     "awq_to_ref": "dequant_int4 of the result equals (q - z) s of the unpacked checkpoint",
 }
 
@@ -351,3 +358,81 @@ def awq_to_ref(qweight, qzeros, scales, N: int, K: int, group_size: int):
     ng = (K + group_size - 1) // group_size
     z = _unpack_words(qzeros)[:, :, inv].reshape(ng, N).T.astype(np.int64)
     return pack_int4(q), np.asarray(scales).T.copy(), z
+
+
+# ---------------------------------------------------------------------------
+# FP8 formats: the decoders of triton_metal/codegen/msl_builtins.py
+# ---------------------------------------------------------------------------
+# (exponent bits, mantissa bits, bias, has inf) per Triton dtype name:
+#   fp8e4nv  FP8_E4M3_TO_FLOAT    msl_builtins.py:53-66   (exp 15 / mant 7 = NaN)
+#   fp8e5    FP8_E5M2_TO_FLOAT    msl_builtins.py:95-109  (exp 31: inf / NaN)
+#   fp8e4b15 FP8_E4M3B15_TO_FLOAT msl_builtins.py:140-153
+#   fp8e4b8  FP8_E4M3B8_TO_FLOAT  msl_builtins.py:182-195
+#   fp8e5b16 FP8_E5M2B16_TO_FLOAT msl_builtins.py:223-237
+# (the dtype map is msl_builtins.py:264-272)
+FP8_FORMATS = {
+    "fp8e4nv": (4, 3, 7, False),
+    "fp8e5": (5, 2, 15, True),
+    "fp8e4b15": (4, 3, 15, False),
+    "fp8e4b8": (4, 3, 8, False),
+    "fp8e5b16": (5, 2, 16, True),
+}
+
+
+def fp8_decode(codes, fmt: str) -> np.ndarray:
+    """uint8 codes -> float64 values as the reference's MSL decoders compute
+    them: exponent field 0 is subnormal (mant / 2^mbits * 2^(1 - bias)); the
+    all-ones exponent is NaN with mantissa all ones (4-bit exponent formats) or
+    inf / NaN (5-bit formats); otherwise (1 + mant / 2^mbits) * 2^(exp - bias);
+    the sign bit negates."""
+    eb, mb, bias, has_inf = FP8_FORMATS[fmt]
+    c = np.asarray(codes, np.uint8).astype(np.int64)
+    sign = (c >> 7) & 1
+    e = (c >> mb) & ((1 << eb) - 1)
+    m = c & ((1 << mb) - 1)
+    emax = (1 << eb) - 1
+    val = np.where(e == 0, m / (1 << mb) * 2.0 ** (1 - bias),
+                   (1 + m / (1 << mb)) * 2.0 ** (e.astype(np.float64) - bias))
+    if has_inf:
+        val = np.where(e == emax, np.where(m == 0, np.inf, np.nan), val)
+    else:
+        val = np.where((e == emax) & (m == (1 << mb) - 1), np.nan, val)
+    return np.where(sign == 1, -val, val)
+
+
+# ---------------------------------------------------------------------------
+# tl.dot with strides, batches and epilogues
+# ---------------------------------------------------------------------------
+DOT_EPILOGUES = ("none", "add-matrix", "add-rows", "add-cols", "softmax", "chain-dot")
+
+
+def dot(A, B, epilogue: str = "none", Z=None, W=None) -> np.ndarray:
+    """The strided tl.dot template of _lowerer_templates.py:1116-1540, float64.
+
+    A [.., M, K] @ B [.., K, N] (a leading batch dimension for the 3-D dot,
+    1151-1160 and 1453-1470), accumulated from zero or from the epilogue's bias
+    (1429-1438): add-matrix Z[.., m, n], add-rows Z[.., m, 0], add-cols
+    Z[.., 0, n] (the bias loads of 1395-1420); softmax over each row of the
+    product, exp(x - rowmax) / sum (1488-1505); chain-dot (A @ B) @ W with W
+    [N, L] from the unrounded product (1506-1522).  Strides only select which
+    elements are read and written, so the restatement takes the logical
+    matrices."""
+    A = np.asarray(A, np.float64)
+    B = np.asarray(B, np.float64)
+    P = A @ B
+    if epilogue == "none":
+        return P
+    Z = None if Z is None else np.asarray(Z, np.float64)
+    if epilogue == "add-matrix":
+        return P + Z
+    if epilogue == "add-rows":
+        return P + Z[..., :, :1]
+    if epilogue == "add-cols":
+        return P + Z[..., :1, :]
+    if epilogue == "softmax":
+        mx = P.max(axis=-1, keepdims=True)
+        e = np.exp(P - mx)
+        return e / e.sum(axis=-1, keepdims=True)
+    if epilogue == "chain-dot":
+        return P @ np.asarray(W, np.float64)
+    raise ValueError(f"unknown epilogue {epilogue}")

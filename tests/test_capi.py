@@ -109,3 +109,29 @@ def test_int8_matmul_rejects_uint8_weights():
     with pytest.raises(TypeError, match="int8"):
         tm.int8_matmul(x, w, torch.zeros(1, 16, dtype=torch.float16),
                        torch.ones(16, dtype=torch.float16), None, 1, 16, 64)
+
+
+def test_dot_validation_before_any_hip_call():
+    import triton_metal_amd._lib as L
+    lib = L.lib()
+    p = ctypes.c_void_p(16)
+    st = (ctypes.c_longlong * 14)(0, 8, 1, 0, 8, 1, 0, 8, 1, 0, 0, 0, 0, 0)
+    args = (p, p, p, None, None, 1, 8, 8, 8, 0, st)
+    # unknown epilogue, bad dtype, add epilogue without Z, negative stride
+    assert lib.tm_dot(*args, 9, L.TM_DT_F16, L.TM_DT_F16, L.TM_DT_NONE, L.TM_DT_NONE,
+                      None) == L.TM_ERR_INVALID_ARG
+    assert lib.tm_dot(*args, 0, 42, L.TM_DT_F16, L.TM_DT_NONE, L.TM_DT_NONE,
+                      None) == L.TM_ERR_INVALID_ARG
+    assert lib.tm_dot(*args, L.TM_EPI_ADD_ROWS, L.TM_DT_F16, L.TM_DT_F16, L.TM_DT_NONE,
+                      L.TM_DT_NONE, None) == L.TM_ERR_INVALID_ARG
+    assert "Z" in L.last_error()
+    neg = (ctypes.c_longlong * 14)(0, 8, -1, 0, 8, 1, 0, 8, 1, 0, 0, 0, 0, 0)
+    assert lib.tm_dot(p, p, p, None, None, 1, 8, 8, 8, 0, neg, 0, L.TM_DT_F16, L.TM_DT_F16,
+                      L.TM_DT_NONE, L.TM_DT_NONE, None) == L.TM_ERR_INVALID_ARG
+    # softmax rows beyond what a workgroup keeps on chip
+    assert lib.tm_dot(p, p, p, None, None, 1, 8, 9000, 8, 0, st, L.TM_EPI_SOFTMAX,
+                      L.TM_DT_F16, L.TM_DT_F32, L.TM_DT_NONE, L.TM_DT_NONE,
+                      None) == L.TM_ERR_UNSUPPORTED
+    # empty problems succeed without touching the device
+    assert lib.tm_dot(p, p, p, None, None, 0, 8, 8, 8, 0, st, 0, L.TM_DT_F16, L.TM_DT_F16,
+                      L.TM_DT_NONE, L.TM_DT_NONE, None) == 0

@@ -1,0 +1,196 @@
+"""tl.dot in general form on the GPU against oracle.dot: strided, transposed
+and column-major views, batched 3-D operands, every epilogue, fp16 / bf16 /
+fp32 and the five FP8 formats.
+
+Tolerances: fp16 / bf16 outputs atol 2e-2 / rtol 1e-2.  fp32 outputs (fp32
+accumulation of exact products): |err| <= 1e-4 |ref| + 2^-16 (|A| @ |B|), the
+accumulation bound with the magnitude of the terms (the FP8 tests draw codes
+across each format's whole range, subnormals and extremes included).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import triton_metal_amd as tm
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 2e-2, 1e-2
+FP8 = ["fp8e4nv", "fp8e5", "fp8e4b15", "fp8e4b8", "fp8e5b16"]
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _rand(shape, seed, dt):
+    return torch.randn(*shape, generator=_gen(seed)).to(dt)
+
+
+def _np(t):
+    return t.double().cpu().numpy()
+
+
+def _check(got, ref, out_dt, absA=None, absB=None):
+    got = got.double().cpu().numpy()
+    if out_dt == torch.float32:
+        bound = 1e-4 * np.abs(ref) + (2.0 ** -16 * (absA @ absB) if absA is not None else 1e-5)
+        err = np.abs(got - ref)
+        assert (err <= bound + 1e-30).all(), f"max err {err.max():.3e}, worst {(err / (bound + 1e-30)).max():.2f}"
+    else:
+        np.testing.assert_allclose(got, ref, atol=ATOL, rtol=RTOL)
+
+
+def _views(M, N, K, dt, layout, seed, batch=None, dev="cuda"):
+    """a [.., M, K], b [.., K, N] as views of the requested layout; returns the
+    device views and their CPU copies (logical values)."""
+    bs = () if batch is None else (batch,)
+    a = _rand(bs + (M, K), seed, dt)
+    b = _rand(bs + (K, N), seed + 1, dt)
+    if layout == "row":
+        da, db = a.to(dev), b.to(dev)
+    elif layout == "trans_a":      # A stored [K, M] (column-major A)
+        da = a.transpose(-1, -2).contiguous().to(dev).transpose(-1, -2)
+        db = b.to(dev)
+    elif layout == "trans_b":      # B stored [N, K]
+        da = a.to(dev)
+        db = b.transpose(-1, -2).contiguous().to(dev).transpose(-1, -2)
+    elif layout == "strided":      # every second element of wider buffers
+        ap = torch.zeros(bs + (M, 2 * K + 3), dtype=dt)
+        ap[..., : 2 * K : 2] = a
+        bp = torch.zeros(bs + (2 * K, N + 5), dtype=dt)
+        bp[..., ::2, :N] = b
+        da = ap.to(dev)[..., : 2 * K : 2]
+        db = bp.to(dev)[..., ::2, :N]
+    else:
+        raise ValueError(layout)
+    return da, db, a, b
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["row", "trans_a", "trans_b", "strided"])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 32), (100, 72, 136), (7, 130, 50)])
+def test_dot_layouts(dev, dt, layout, M, N, K):
+    da, db, a, b = _views(M, N, K, dt, layout, seed=M + N + K)
+    c = torch.empty(M, N, dtype=dt, device=dev)
+    tm.dot(da, db, c)
+    _check(c, oracle.dot(_np(a), _np(b)), dt)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_dot_column_major_output(dev, dt):
+    """The reference's "trans" case: C written through column-major strides."""
+    M, N, K = 96, 80, 64
+    da, db, a, b = _views(M, N, K, dt, "row", seed=5)
+    cbuf = torch.zeros(N, M, dtype=dt, device=dev)
+    tm.dot(da, db, cbuf.t())
+    _check(cbuf.t(), oracle.dot(_np(a), _np(b)), dt)
+
+
+@pytest.mark.parametrize("layout", ["row", "trans_a", "trans_b", "strided"])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_dot_batched_3d(dev, layout, dt):
+    B, M, N, K = 3, 70, 40, 96
+    da, db, a, b = _views(M, N, K, dt, layout, seed=17, batch=B)
+    c = torch.empty(B, M, N, dtype=torch.float32, device=dev)
+    tm.dot(da, db, c)
+    ref = oracle.dot(_np(a), _np(b))
+    _check(c, ref, torch.float32, np.abs(_np(a)), np.abs(_np(b)))
+
+
+@pytest.mark.parametrize("epilogue", ["add-matrix", "add-rows", "add-cols"])
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("batch", [None, 2])
+def test_dot_add_epilogues(dev, epilogue, dt, batch):
+    M, N, K = 90, 66, 48
+    da, db, a, b = _views(M, N, K, dt, "trans_b", seed=23, batch=batch)
+    bs = () if batch is None else (batch,)
+    z = _rand(bs + (M, N), 29, dt)
+    c = torch.empty(bs + (M, N), dtype=dt, device=dev)
+    tm.dot(da, db, c, epilogue, z=z.to(dev))
+    _check(c, oracle.dot(_np(a), _np(b), epilogue, Z=_np(z)), dt,
+           np.abs(_np(a)), np.abs(_np(b)))
+
+
+@pytest.mark.parametrize("epilogue", ["add-matrix", "add-rows"])
+def test_dot_bias_read_in_place(dev, epilogue):
+    """Z is the output buffer itself, as in the reference's test kernels."""
+    M, N, K = 130, 70, 64
+    da, db, a, b = _views(M, N, K, torch.float16, "row", seed=31)
+    z = _rand((M, N), 37, torch.float16)
+    c = z.to(dev)
+    tm.dot(da, db, c, epilogue, z=c)
+    _check(c, oracle.dot(_np(a), _np(b), epilogue, Z=_np(z)), torch.float16)
+
+
+def test_dot_add_cols_in_place_rejected_for_many_rows(dev):
+    M, N, K = 8, 16, 16
+    da, db, _, _ = _views(M, N, K, torch.float16, "row", seed=41)
+    c = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="add-cols"):
+        tm.dot(da, db, c, "add-cols", z=c)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("N", [40, 1500])
+def test_dot_softmax(dev, dt, N):
+    M, K = 33, 2100  # two pieces of A's row, two column groups at N = 1500
+    da, db, a, b = _views(M, N, K, dt, "trans_a", seed=43)
+    c = torch.empty(M, N, dtype=torch.float32, device=dev)
+    # scale so that the softmax is neither uniform nor one-hot
+    da = (da.float() * 0.05).to(dt)
+    a = (a.float() * 0.05).to(dt)
+    tm.dot(da, db, c, "softmax")
+    ref = oracle.dot(_np(a), _np(b), "softmax")
+    np.testing.assert_allclose(c.cpu().numpy(), ref, atol=1e-6, rtol=1e-4)
+    np.testing.assert_allclose(c.sum(-1).cpu().numpy(), 1.0, rtol=1e-5)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_dot_chain(dev, dt):
+    M, N, K, L = 50, 64, 80, 24
+    da, db, a, b = _views(M, N, K, dt, "strided", seed=47)
+    w = _rand((N, L), 53, dt)
+    c = torch.empty(M, L, dtype=torch.float32, device=dev)
+    tm.dot(da, db, c, "chain-dot", w=w.to(dev).t().contiguous().t())  # W column-major
+    ref = oracle.dot(_np(a), _np(b), "chain-dot", W=_np(w))
+    absP = np.abs(_np(a)) @ np.abs(_np(b))
+    bound = 1e-4 * np.abs(ref) + 2.0 ** -16 * (absP @ np.abs(_np(w)))
+    assert (np.abs(c.cpu().numpy() - ref) <= bound).all()
+
+
+def _fp8_codes(shape, fmt, seed):
+    """Codes over the whole format, NaN / inf codes replaced by 0."""
+    c = torch.randint(0, 256, shape, generator=_gen(seed), dtype=torch.uint8)
+    v = oracle.fp8_decode(c.numpy(), fmt)
+    c[torch.from_numpy(~np.isfinite(v))] = 0
+    return c
+
+
+@pytest.mark.parametrize("fmt", FP8)
+@pytest.mark.parametrize("layout", ["row", "trans_b"])
+def test_dot_fp8_formats(dev, fmt, layout):
+    M, N, K = 96, 80, 160
+    a = _fp8_codes((M, K), fmt, 61)
+    b = _fp8_codes((K, N), fmt, 67)
+    da = a.to(dev)
+    db = b.to(dev) if layout == "row" else b.t().contiguous().to(dev).t()
+    c = torch.empty(M, N, dtype=torch.float32, device=dev)
+    tm.dot(da, db, c, fp8_format=fmt)
+    av, bv = oracle.fp8_decode(a.numpy(), fmt), oracle.fp8_decode(b.numpy(), fmt)
+    ref = oracle.dot(av, bv)
+    _check(c, ref, torch.float32, np.abs(av), np.abs(bv))
+
+
+@pytest.mark.parametrize("tdt,fmt", [(torch.float8_e4m3fn, "fp8e4nv"),
+                                     (torch.float8_e5m2, "fp8e5")])
+def test_matmul_fp8_c1_shape(dev, tdt, fmt):
+    """tm_matmul with FP8 inputs (the reference's FP8 make_matmul_kernel: fp32
+    output) at the C1 shape, torch's FP8 dtypes."""
+    M = N = K = 512
+    a = (torch.randn(M, K, generator=_gen(71)) * 2).to(tdt)
+    b = (torch.randn(K, N, generator=_gen(73)) * 2).to(tdt)
+    c = torch.empty(M, N, dtype=torch.float32, device=dev)
+    tm.matmul(a.to(dev), b.to(dev), c, M, N, K)
+    av, bv = a.double().numpy(), b.double().numpy()
+    _check(c, av @ bv, torch.float32, np.abs(av), np.abs(bv))

@@ -1,0 +1,136 @@
+// Typed entry point for tl.dot in general form (strided / transposed
+// operands, a batch dimension, FP8 inputs, epilogues): dot_tile_{f16,bf16}
+// (MFMA) or dot_rows (fp32, every epilogue).  Also the FP8 path of tm_matmul.
+#include <cstring>
+
+#include "runtime.h"
+
+using namespace tmhip;
+
+namespace {
+
+// Kernel argument block; must match struct DotParams in dot.hip.
+struct DotParams {
+  const void* A;
+  const void* B;
+  void* C;
+  const void* Z;
+  const void* W;
+  long long sa_b, sa_m, sa_k;
+  long long sb_b, sb_k, sb_n;
+  long long sc_b, sc_m, sc_n;
+  long long sz_b, sz_m, sz_n;
+  long long sw_n, sw_l;
+  int batch, M, N, K, L;
+  int epi;
+  int in_dt, out_dt, z_dt, w_dt;
+  int a_mode, b_mode;
+};
+
+enum { MODE_KC = 0, MODE_RC = 1, MODE_SCALAR = 2 };
+
+bool is_fp8(int dt) { return dt >= TM_DT_FP8_E4M3 && dt <= TM_DT_FP8_E5M2B16; }
+int elem_size(int dt) { return dt == TM_DT_F32 ? 4 : is_fp8(dt) ? 1 : 2; }
+bool is_input(int dt) { return is_float(dt) || is_fp8(dt); }
+
+// Fetch mode of a [rows, K] operand with strides (s_b, s_r, s_k): 16-byte
+// (FP8: 8-byte) pieces along k or along the rows when that dimension is
+// contiguous and every piece starts aligned, else element by element.
+int fetch_mode(const void* X, long long s_b, long long s_r, long long s_k, int batch, int esz) {
+  const uintptr_t align = 8u * (uintptr_t)esz;
+  const bool base_ok = ((uintptr_t)X % align) == 0 && (batch <= 1 || s_b % 8 == 0);
+  if (base_ok && s_k == 1 && s_r % 8 == 0) return MODE_KC;
+  if (base_ok && s_r == 1 && s_k % 8 == 0) return MODE_RC;
+  return MODE_SCALAR;
+}
+
+// Byte extent [lo, hi) of a strided 3-D view (non-negative strides).
+void extent(const void* p, int esz, long long d0, long long d1, long long d2, long long s0,
+            long long s1, long long s2, uintptr_t* lo, uintptr_t* hi) {
+  const long long last = (d0 - 1) * s0 + (d1 - 1) * s1 + (d2 - 1) * s2;
+  *lo = (uintptr_t)p;
+  *hi = (uintptr_t)p + (uintptr_t)((last + 1) * esz);
+}
+
+}  // namespace
+
+namespace tmhip {
+
+int dot_impl(const char* op, const void* A, const void* B, void* C, const void* Z, const void* W,
+             int batch, int M, int N, int K, int L, const long long* st, int epilogue,
+             int in_dtype, int out_dtype, int z_dtype, int w_dtype, void* stream) {
+  if (batch < 0 || M < 0 || N < 0 || K < 0)
+    return fail(TM_ERR_INVALID_ARG, "%s: batch=%d M=%d N=%d K=%d", op, batch, M, N, K);
+  if (epilogue < TM_EPI_NONE || epilogue > TM_EPI_CHAIN_DOT)
+    return fail(TM_ERR_INVALID_ARG, "%s: epilogue %d", op, epilogue);
+  if (!is_input(in_dtype) || !is_float(out_dtype))
+    return fail(TM_ERR_INVALID_ARG, "%s: dtypes %d -> %d", op, in_dtype, out_dtype);
+  const bool chain = epilogue == TM_EPI_CHAIN_DOT;
+  const bool add = epilogue >= TM_EPI_ADD_MATRIX && epilogue <= TM_EPI_ADD_COLS;
+  if (chain && L < 0) return fail(TM_ERR_INVALID_ARG, "%s: L=%d", op, L);
+  const int NC = chain ? L : N;  // columns of C
+  if (batch == 0 || M == 0 || NC == 0) return 0;
+  if (!A || !B || !C || !st) return fail(TM_ERR_INVALID_ARG, "%s: null buffer or strides", op);
+  if (add && (!Z || !is_input(z_dtype)))
+    return fail(TM_ERR_INVALID_ARG, "%s: the add epilogues need Z and its dtype", op);
+  if (chain && (!W || !is_input(w_dtype)))
+    return fail(TM_ERR_INVALID_ARG, "%s: chain-dot needs W and its dtype", op);
+  for (int i = 0; i < 14; ++i)
+    if (st[i] < 0) return fail(TM_ERR_INVALID_ARG, "%s: negative stride %d", op, i);
+  if ((epilogue == TM_EPI_SOFTMAX || chain) && N > 8192)
+    return fail(TM_ERR_UNSUPPORTED, "%s: softmax / chain-dot rows of N=%d > 8192", op, N);
+  if (!api()) return TM_ERR_NO_RUNTIME;
+  clear_error();
+
+  DotParams p;
+  memset(&p, 0, sizeof p);
+  p.A = A; p.B = B; p.C = C; p.Z = Z; p.W = W;
+  p.sa_b = st[0]; p.sa_m = st[1]; p.sa_k = st[2];
+  p.sb_b = st[3]; p.sb_k = st[4]; p.sb_n = st[5];
+  p.sc_b = st[6]; p.sc_m = st[7]; p.sc_n = st[8];
+  p.sz_b = st[9]; p.sz_m = st[10]; p.sz_n = st[11];
+  p.sw_n = st[12]; p.sw_l = st[13];
+  p.batch = batch; p.M = M; p.N = N; p.K = K; p.L = L;
+  p.epi = epilogue;
+  p.in_dt = in_dtype; p.out_dt = out_dtype; p.z_dt = z_dtype; p.w_dt = w_dtype;
+
+  // A bias read in place from the output (Z overlapping C), as the
+  // reference's test kernels do: add-matrix reads and writes each element in
+  // one thread; add-rows reads its row's element in the row's own workgroup
+  // (dot_rows) before any store; add-cols across rows would race.
+  bool rows_kernel = epilogue == TM_EPI_SOFTMAX || chain || in_dtype == TM_DT_F32 || K == 0;
+  if (add && epilogue != TM_EPI_ADD_MATRIX) {
+    uintptr_t zl, zh, cl, ch;
+    extent(Z, elem_size(z_dtype), batch, M, N, st[9], st[10], st[11], &zl, &zh);
+    extent(C, elem_size(out_dtype), batch, M, NC, st[6], st[7], st[8], &cl, &ch);
+    if (zl < ch && cl < zh) {
+      if (epilogue == TM_EPI_ADD_COLS && (long long)batch * M > 1)
+        return fail(TM_ERR_INVALID_ARG,
+                    "%s: add-cols with Z overlapping C is only defined for one row", op);
+      rows_kernel = true;
+    }
+  }
+  if (!rows_kernel && batch > 65535) rows_kernel = true;
+  if (rows_kernel) {
+    static Kernel kr("dot_rows");
+    return launch(kr, dim3((unsigned)((long long)batch * M)), dim3(256), 0, stream, p);
+  }
+  const int esz = elem_size(in_dtype);
+  p.a_mode = fetch_mode(A, p.sa_b, p.sa_m, p.sa_k, batch, esz);
+  p.b_mode = fetch_mode(B, p.sb_b, p.sb_n, p.sb_k, batch, esz);
+  static Kernel kf("dot_tile_f16"), kb("dot_tile_bf16");
+  const long long tiles = (long long)((M + 63) / 64) * ((N + 63) / 64);
+  if (tiles > 0x7fffffffLL) return fail(TM_ERR_UNSUPPORTED, "%s: too many tiles", op);
+  return launch(in_dtype == TM_DT_BF16 ? kb : kf, dim3((unsigned)tiles, (unsigned)batch),
+                dim3(256), 0, stream, p);
+}
+
+}  // namespace tmhip
+
+extern "C" int tm_dot(const void* A, const void* B, void* C, const void* Z, const void* W,
+                      int batch, int M, int N, int K, int L, const long long* strides,
+                      int epilogue, int in_dtype, int out_dtype, int z_dtype, int w_dtype,
+                      void* stream) {
+  return dot_impl("tm_dot", A, B, C, Z, W, batch, M, N, K, L, strides, epilogue, in_dtype,
+                  out_dtype, z_dtype, w_dtype, stream);
+}

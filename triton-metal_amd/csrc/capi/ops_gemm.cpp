@@ -165,6 +165,14 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
 int dense(const void* A, const void* B, void* C, const void* bias, int M, int N, int K, int lda,
           int ldb, int ldc, bool bt, int idt, int odt, void* stream) {
   const char* op = bt ? "tm_linear" : "tm_matmul";
+  if (!bt && idt >= TM_DT_FP8_E4M3 && idt <= TM_DT_FP8_E5M2B16) {
+    // FP8 inputs: the general dot on row-major operands
+    if (lda < K || ldb < N || ldc < N)
+      return fail(TM_ERR_INVALID_ARG, "%s: leading dimension too small", op);
+    const long long st[14] = {0, lda, 1, 0, ldb, 1, 0, ldc, 1, 0, 0, 0, 0, 0};
+    return dot_impl(op, A, B, C, nullptr, nullptr, 1, M, N, K, 0, st, TM_EPI_NONE, idt, odt,
+                    TM_DT_NONE, TM_DT_NONE, stream);
+  }
   if (M < 0 || N < 0 || K < 0) return fail(TM_ERR_INVALID_ARG, "%s: negative size", op);
   if (M == 0 || N == 0) return 0;
   if (!A || !B || !C) return fail(TM_ERR_INVALID_ARG, "%s: null buffer", op);

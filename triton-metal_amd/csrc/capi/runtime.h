@@ -97,6 +97,11 @@ int launch(Kernel& k, dim3 grid, dim3 block, unsigned shared, void* stream, Args
   return 0;
 }
 
+// tm_dot's implementation (ops_dot.cpp), shared with tm_matmul's FP8 path.
+int dot_impl(const char* op, const void* A, const void* B, void* C, const void* Z, const void* W,
+             int batch, int M, int N, int K, int L, const long long* strides, int epilogue,
+             int in_dtype, int out_dtype, int z_dtype, int w_dtype, void* stream);
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline bool is_half(int dt) { return dt == TM_DT_F16 || dt == TM_DT_BF16; }
 inline bool is_float(int dt) { return dt == TM_DT_F32 || dt == TM_DT_F16 || dt == TM_DT_BF16; }

@@ -15,6 +15,10 @@ from .errors import HipLaunchError, KernelLoadError, NativeLibraryMissing, NoDev
 LIB_PATH = Path(__file__).resolve().parent / "libtm_hip.so"
 
 TM_DT_NONE, TM_DT_F32, TM_DT_F16, TM_DT_BF16, TM_DT_U8 = -1, 0, 1, 2, 3
+TM_DT_FP8_E4M3, TM_DT_FP8_E5M2, TM_DT_FP8_E4M3B15, TM_DT_FP8_E4M3B8, TM_DT_FP8_E5M2B16 = (
+    4, 5, 6, 7, 8)
+TM_EPI_NONE, TM_EPI_ADD_MATRIX, TM_EPI_ADD_ROWS, TM_EPI_ADD_COLS, TM_EPI_SOFTMAX, \
+    TM_EPI_CHAIN_DOT = range(6)
 TM_ERR_INVALID_ARG, TM_ERR_UNSUPPORTED, TM_ERR_NO_RUNTIME, TM_ERR_NOT_FOUND, TM_ERR_LOAD = (
     -1, -2, -3, -4, -5)
 
@@ -43,6 +47,8 @@ SIGNATURES = {
     "tm_wq_repack_awq": [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp],
     "tm_matmul": [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_linear": [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp],
+    "tm_dot": [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, C.POINTER(C.c_longlong), i32, i32,
+               i32, i32, i32, vp],
     "tm_flash_attention": [vp, vp, vp, vp, vp, i32, i32, i32, i32, C.POINTER(C.c_longlong),
                            C.c_float, i32, i32, vp],
     "tm_kda_workspace_size": [i32, i32, i32, i32, i32, i32],

@@ -332,7 +332,8 @@ def plan_matmul(A, B, C, M, N, K, stream=None) -> Launch:
     _numel_at_least(A, M * K, "A")
     _numel_at_least(B, K * N, "B")
     _numel_at_least(C, M * N, "C")
-    args = (_ptr(A), _ptr(B), _ptr(C), M, N, K, K, N, N, _dt(A, "A"), _dt(C, "C"))
+    idt = _FP8_DT[_TORCH_FP8[A.dtype]] if A.dtype in _TORCH_FP8 else _dt(A, "A")
+    args = (_ptr(A), _ptr(B), _ptr(C), M, N, K, K, N, N, idt, _dt(C, "C"))
     return Launch(_lib.lib().tm_matmul, args, "matmul_kernel", dev, stream)
 
 
@@ -365,6 +366,109 @@ def fused_linear(input, weight, C, bias, M, N, K):
             _dt(C, "C"))
     _run(Launch(_lib.lib().tm_linear, args, "fused_linear", dev))
     return C
+
+
+# tl.dot in general form (A2): strides, batches, FP8, epilogues
+_FP8_DT = {"fp8e4nv": _lib.TM_DT_FP8_E4M3, "fp8e5": _lib.TM_DT_FP8_E5M2,
+           "fp8e4b15": _lib.TM_DT_FP8_E4M3B15, "fp8e4b8": _lib.TM_DT_FP8_E4M3B8,
+           "fp8e5b16": _lib.TM_DT_FP8_E5M2B16}
+_TORCH_FP8 = {torch.float8_e4m3fn: "fp8e4nv", torch.float8_e5m2: "fp8e5"}
+DOT_EPILOGUES = {"none": _lib.TM_EPI_NONE, "add-matrix": _lib.TM_EPI_ADD_MATRIX,
+                 "add-rows": _lib.TM_EPI_ADD_ROWS, "add-cols": _lib.TM_EPI_ADD_COLS,
+                 "softmax": _lib.TM_EPI_SOFTMAX, "chain-dot": _lib.TM_EPI_CHAIN_DOT}
+
+
+def _in_dt(t, what, fp8_format):
+    """dtype code of a dot operand: float tensors by dtype, torch's FP8 dtypes
+    by name, raw uint8 codes by the Triton FP8 format name given."""
+    if t.dtype in _FLOAT_DT:
+        return _FLOAT_DT[t.dtype]
+    if t.dtype in _TORCH_FP8:
+        return _FP8_DT[_TORCH_FP8[t.dtype]]
+    if t.dtype == torch.uint8 and fp8_format is not None:
+        try:
+            return _FP8_DT[fp8_format]
+        except KeyError:
+            raise ValueError(f"unknown FP8 format {fp8_format!r}; one of {sorted(_FP8_DT)}") from None
+    raise TypeError(f"{what}: unsupported dtype {t.dtype} (uint8 FP8 codes need fp8_format=)")
+
+
+def _bmk(t, what):
+    """(batch, d0, d1) sizes and element strides of a 2-D or 3-D view."""
+    if t.dim() == 2:
+        return (1,) + tuple(t.shape), (0,) + tuple(t.stride())
+    if t.dim() == 3:
+        return tuple(t.shape), tuple(t.stride())
+    raise ValueError(f"{what} must be 2-D or 3-D, got {t.dim()}-D")
+
+
+def plan_dot(a, b, c, epilogue="none", z=None, w=None, fp8_format=None, stream=None) -> Launch:
+    """Validate and bind one tl.dot (see dot)."""
+    if epilogue not in DOT_EPILOGUES:
+        raise ValueError(f"epilogue must be one of {sorted(DOT_EPILOGUES)}, got {epilogue!r}")
+    dev = _device_of(a, b, c, z, w)
+    (ba, M, K), sa = _bmk(a, "a")
+    (bb, K2, N), sb = _bmk(b, "b")
+    (bc, Mc, Nc), sc = _bmk(c, "c")
+    if K2 != K or Mc != M:
+        raise ValueError(f"shapes {tuple(a.shape)} @ {tuple(b.shape)} -> {tuple(c.shape)}")
+    batch = max(ba, bb, bc)
+    for nb, what in ((ba, "a"), (bb, "b"), (bc, "c")):
+        if nb not in (1, batch) or (nb == 1 and what == "c" and batch > 1):
+            raise ValueError(f"{what}: batch {nb} does not match {batch}")
+    if ba == 1 and a.dim() == 2:
+        sa = (0,) + sa[1:]
+    if bb == 1 and b.dim() == 2:
+        sb = (0,) + sb[1:]
+    idt = _in_dt(a, "a", fp8_format)
+    if _in_dt(b, "b", fp8_format) != idt:
+        raise TypeError("a and b must share a dtype")
+    L = 0
+    sw = (0, 0)
+    wdt = TM_DT_NONE
+    if epilogue == "chain-dot":
+        if w is None or w.dim() != 2 or w.shape[0] != N:
+            raise ValueError(f"chain-dot needs w [N={N}, L]")
+        L = w.shape[1]
+        sw = tuple(w.stride())
+        wdt = _in_dt(w, "w", fp8_format)
+        if Nc != L:
+            raise ValueError(f"chain-dot output must be [.., M, L={L}], got {tuple(c.shape)}")
+    elif Nc != N:
+        raise ValueError(f"c must be [.., {M}, {N}], got {tuple(c.shape)}")
+    sz = (0, 0, 0)
+    zdt = TM_DT_NONE
+    if epilogue.startswith("add-"):
+        if z is None:
+            raise ValueError(f"{epilogue} needs z")
+        (bz, Mz, Nz), sz = _bmk(z, "z")
+        need = {"add-matrix": (M, N), "add-rows": (M, 1), "add-cols": (1, N)}[epilogue]
+        if Mz < need[0] or Nz < need[1] or bz not in (1, batch):
+            raise ValueError(f"z of shape {tuple(z.shape)} too small for {epilogue}")
+        if bz == 1:
+            sz = (0,) + tuple(sz[1:])
+        zdt = _in_dt(z, "z", fp8_format)
+    strides = (C.c_longlong * 14)(*sa, *sb, *sc, *sz, *sw)
+    args = (_ptr(a), _ptr(b), _ptr(c), _ptr(z), _ptr(w), batch, M, N, K, L, strides,
+            DOT_EPILOGUES[epilogue], idt, _dt(c, "c"), zdt, wdt)
+    launch = Launch(_lib.lib().tm_dot, args, "dot", dev, stream)
+    launch._keep = strides
+    return launch
+
+
+def dot(a, b, c, epilogue="none", z=None, w=None, fp8_format=None):
+    """c = epilogue(a @ b) for 2-D ([M, K] @ [K, N]) or batched 3-D views with
+    any element strides (transposed and column-major views included), the
+    strided tl.dot template of _lowerer_templates.py:1116-1540:
+      "none", "add-matrix" (+ z[.., m, n]), "add-rows" (+ z[.., m, 0]),
+      "add-cols" (+ z[.., 0, n]), "softmax" (over n), "chain-dot" ((a @ b) @ w,
+      w [N, L], c [.., M, L]).
+    Inputs fp16 / bf16 / fp32, torch.float8_e4m3fn / float8_e5m2, or uint8
+    FP8 codes with fp8_format one of "fp8e4nv", "fp8e5", "fp8e4b15", "fp8e4b8",
+    "fp8e5b16"; fp32 accumulation; c's dtype is the output dtype.  z may be c
+    itself (the reference reads the bias from the output buffer)."""
+    _run(plan_dot(a, b, c, epilogue, z, w, fp8_format))
+    return c
 
 
 def make_matmul_kernel(block_m=32, block_n=32, block_k=32, dtype="fp32"):
