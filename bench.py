@@ -15,8 +15,10 @@ The K steps are captured into one HIP graph and replayed (how a decode loop
 issues them); the same K steps enqueued eagerly from Python are reported as
 ``eager_us_per_call``.
 
-The CPU baseline times the CPU oracle (a numpy restatement of the reference's
-arithmetic) on a bounded sample of the same workload on the host cores.
+The CPU baseline times the reference's own CPU path for every configuration
+(its test-side references restated in torch fp32, oracle/cpu_paths.py) on the
+host's threads, after the GPU measurements; attention and KDA on a stated
+sample of heads / steps.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME ...]
                        [--no-cpu] [--list]
@@ -254,9 +256,17 @@ def hbm_copy(dev, nbytes=512 << 20):
 EXTRA = {"hbm_copy": hbm_copy}
 
 
-def time_workload(w, steps, warmup, graph=True):
-    """Average ms per step: eagerly enqueued, and replayed from one HIP graph
-    holding the K steps (the launch pattern of a captured decode loop)."""
+def time_workload(w, steps, warmup, graph=True, budget_s=2.0, min_replays=100):
+    """ms per step.  W warm-up steps, then the K steps captured into one HIP
+    graph (the launch pattern of a captured decode loop) and replayed: each
+    replay is bracketed by synchronisation and timed with HIP events on the
+    launch stream; the per-step time is the median over the replays (at
+    least min_replays while one replay is short, fewer when replays are long,
+    within about budget_s).  The same K steps enqueued eagerly from Python
+    are timed once (eager_ms).  Returns (median_ms, mean_ms, eager_ms,
+    replays)."""
+    import statistics
+
     import torch
     L = w["launches"]
     R = len(L)
@@ -273,7 +283,7 @@ def time_workload(w, steps, warmup, graph=True):
     torch.cuda.synchronize()
     eager_ms = start.elapsed_time(end) / steps
     if not graph:
-        return eager_ms, eager_ms
+        return eager_ms, eager_ms, eager_ms, 1
     g = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
     with torch.cuda.graph(g, stream=cap):
@@ -282,16 +292,20 @@ def time_workload(w, steps, warmup, graph=True):
             L[i % R](sp)
     g.replay()
     torch.cuda.synchronize()
-    start.record(stream)
-    g.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    graph_ms = start.elapsed_time(end) / steps
+    replays = max(3, min(min_replays, int(budget_s / max(1e-6, eager_ms * 1e-3 * steps))))
+    per_step = []
+    for _ in range(replays):
+        torch.cuda.synchronize()
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        per_step.append(start.elapsed_time(end) / steps)
     del g
-    return graph_ms, eager_ms
+    return statistics.median(per_step), statistics.fmean(per_step), eager_ms, replays
 
 
-def summarize(w, ms, eager_ms):
+def summarize(w, ms, mean_ms, eager_ms, replays):
     s = ms * 1e-3
     gbs = w["bytes"] / s / 1e9
     tfl = w["flops"] / s / 1e12
@@ -301,41 +315,118 @@ def summarize(w, ms, eager_ms):
     else:
         roof = dict(bound="mfma", achieved=round(tfl, 2), peak=MFMA_PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(tfl / MFMA_PEAK_TFLOPS, 4))
-    return dict(us_per_call=round(ms * 1e3, 3), eager_us_per_call=round(eager_ms * 1e3, 3),
+    return dict(us_per_call=round(ms * 1e3, 3), mean_us_per_call=round(mean_ms * 1e3, 3),
+                replays=replays, eager_us_per_call=round(eager_ms * 1e3, 3),
                 GBps=round(gbs, 1), TFLOPs=round(tfl, 3), roofline=roof, config=w["config"])
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle on a bounded sample of the headline workload
+# CPU baseline: the reference's own CPU path for each op (its test-side
+# references, restated in torch fp32 in oracle/cpu_paths.py) on the host's
+# threads, outside every GPU timed region
 # ---------------------------------------------------------------------------
-def cpu_baseline(target_s=12.0):
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    import oracle
+
+def _median_time(fn, reps=3, budget_s=4.0):
+    """1 warm-up, then at least `reps` timed runs (more while under budget_s);
+    median wall seconds and the count."""
+    import statistics
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < reps or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline():
+    """Every BASELINE configuration through the reference's CPU path (torch
+    fp32).  W-only matmuls are timed with and without their dequantisation;
+    attention and KDA run on a stated sample of heads.  Units as the GPU
+    numbers: GB/s for W-only and KDA, TFLOP/s for dense and attention."""
+    import torch
+    import torch.nn.functional as F
+
+    from oracle import cpu_paths
     cores = len(os.sched_getaffinity(0))
-    K, G, M = 4096, 128, 1
-    N = 14336 // 4  # sample: a quarter of the output columns per call
-    rng = np.random.default_rng(0)
-    packed = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
-    s = (rng.random((N, K // G)) * 0.019 + 0.001).astype(np.float16).astype(np.float32)
-    z = rng.integers(0, 16, (N, K // G)).astype(np.float32)
-    x = rng.standard_normal((M, K)).astype(np.float16).astype(np.float32)
-    nbytes = N * K // 2 + 4 * N * (K // G) + 2 * M * K + 2 * M * N
-    with threadpool_limits(cores):
-        oracle.int4_matmul(x, packed, s, z, M, N, K, G)  # warm-up
-        times = []
-        t_end = time.perf_counter() + target_s
-        while time.perf_counter() < t_end or len(times) < 3:
-            t0 = time.perf_counter()
-            oracle.int4_matmul(x, packed, s, z, M, N, K, G)
-            times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    return dict(value=round(nbytes / med / 1e9, 3), unit="GB/s", cores=cores, kind="port",
-                sample=f"oracle.int4_matmul (numpy unpack + fp32 dequant + fp64 matmul), "
-                       f"M=1 K=4096 N={N} (1/4 of the columns), {len(times)} reps, median "
-                       f"{med * 1e3:.1f} ms; elementwise numpy single-threaded, BLAS "
-                       f"{cores} threads")
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    out = {}
+
+    def rec(name, secs, n, units_per_call, unit, sample):
+        rate = units_per_call / secs / (1e9 if unit == "GB/s" else 1e12)
+        out[name] = dict(value=round(rate, 4), unit=unit, ms=round(secs * 1e3, 2), reps=n,
+                         sample=sample)
+
+    # C1 dense 512^3, fp16 inputs
+    A, Bm = torch.randn(512, 512, generator=g).half(), torch.randn(512, 512, generator=g).half()
+    t, n = _median_time(lambda: cpu_paths.dense(A, Bm))
+    rec("dense_512", t, n, 2 * 512 ** 3, "TFLOP/s", "full workload")
+    # C3 W4A16, M in {1, 8, 32, 128}
+    K, N, G = 4096, 14336, 128
+    packed = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
+    s4 = (torch.rand(N, K // G, generator=g) * 0.019 + 0.001).half()
+    z4 = torch.randint(0, 16, (N, K // G), generator=g).half()
+    w4 = cpu_paths.w4a16_dequant(packed, s4, z4, K, G)
+    for M in (1, 8, 32, 128):
+        x = torch.randn(M, K, generator=g).half()
+        nbytes = N * K // 2 + 4 * N * (K // G) + 2 * M * K + 2 * M * N
+        t, n = _median_time(lambda: cpu_paths.w4a16(x, packed, s4, z4, K, G))
+        rec(f"w4a16_m{M}", t, n, nbytes, "GB/s", "full workload, unpack + dequantise + matmul")
+        t, n = _median_time(lambda: (x.float() @ w4.T).half())
+        rec(f"w4a16_m{M}_matmul_only", t, n, nbytes, "GB/s",
+            "full workload, matmul on the pre-dequantised fp32 weight")
+    del w4
+    # C2 W8A16, M in {1, 16, 128}
+    N8 = 11008
+    q8 = torch.randint(-127, 128, (N8, K), generator=g, dtype=torch.int8)
+    s8 = (torch.rand(N8, generator=g) * 0.019 + 0.001).half()
+    w8 = cpu_paths.w8a16_dequant(q8, s8)
+    for M in (1, 16, 128):
+        x = torch.randn(M, K, generator=g).half()
+        nbytes = N8 * K + 2 * N8 + 2 * M * K + 2 * M * N8
+        t, n = _median_time(lambda: cpu_paths.w8a16(x, q8, s8))
+        rec(f"w8a16_m{M}", t, n, nbytes, "GB/s", "full workload, dequantise + matmul")
+        t, n = _median_time(lambda: (x.float() @ w8.T).half())
+        rec(f"w8a16_m{M}_matmul_only", t, n, nbytes, "GB/s",
+            "full workload, matmul on the pre-dequantised fp32 weight")
+    del w8
+    # C4 attention, S=4096, D=128: 2 of the 128 (b, h) heads per variant
+    S, D, nh = 4096, 128, 2
+    q, k, v = (torch.randn(1, nh, S, D, generator=g).bfloat16() for _ in range(3))
+    for causal in (True, False):
+        t, n = _median_time(lambda: cpu_paths.ref_attention(q, k, v, causal), budget_s=6.0)
+        flops = 4 * nh * S * S * D // (2 if causal else 1)
+        rec(f"flash_{'causal' if causal else 'full'}", t, n, flops, "TFLOP/s",
+            f"{nh} of the 128 (b, h) heads, _ref_attention in fp32 + logsumexp")
+    # C5 KDA: every head of the workload, the first 1024 of its 8192 steps
+    T, H = 1024, 16
+    qk = [F.normalize(torch.randn(1, T, H, D, generator=g), dim=-1).bfloat16() for _ in range(2)]
+    vk = torch.randn(1, T, H, D, generator=g).bfloat16()
+    bk = torch.sigmoid(torch.randn(1, T, H, generator=g))
+    gk = -F.softplus(torch.randn(1, T, H, D, generator=g))
+    t, n = _median_time(lambda: cpu_paths.kda(qk[0], qk[1], vk, gk, bk), reps=3, budget_s=1.0)
+    nbytes = 4 * T * H * D * 2 + T * H * D * 4 + T * H * 4 + H * D * D * 4
+    rec("kda", t, n, nbytes, "GB/s",
+        f"all 16 heads, the first {T} of the 8192 steps (per-token recurrence in fp32; the "
+        f"build's restatement, the reference has none)")
+    head = out["w4a16_m1"]
+    return dict(value=head["value"], unit="GB/s", cores=cores, kind="port",
+                sample=f"W4A16 M=1 K=4096 N=14336 G=128, full workload: the reference's CPU "
+                       f"path (unpack, dequantise, x @ w^T) in torch fp32, median of "
+                       f"{head['reps']} reps, {head['ms']} ms",
+                threads=torch.get_num_threads(), cpu_model=_cpu_model(),
+                configs={k: v for k, v in out.items() if k != "w4a16_m1"})
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "wq_gemv4_w4a16_m1_hbm_traffic.md"
@@ -384,8 +475,9 @@ def main():
     for name in names:
         log(f"[bench] {name}: setup")
         w = (WORKLOADS.get(name) or EXTRA[name])(dev)
-        ms, eager_ms = time_workload(w, args.steps, args.warmup, graph=not args.eager)
-        results[name] = summarize(w, ms, eager_ms)
+        ms, mean_ms, eager_ms, replays = time_workload(w, args.steps, args.warmup,
+                                                       graph=not args.eager)
+        results[name] = summarize(w, ms, mean_ms, eager_ms, replays)
         log(f"[bench] {name}: {results[name]['us_per_call']} us/call "
             f"{results[name]['GBps']} GB/s {results[name]['TFLOPs']} TFLOP/s")
         del w
@@ -407,8 +499,9 @@ def main():
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic",
-        "timing": "eager" if args.eager else "K steps replayed from one HIP graph; "
-                  "eager_us_per_call is the same loop enqueued from Python",
+        "timing": "eager" if args.eager else "K steps captured in one HIP graph, each replay "
+                  "synchronised and timed with HIP events; per-step time = median over the "
+                  "replays; eager_us_per_call is the same loop enqueued from Python",
         "config": head["config"],
         "roofline": dict(head["roofline"], traffic=profiled_traffic()),
         "workloads": {k: v for k, v in results.items() if k != HEADLINE},
