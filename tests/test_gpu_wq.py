@@ -200,11 +200,13 @@ def _cols(N, n=384, seed=0):
 
 
 @pytest.mark.parametrize("M,K,zeros", [(2, 8192, "f16"), (3, 4096, "u8"), (5, 4096, None),
-                                       (1, 8192, None)])
-def test_int4_gemv_shapes(dev, M, K, zeros):
+                                       (1, 8192, None), (1, 4096, "u8"), (1, 4096, None),
+                                       (1, 8192, "u8")])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int4_gemv_shapes(dev, M, K, zeros, act):
     N, G = 1024, 128
-    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 31 + K, zeros=zeros)
-    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=M * 31 + K, zeros=zeros, act=act)
+    out = torch.empty(M, N, dtype=act, device=dev)
     tm.int4_matmul(x.to(dev), packed.to(dev), out, s.to(dev),
                    None if z is None else z.to(dev), M, N, K, G)
     ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), M, N, K, G)

@@ -84,8 +84,9 @@ extern "C" int tm_flash_attention(const void* q, const void* k, const void* v, v
     char name[64];
     snprintf(name, sizeof name, "flash_fwd_d%d_%s_%s", head_dim,
              dtype == TM_DT_BF16 ? "bf16" : "f16", causal ? "causal" : "full");
+    // causal: one workgroup per pair of query blocks (i, nqb - 1 - i)
     const long long nqb = (seq_len + 127) / 128;
-    const long long grid = nqb * (long long)batch * heads;
+    const long long grid = (causal ? (nqb + 1) / 2 : nqb) * (long long)batch * heads;
     if (grid > 0x7fffffffLL) return fail(TM_ERR_UNSUPPORTED, "tm_flash_attention: grid");
     return launch(flash_kernel(name), dim3((unsigned)grid), dim3(256), 0, stream, p);
   }

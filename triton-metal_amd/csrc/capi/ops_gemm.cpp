@@ -121,6 +121,14 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
                     stream, X, W, Y, S, Z, M, N, K, bias);
     }
   }
+  // linear int4 GEMV: M = 1, G = 128, K = 4096 or 8192 (VALU dot products,
+  // 1 KB of one row per load instruction)
+  if (fast && qbits == 4 && M == 1 && G == 128 && (K == 4096 || K == 8192)) {
+    char name[64];
+    snprintf(name, sizeof name, "wq_gemv4l_%s_z%c_k%d", act, zc, K / 2048);
+    return launch(kernel(name), dim3(N / 16), dim3(512), 0, stream, X, W, Y, S, Z, M, N, K,
+                  bias);
+  }
   // exact-shape int4 GEMV: K = NW * PF * 128, G = 128
   if (fast && qbits == 4 && M <= 8 && G == 128 && (K == 4096 || K == 8192) && aligned16(S) &&
       (!Z || aligned16(Z))) {

@@ -24,7 +24,8 @@
 // operands are read with ds_read_b64_tr_b16.  The next block's copies are in
 // flight while the current block computes.  Softmax runs in the exp2 domain with
 // scale * log2(e) folded into the scores.  Causal: key blocks past a wave's
-// last query are skipped, and the heaviest query blocks are scheduled first.
+// last query are skipped, and a workgroup runs query blocks nqb - 1 - i and i
+// so that every workgroup has the same number of key blocks.
 //
 // General kernel (flash_fwd_general): any head dim <= 128, fp32/fp16/bf16,
 // one thread per query row, fp32 throughout.
@@ -124,48 +125,55 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
   const int nqb = (S + BM - 1) / BM;
   const int BH = p.B * p.H;
   // Work order.  Consecutive workgroups go round-robin to the 8 XCDs
-  // (blockIdx % 8), each with its own L2.  When B*H % 8 == 0, every query
-  // block of head bh runs on XCD bh % 8 and the heads of one XCD are taken
-  // two at a time, their query blocks alternating, so two heads' K and V are
-  // live in that L2 at once.  Within a pair the heaviest (causal) query blocks
-  // of both heads go first: taking one head at a time would start the next
-  // head's heaviest blocks while the last light blocks of the previous one
-  // run, and the causal grid would end with long blocks on a few CUs.
-  int qslot, bh;
-  if ((BH & 7) == 0) {
-    const int x = blockIdx.x & 7, sl = blockIdx.x >> 3;
-    const int hpx = BH >> 3;  // heads per XCD
-    const int pair = sl / (2 * nqb), r = sl - pair * (2 * nqb);
-    if (2 * pair + 1 < hpx) {
-      bh = x + 8 * (2 * pair + (r & 1));
-      qslot = r >> 1;
-    } else {  // an odd count leaves the last head alone: r < nqb
-      bh = x + 8 * (2 * pair);
-      qslot = r;
+  // (blockIdx % 8), each with its own L2; when B*H % 8 == 0 every query block
+  // of head bh runs on XCD bh % 8.
+  // Causal: a workgroup takes query blocks nqb - 1 - i and i of one head, one
+  // after the other (2 (nqb - i) + 2 (i + 1) = 2 nqb + 2 key blocks of 64), so
+  // every workgroup has the same work and the grid ends evenly instead of with
+  // the long blocks of the last heads on a few CUs.
+  // Full: one query block per workgroup; an XCD takes its heads two at a time
+  // with their query blocks alternating, so two heads' K and V are live in
+  // its L2 at once.
+  int bh, qb_first, qb_second, npass;
+  if constexpr (CAUSAL) {
+    const int npair = (nqb + 1) / 2;
+    int pi;
+    if ((BH & 7) == 0) {
+      const int x = blockIdx.x & 7, sl = blockIdx.x >> 3;
+      bh = x + 8 * (sl / npair);
+      pi = sl % npair;
+    } else {
+      bh = blockIdx.x % BH;
+      pi = blockIdx.x / BH;
     }
+    qb_first = nqb - 1 - pi;                 // the heavier block first
+    qb_second = pi;
+    npass = (2 * pi + 1 == nqb) ? 1 : 2;     // the middle block of an odd count
   } else {
-    bh = blockIdx.x % BH;
-    qslot = blockIdx.x / BH;
+    int qslot;
+    if ((BH & 7) == 0) {
+      const int x = blockIdx.x & 7, sl = blockIdx.x >> 3;
+      const int hpx = BH >> 3;  // heads per XCD
+      const int pair = sl / (2 * nqb), r = sl - pair * (2 * nqb);
+      if (2 * pair + 1 < hpx) {
+        bh = x + 8 * (2 * pair + (r & 1));
+        qslot = r >> 1;
+      } else {  // an odd count leaves the last head alone: r < nqb
+        bh = x + 8 * (2 * pair);
+        qslot = r;
+      }
+    } else {
+      bh = blockIdx.x % BH;
+      qslot = blockIdx.x / BH;
+    }
+    qb_first = qb_second = qslot;
+    npass = 1;
   }
-  const int qb = CAUSAL ? nqb - 1 - qslot : qslot;
   const int b = bh / p.H, hh = bh - b * p.H;
   const uint16_t* qg = (const uint16_t*)p.q + b * p.sqb + hh * p.sqh;
   const uint16_t* kg = (const uint16_t*)p.k + b * p.skb + hh * p.skh;
   const uint16_t* vg = (const uint16_t*)p.v + b * p.svb + hh * p.svh;
   uint16_t* og = (uint16_t*)p.o + b * p.sob + hh * p.soh;
-
-  const int q0 = qb * BM + wave * 32;      // first query row of this wave
-  const int qi = q0 + l32;                  // this lane's query row
-  const int qlast_blk = min(qb * BM + BM - 1, S - 1);
-  const int nkb = CAUSAL ? qlast_blk / BN + 1 : (S + BN - 1) / BN;
-
-  // Q^T operands: qreg[c] = Q[qi][16c + 8*h32 .. +8]
-  u4_t qreg[DC];
-#pragma unroll
-  for (int c = 0; c < DC; ++c) {
-    qreg[c] = u4_t{0u, 0u, 0u, 0u};
-    if (qi < S) qreg[c] = ldg128(qg + (long long)qi * p.sqs + 16 * c + 8 * h32);
-  }
 
   // ---- K / V tiles: global -> LDS directly ----------------------------------
   // this lane's piece of each 1 KB block: row rb + lane / (D/8), phys chunk
@@ -202,180 +210,208 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
     }
   };
 
-  f16_t oacc[DT];
-#pragma unroll
-  for (int t = 0; t < DT; ++t) oacc[t] = f16_t{};
-  float m_run = -INFINITY, l_run = 0.0f;
-  const float sl2 = p.sl2;
-
-  // per-lane constants of the transposing V reads
+  // ---- LDS read addresses, fixed per lane --------------------------------------
+  // K operand rows r = 32 kt + l32 keep their swizzle k_swz(r) = k_swz(l32)
+  // for every kt, so the byte offset of chunk 2c + h32 of this lane's row is a
+  // per-lane constant kro[c]; the key half (kt) and the buffer are immediates.
+  // V^T reads: rows r0 = 16 u + tv_row (+8) keep v_swz(tv_row), which only
+  // flips bits 2..3 of the chunk index 4t + cl, so the offset of d tile t is a
+  // per-lane constant vro[t]; u and the row half are immediates.
   const int tg = lane >> 4, tj = lane & 15;
-  const int tv_row = 4 * (tg >> 1) + (tj >> 2);          // + key base
-  const int tv_d = 16 * (tg & 1) + 4 * (tj & 3);         // + 32 dt
-
-  issue_kv(Ks0, Vs0, 0);
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-  __syncthreads();
-
-  // one key block: compute from (ks, vs) while the next block streams into
-  // (kn, vn); BUF is the compile-time buffer parity
-  auto step = [&](auto bufc, int j) {
-    constexpr int BUF = decltype(bufc)::value;
-    const uint16_t* ks = BUF ? Ks1 : Ks0;
-    const uint16_t* vs = BUF ? Vs1 : Vs0;
-    uint16_t* kn = BUF ? Ks0 : Ks1;
-    uint16_t* vn = BUF ? Vs0 : Vs1;
-    const int kv0 = j * BN;
-    const bool more = j + 1 < nkb;
-    if (more) issue_kv(kn, vn, kv0 + BN);
-
-    // a wave whose rows all precede this key block has nothing to do
-    const bool active = !CAUSAL || kv0 <= q0 + 31;
-    if (active) {
-      // raise this wave's issue priority while it feeds the MFMA pipe, so the
-      // co-resident wave's softmax fills the gaps instead of competing
-      __builtin_amdgcn_s_setprio(1);
-      f16_t s[2];
+  const int tv_row = 4 * (tg >> 1) + (tj >> 2);
+  const int tv_d = 16 * (tg & 1) + 4 * (tj & 3);
+  uint32_t kro[DC], vro[DT];
+  {
+    const int ks = k_swz<D>(l32);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) s[kt] = f16_t{};
-      // The two key halves alternate, so consecutive MFMAs are independent;
-      // the K operands of step c + KPD are read while step c multiplies.
-      constexpr int KPD = 2;
-      u4_t ka[DC][2];
-      auto kread = [&](int c) {
+    for (int c = 0; c < DC; ++c) kro[c] = 2u * (uint32_t)(l32 * D + 8 * ((2 * c + h32) ^ ks));
+    const int vsw = v_swz<D>(tv_row);
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int r = kt * 32 + l32;
-          ka[c][kt] = *(const u4_t*)(ks + r * D + 8 * ((2 * c + h32) ^ k_swz<D>(r)));
-        }
-      };
-#pragma unroll
-      for (int c = 0; c < KPD; ++c) kread(c);
-#pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        if (c + KPD < DC) kread(c + KPD);
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) s[kt] = mfma32<BF16>(ka[c][kt], qreg[c], s[kt]);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * KPD, 0);
-#pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        if (c + KPD < DC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      }
-      __builtin_amdgcn_s_setprio(0);
-      // raw scores sc[16 kt + i] of key kv0 + 32 kt + 8 (i / 4) + 4 h32 + i % 4
-      float sc[32];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sc[16 * kt + i] = s[kt][i];
-      if ((kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0)) {
-        // keys past the end, or (causal) past this lane's query row
-        const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int kv = kv0 + 32 * (i >> 4) + 8 * ((i >> 2) & 3) + 4 * h32 + (i & 3);
-          sc[i] = kv > lim ? -INFINITY : sc[i];
-        }
-      }
-      float mx = sc[0];
-#pragma unroll
-      for (int i = 1; i < 32; ++i) mx = fmaxf(mx, sc[i]);
-      {
-        // max with the partner lane l ^ 32 (the other half of this query's keys)
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx),
-                                                         __float_as_uint(mx), false, false);
-        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
-      }
-      // Lazy rescale: the running max only moves when a row's max grows by
-      // more than 2^8 (log2 domain), so p = exp2(s - m) <= 256 and O is
-      // rescaled rarely; l and O always share the same reference m.
-      float alpha = 1.0f;
-      if (mx > m_run + 8.0f) {
-        alpha = fast_exp2(m_run - mx);  // 0 on the first block (m_run = -inf)
-        m_run = mx;
-      }
-      const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
-      float lsum = 0.0f;
-      u4_t pop[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float pv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pv[e] = fast_exp2(__builtin_fmaf(sc[8 * u + e], sl2, -m_use));
-          lsum += pv[e];
-        }
-        pop[u] = pack8(pv, BF16);
-      }
-      l_run = l_run * alpha + lsum;
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // some row's max moved
-#pragma unroll
-        for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
-      }
-      // O^T[d][q] += V^T[d][kv] P^T[kv][q]; MFMA u covers keys
-      //   32 (u/2) + 16 (u%2) + 8 (e/4) + 4 h32 + e % 4
-      __builtin_amdgcn_s_setprio(1);
-      // operand i = DT u + t; the V^T operands of i + VPD are read while i multiplies
-      constexpr int NVO = 4 * DT, VPD = 2;
-      u4_t va[NVO];
-      auto vread = [&](int i) {
-        const int u = i / DT, t = i % DT;
-        const int kb = 32 * (u >> 1) + 16 * (u & 1);
-        const int r0 = kb + tv_row, r1 = r0 + 8;
-        const int c = (32 * t + tv_d) >> 3, off = (32 * t + tv_d) & 7;
-        const u2_t lo = lds_tr16(vs + r0 * D + 8 * (c ^ v_swz<D>(r0)) + off);
-        const u2_t hi = lds_tr16(vs + r1 * D + 8 * (c ^ v_swz<D>(r1)) + off);
-        va[i].x = lo.x; va[i].y = lo.y; va[i].z = hi.x; va[i].w = hi.y;
-      };
-#pragma unroll
-      for (int i = 0; i < VPD; ++i) vread(i);
-#pragma unroll
-      for (int i = 0; i < NVO; ++i) {
-        if (i + VPD < NVO) vread(i + VPD);
-        oacc[i % DT] = mfma32<BF16>(va[i], pop[i / DT], oacc[i % DT]);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * VPD, 0);
-#pragma unroll
-      for (int i = 0; i < NVO; ++i) {
-        if (i + VPD < NVO) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
-      __builtin_amdgcn_s_setprio(0);
+    for (int t = 0; t < DT; ++t) {
+      const int cch = (32 * t + tv_d) >> 3, off = (32 * t + tv_d) & 7;
+      vro[t] = 2u * (uint32_t)(tv_row * D + 8 * (cch ^ vsw) + off);
     }
-    if (more) {
-      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's tile loads landed
-    }
-    __syncthreads();
-  };
-  for (int j = 0; j < nkb; j += 2) {
-    step(std::integral_constant<int, 0>{}, j);
-    if (j + 1 < nkb) step(std::integral_constant<int, 1>{}, j + 1);
   }
 
-  // ---- epilogue: O = O / l, LSE ----------------------------------------------
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (qi < S) {
-    uint16_t* orow = og + (long long)qi * p.sos;
+  const float sl2 = p.sl2;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int qb = pass == 0 ? qb_first : qb_second;
+    const int q0 = qb * BM + wave * 32;      // first query row of this wave
+    const int qi = q0 + l32;                  // this lane's query row
+    const int qlast_blk = min(qb * BM + BM - 1, S - 1);
+    const int nkb = CAUSAL ? qlast_blk / BN + 1 : (S + BN - 1) / BN;
+
+    // Q^T operands: qreg[c] = Q[qi][16c + 8*h32 .. +8]
+    u4_t qreg[DC];
 #pragma unroll
-    for (int t = 0; t < DT; ++t)
+    for (int c = 0; c < DC; ++c) {
+      qreg[c] = u4_t{0u, 0u, 0u, 0u};
+      if (qi < S) qreg[c] = ldg128(qg + (long long)qi * p.sqs + 16 * c + 8 * h32);
+    }
+
+    f16_t oacc[DT];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = t * 32 + 8 * g + 4 * h32;
-        u2_t w;
-        if (BF16) {
-          w.x = pack_bf16x2(oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv);
-          w.y = pack_bf16x2(oacc[t][4 * g + 2] * inv, oacc[t][4 * g + 3] * inv);
-        } else {
-          w.x = pack_f16x2(oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv);
-          w.y = pack_f16x2(oacc[t][4 * g + 2] * inv, oacc[t][4 * g + 3] * inv);
+    for (int t = 0; t < DT; ++t) oacc[t] = f16_t{};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    issue_kv(Ks0, Vs0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+
+    // one key block: compute from (ks, vs) while the next block streams into
+    // (kn, vn); BUF is the compile-time buffer parity
+    auto step = [&](auto bufc, int j) {
+      constexpr int BUF = decltype(bufc)::value;
+      const char* ks = (const char*)(BUF ? Ks1 : Ks0);
+      const char* vs = (const char*)(BUF ? Vs1 : Vs0);
+      uint16_t* kn = BUF ? Ks0 : Ks1;
+      uint16_t* vn = BUF ? Vs0 : Vs1;
+      const int kv0 = j * BN;
+      const bool more = j + 1 < nkb;
+      if (more) issue_kv(kn, vn, kv0 + BN);
+
+      // a wave whose rows all precede this key block has nothing to do
+      const bool active = !CAUSAL || kv0 <= q0 + 31;
+      if (active) {
+        // raise this wave's issue priority while it feeds the MFMA pipe, so the
+        // co-resident wave's softmax fills the gaps instead of competing
+        __builtin_amdgcn_s_setprio(1);
+        f16_t s[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s[kt] = f16_t{};
+        // The two key halves alternate, so consecutive MFMAs are independent;
+        // the K operands of step c + KPD are read while step c multiplies.
+        constexpr int KPD = 2;
+        u4_t ka[DC][2];
+        auto kread = [&](int c) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) ka[c][kt] = *(const u4_t*)(ks + kro[c] + kt * 32 * D * 2);
+        };
+#pragma unroll
+        for (int c = 0; c < KPD; ++c) kread(c);
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          if (c + KPD < DC) kread(c + KPD);
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) s[kt] = mfma32<BF16>(ka[c][kt], qreg[c], s[kt]);
         }
-        *(u2_t*)(orow + d) = w;
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * KPD, 0);
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          if (c + KPD < DC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        // raw scores sc[16 kt + i] of key kv0 + 32 kt + 8 (i / 4) + 4 h32 + i % 4
+        float sc[32];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[16 * kt + i] = s[kt][i];
+        if ((kv0 + BN > S) || (CAUSAL && kv0 + BN - 1 > q0)) {
+          // keys past the end, or (causal) past this lane's query row
+          const int lim = CAUSAL ? min(qi, S - 1) : S - 1;
+#pragma unroll
+          for (int i = 0; i < 32; ++i) {
+            const int kv = kv0 + 32 * (i >> 4) + 8 * ((i >> 2) & 3) + 4 * h32 + (i & 3);
+            sc[i] = kv > lim ? -INFINITY : sc[i];
+          }
+        }
+        float mx = sc[0];
+#pragma unroll
+        for (int i = 1; i < 32; ++i) mx = fmaxf(mx, sc[i]);
+        {
+          // max with the partner lane l ^ 32 (the other half of this query's keys)
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx),
+                                                           __float_as_uint(mx), false, false);
+          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
+        }
+        // Lazy rescale: the running max only moves when a row's max grows by
+        // more than 2^8 (log2 domain), so p = exp2(s - m) <= 256 and O is
+        // rescaled rarely; l and O always share the same reference m.
+        float alpha = 1.0f;
+        if (mx > m_run + 8.0f) {
+          alpha = fast_exp2(m_run - mx);  // 0 on the first block (m_run = -inf)
+          m_run = mx;
+        }
+        const float m_use = (m_run == -INFINITY) ? 0.0f : m_run;
+        float lsum = 0.0f;
+        u4_t pop[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          float pv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            pv[e] = fast_exp2(__builtin_fmaf(sc[8 * u + e], sl2, -m_use));
+            lsum += pv[e];
+          }
+          pop[u] = pack8(pv, BF16);
+        }
+        l_run = l_run * alpha + lsum;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // some row's max moved
+#pragma unroll
+          for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+        }
+        // O^T[d][q] += V^T[d][kv] P^T[kv][q]; MFMA u covers keys
+        //   32 (u/2) + 16 (u%2) + 8 (e/4) + 4 h32 + e % 4
+        __builtin_amdgcn_s_setprio(1);
+        // operand i = DT u + t; the V^T operands of i + VPD are read while i multiplies
+        constexpr int NVO = 4 * DT, VPD = 2;
+        u4_t va[NVO];
+        auto vread = [&](int i) {
+          const int u = i / DT, t = i % DT;
+          const u2_t lo = lds_tr16((const uint16_t*)(vs + vro[t] + 16 * u * D * 2));
+          const u2_t hi = lds_tr16((const uint16_t*)(vs + vro[t] + (16 * u + 8) * D * 2));
+          va[i].x = lo.x; va[i].y = lo.y; va[i].z = hi.x; va[i].w = hi.y;
+        };
+#pragma unroll
+        for (int i = 0; i < VPD; ++i) vread(i);
+#pragma unroll
+        for (int i = 0; i < NVO; ++i) {
+          if (i + VPD < NVO) vread(i + VPD);
+          oacc[i % DT] = mfma32<BF16>(va[i], pop[i / DT], oacc[i % DT]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * VPD, 0);
+#pragma unroll
+        for (int i = 0; i < NVO; ++i) {
+          if (i + VPD < NVO) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
       }
-    if (p.lse && h32 == 0)
-      p.lse[(long long)bh * S + qi] = l_tot > 0.0f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+      if (more) {
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's tile loads landed
+      }
+      __syncthreads();
+    };
+    for (int j = 0; j < nkb; j += 2) {
+      step(std::integral_constant<int, 0>{}, j);
+      if (j + 1 < nkb) step(std::integral_constant<int, 1>{}, j + 1);
+    }
+
+    // ---- epilogue: O = O / l, LSE ----------------------------------------------
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (qi < S) {
+      uint16_t* orow = og + (long long)qi * p.sos;
+#pragma unroll
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = t * 32 + 8 * g + 4 * h32;
+          u2_t w;
+          if (BF16) {
+            w.x = pack_bf16x2(oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv);
+            w.y = pack_bf16x2(oacc[t][4 * g + 2] * inv, oacc[t][4 * g + 3] * inv);
+          } else {
+            w.x = pack_f16x2(oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv);
+            w.y = pack_f16x2(oacc[t][4 * g + 2] * inv, oacc[t][4 * g + 3] * inv);
+          }
+          *(u2_t*)(orow + d) = w;
+        }
+      if (p.lse && h32 == 0)
+        p.lse[(long long)bh * S + qi] = l_tot > 0.0f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+    }
   }
 }
 

@@ -25,8 +25,10 @@
 // is staged into LDS.
 //
 // Kernels
-//   wq_gemv4_*   int4, M = 1 (and M <= 8 when K = 8192): GEMV, the whole grid
-//                resident, per-chunk MFMAs as the weights land.
+//   wq_gemv4l_*  int4, M = 1, K = 4096 / 8192: GEMV with 1 KB linear weight
+//                loads per instruction and VALU dot products.
+//   wq_gemv4_*   int4, M <= 8 when K = 8192: GEMV, the whole grid resident,
+//                per-chunk MFMAs as the weights land.
 //   wq_gemv4x2_* int4, 2 <= M <= 6, K = 4096: the GEMV with two column tiles
 //                per workgroup and MFMA row sums.
 //   wq_gemv8_*   int8, M = 1, K = 4096: the GEMV layout for int8 weights.
@@ -521,6 +523,128 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
       const int row = 4 * q + e;
       if (row < M) store_out(Y, (size_t)row * N + n, y[e] + bias_at(bias, n, BF16), BF16);
     }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Linear int4 GEMV, M = 1, K = 2048 * NS, G = 128: wq_gemv4l_<act>_z<zs>_k<NS>.
+// grid.x = N / 16, block = 512 (8 waves); the workgroup owns 16 weight rows
+// (16 * K / 2 contiguous bytes).  Every weight load instruction reads 1 KB of
+// one row (lane l: bytes 1024 h + 16 l): whole 128-byte lines, consecutive
+// lines per instruction, non-temporal - the pattern that streams fastest
+// (a plain read of the C3 weights this way takes 6.5 us on a box where the
+// 16 rows x 64 B pattern of the MFMA GEMV takes 7.4 us).  Wave w takes K
+// slice h = w % NS of rows RW * (w / NS) .. +RW (RW = 2 NS), so each lane's
+// 32 activations x[2048 h + 32 l .. +32] serve all its rows and its 32 k lie
+// in one quantisation group g = 16 h + l / 4.  X comes straight from global
+// memory (L2-resident after the first workgroups): staging it (and the scales)
+// through LDS behind a workgroup barrier measured slower.
+// M = 1 leaves 15 of 16 MFMA rows idle, so the dot products run on the VALU:
+// the exact half OFF + q (fp16: a nibble ORed under 0x6400 is 1024 + q, under
+// 0x5400 at bits 4..7 it is 64 + q; bf16: under 0x4300 it is 128 + q) times
+// pairs of x with v_dot2_f32_{f16,bf16} into fp32, then per row
+// s * (sum x (OFF + q) - sum x OFF - z sum x).  The 64 lanes of a row are
+// summed with DPP / shuffles and the NS slices through LDS.
+// ----------------------------------------------------------------------------
+template <bool BF16, int ZDT, int NS>
+__device__ __forceinline__ void wq_gemv4l_body(const uint16_t* __restrict__ X,
+                                               const uint8_t* __restrict__ W,
+                                               uint16_t* __restrict__ Y,
+                                               const uint16_t* __restrict__ S,
+                                               const void* __restrict__ Z, int N,
+                                               const uint16_t* bias) {
+  constexpr int K = 2048 * NS, RB = K / 2, NG = K / 128, RW = 2 * NS;
+  constexpr int SDT = BF16 ? TM_DT_BF16 : TM_DT_F16;
+  __shared__ float red[NS][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = wave % NS, r0 = RW * (wave / NS);
+  const int n0 = blockIdx.x * 16;
+  const int g = 16 * h + (lane >> 2);
+
+  // activations first (short L2 latency, needed before any dot), then the
+  // weights, then the scales / zero-points (needed last)
+  u4_t xr[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) xr[j] = ldg128(X + 2048 * h + 32 * lane + 8 * j);
+  const uint8_t* wb = W + (size_t)(n0 + r0) * RB + 1024 * h + 16 * lane;
+  u4_t wv[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
+    wv[i] = __builtin_nontemporal_load((const u4_t*)(wb + (size_t)i * RB));
+  float sc[RW], zp[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const size_t gi = (size_t)(n0 + r0 + i) * NG + g;
+    sc[i] = raw_to_f32<SDT>(S[gi]);
+    zp[i] = 0.0f;
+    if constexpr (ZDT == 3) zp[i] = (float)((const uint8_t*)Z)[gi];
+    else if constexpr (ZDT >= 0) zp[i] = raw_to_f32<ZDT>(((const uint16_t*)Z)[gi]);
+  }
+
+  // x as operand pairs (x0, x4) (x1, x5) (x2, x6) (x3, x7) per 8-k word, and
+  // its sums
+  u4_t xp[4];
+  float xsum = 0.0f, xoff = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    xp[j] = perm_x8(xr[j]);
+    xsum += sum8<BF16>(xr[j]);
+    if constexpr (!BF16) xoff += sumoff8_h(xr[j]);
+  }
+  if constexpr (BF16) xoff = w4_offset<true>() * xsum;
+
+  const uint32_t m_lo = vgpr_const(0x000F000Fu), g_lo = vgpr_const(w4_magic<BF16>());
+  const uint32_t m_hi = vgpr_const(0x00F000F0u), g_hi = vgpr_const(0x54005400u);
+  float part[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (BF16) {
+        // (128 + n0, 128 + n4), ...; the pairs are taken from 8-element
+        // vectors (a bit cast of one dword to a bf16 pair is mis-selected by
+        // this compiler: every such dot reads the first dword)
+        const b8_t op = __builtin_bit_cast(b8_t, w4_operand(wd[j], m_lo, g_lo));
+        const b8_t xb = __builtin_bit_cast(b8_t, xp[j]);
+        a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(op, op, 0, 1),
+                                            __builtin_shufflevector(xb, xb, 0, 1), a, false);
+        a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(op, op, 2, 3),
+                                            __builtin_shufflevector(xb, xb, 2, 3), a, false);
+        a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(op, op, 4, 5),
+                                            __builtin_shufflevector(xb, xb, 4, 5), a, false);
+        a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(op, op, 6, 7),
+                                            __builtin_shufflevector(xb, xb, 6, 7), a, false);
+      } else {
+        const u4_t op = w4_operand_h(wd[j], m_lo, m_hi, g_lo, g_hi);
+        a = __builtin_amdgcn_fdot2(as_h2(op.x), as_h2(xp[j].x), a, false);
+        a = __builtin_amdgcn_fdot2(as_h2(op.y), as_h2(xp[j].y), a, false);
+        a = __builtin_amdgcn_fdot2(as_h2(op.z), as_h2(xp[j].z), a, false);
+        a = __builtin_amdgcn_fdot2(as_h2(op.w), as_h2(xp[j].w), a, false);
+      }
+    }
+    part[i] = sc[i] * (a - xoff - zp[i] * xsum);
+  }
+  // sum each row's 64 lanes: DPP within rows of 16, then across the 4 rows
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    float v = row16_sum(part[i]);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    part[i] = v;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < RW; ++i) red[h][r0 + i] = part[i];
+  }
+  __syncthreads();
+  if (tid < 16) {
+    float y = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) y += red[s2][tid];
+    const int n = n0 + tid;
+    store_out(Y, n, y + bias_at(bias, n, BF16), BF16);
   }
 }
 
@@ -1646,6 +1770,23 @@ TM_GEMV4_Z(false, f16, 4, 8)
 TM_GEMV4_Z(true, bf16, 4, 8)
 TM_GEMV4_Z(false, f16, 8, 8)
 TM_GEMV4_Z(true, bf16, 8, 8)
+
+// Linear GEMV (int4, M = 1, K = 2048 * NS, G = 128): wq_gemv4l_<act>_z<zs>_k<NS>
+#define TM_GEMV4L(BF, ACT, ZS, ZDT, NS)                                                         \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8))) void     \
+      wq_gemv4l_##ACT##_z##ZS##_k##NS(const uint16_t* X, const uint8_t* W, uint16_t* Y,         \
+                                      const uint16_t* S, const void* Z, int M, int N, int K,    \
+                                      const uint16_t* bias) {                                   \
+    wq_gemv4l_body<BF, ZDT, NS>(X, W, Y, S, Z, N, bias);                                        \
+  }
+#define TM_GEMV4L_Z(BF, ACT, NS)                                 \
+  TM_GEMV4L(BF, ACT, n, -1, NS)                                  \
+  TM_GEMV4L(BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), NS)       \
+  TM_GEMV4L(BF, ACT, u, 3, NS)
+TM_GEMV4L_Z(false, f16, 2)
+TM_GEMV4L_Z(true, bf16, 2)
+TM_GEMV4L_Z(false, f16, 4)
+TM_GEMV4L_Z(true, bf16, 4)
 
 // Two-tile GEMV (2 <= M <= 8, K = 4096, G = 128): wq_gemv4x2_<act>_z<zs>_w8p4,
 // 8 waves, two workgroups per CU (<= 128 VGPRs).
