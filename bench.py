@@ -132,25 +132,30 @@ def kda(dev, B=1, H=16, T=8192, D=128, C=64):
     import torch
     import torch.nn.functional as F
     import triton_metal_amd as tm
-    g = torch.Generator(device=dev).manual_seed(5)
-    q = F.normalize(torch.randn(B, T, H, D, device=dev, generator=g).bfloat16().float(),
-                    dim=-1).bfloat16()
-    k = F.normalize(torch.randn(B, T, H, D, device=dev, generator=g).bfloat16().float(),
-                    dim=-1).bfloat16()
-    v = torch.randn(B, T, H, D, device=dev, generator=g).bfloat16()
-    beta = torch.sigmoid(torch.randn(B, T, H, device=dev, generator=g))
-    gl = -F.softplus(torch.randn(B, T, H, D, device=dev, generator=g))
-    o = torch.empty_like(v)
-    st = torch.empty(B, H, D, D, device=dev, dtype=torch.float32)
-    launches = [tm.plan_chunk_kda(q, k, v, gl, beta, o, final_state=st)]
     # q, k, v, o bf16 + g fp32 + beta fp32 + final state fp32
     nbytes = 4 * B * T * H * D * 2 + B * T * H * D * 4 + B * T * H * 4 + B * H * D * D * 4
+    R = _nsets(nbytes)  # input sets rotated past the 256 MB Infinity Cache
+    g = torch.Generator(device=dev).manual_seed(5)
+    ws = torch.empty(tm.kda_workspace_size(B, T, H), dtype=torch.uint8, device=dev)
+    launches, keep = [], [ws]
+    for _ in range(R):
+        q = F.normalize(torch.randn(B, T, H, D, device=dev, generator=g).bfloat16().float(),
+                        dim=-1).bfloat16()
+        k = F.normalize(torch.randn(B, T, H, D, device=dev, generator=g).bfloat16().float(),
+                        dim=-1).bfloat16()
+        v = torch.randn(B, T, H, D, device=dev, generator=g).bfloat16()
+        beta = torch.sigmoid(torch.randn(B, T, H, device=dev, generator=g))
+        gl = -F.softplus(torch.randn(B, T, H, D, device=dev, generator=g))
+        o = torch.empty_like(v)
+        st = torch.empty(B, H, D, D, device=dev, dtype=torch.float32)
+        launches.append(tm.plan_chunk_kda(q, k, v, gl, beta, o, final_state=st, workspace=ws))
+        keep += [q, k, v, beta, gl, o, st]
     nc = -(-T // C)
     per_chunk = 2 * C * C * D * 3 + 2 * C * C * D * 2 + 2 * C * D * D * 3 + C ** 3 // 3
-    return dict(launches=launches, keep=(q, k, v, beta, gl, o, st), bytes=nbytes,
+    return dict(launches=launches, keep=keep, bytes=nbytes,
                 flops=per_chunk * nc * B * H, bound="hbm", dtype="bf16",
                 config={"workload": "kda_chunk_fwd", "B": B, "H": H, "T": T, "Dk": D,
-                        "Dv": D, "chunk": C})
+                        "Dv": D, "chunk": C, "input_sets_rotated": R})
 
 
 def kda_decode(dev, B=16, H=16, D=128):

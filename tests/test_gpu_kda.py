@@ -157,14 +157,15 @@ def test_kda_orthonormal_keys_retrieval(dev):
     _close(o[0, 7:, 0], v[0, :-7, 0].double().numpy(), "retrieved values")
 
 
-def test_kda_split_sequence_bitwise(dev):
+@pytest.mark.parametrize("T", [512, 2048, 4096])
+def test_kda_split_sequence_bitwise(dev, T):
     """Running T steps at once equals running the first half, then the second
     half from the first half's final state (chunk-aligned split): the state
     handed over is the kernel's own fp32 state, so the results are identical."""
-    B, T, H = 1, 512, 4
+    B, H = 1, 4
     q, k, v, g, beta = (t.to(dev) for t in kda_inputs(B, T, H, seed=21, gscale=0.05))
     o_all, st_all = tm.chunk_kda(q, k, v, g, beta, output_final_state=True)
-    h = 256
+    h = T // 2
     o1, st1 = tm.chunk_kda(q[:, :h].contiguous(), k[:, :h].contiguous(), v[:, :h].contiguous(),
                            g[:, :h].contiguous(), beta[:, :h].contiguous(),
                            output_final_state=True)

@@ -25,6 +25,7 @@ struct KdaParams {
   float* st;
   void* ws;
   int B, T, H, NC;
+  int c0, c1;
   float scale;
   int beta_bf16;
 };
@@ -104,10 +105,12 @@ extern "C" int tm_kda_chunk_fwd(const void* q, const void* k, const void* v, con
   if (nc > 0) {
     // one workgroup per CU (its LDS admits no second), each walking its share of
     // the chunks
+    p.c0 = 0; p.c1 = (int)nc;
     const long long grid = std::min<long long>(bh * nc, (long long)cu_count());
     const int rc = launch(intra_kernel(), dim3((unsigned)grid), dim3(256), 0, stream, p);
     if (rc) return rc;
   }
+  p.c0 = 0; p.c1 = (int)nc;
   return launch(state_kernel(), dim3((unsigned)(bh * (kValueDim / 16))), dim3(256), 0, stream, p);
 }
 

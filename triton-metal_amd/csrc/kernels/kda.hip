@@ -100,6 +100,7 @@ struct KdaParams {
   float* st;           // [B, H, KD, VD] fp32 or null
   uint8_t* ws;         // workspace: B*H*NC chunks of WS_CHUNK bytes
   int B, T, H, NC;
+  int c0, c1;          // the chunks [c0, c1) of every (batch, head) this launch covers
   float scale;
   int beta_bf16;
 };
@@ -140,15 +141,18 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
   const int c4 = tid & 31, seg = tid >> 5;  // channels 4c4.., rows 8seg..8seg+7
   const int r0 = 16 * wave;     // first row of this wave's 16-row block
   const int trow = r0 + l16;    // A-operand row of this lane
-  const int total = p.B * p.H * p.NC;
+  const int nsc = p.c1 - p.c0;  // chunks per (batch, head) in this launch
+  const int total = p.B * p.H * nsc;
 
   struct Chunk {
+    int gidx;  // workspace chunk index bh * NC + chunk
     int b, h, t0, nt;
     long long base_k, base_v;
   };
   auto locate = [&](int idx) {
     Chunk c;
-    const int chunk = idx % p.NC, bh = idx / p.NC;
+    const int bh = idx / nsc, chunk = p.c0 + (idx - bh * nsc);
+    c.gidx = bh * p.NC + chunk;
     c.b = bh / p.H;
     c.h = bh - c.b * p.H;
     c.t0 = chunk * KC;
@@ -199,7 +203,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
   const Chunk nxt = locate(has_next ? nidx : idx);
   const int nt = cur.nt;
   const long long base_k = cur.base_k;
-  uint8_t* ws = p.ws + (size_t)idx * WS_CHUNK;
+  uint8_t* ws = p.ws + (size_t)cur.gidx * WS_CHUNK;
 
   // ---- 1. g (cumulative sum), k and v to LDS, beta ---------------------------
   if (tid < KC) bet[tid] = bv;
@@ -509,7 +513,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
   // into `nxt`.
   auto step = [&](const int c, auto bufc, const ChunkOps& cur, ChunkOps& nxt) {
     constexpr int BUF = decltype(bufc)::value;
-    const uint8_t* wsn = wsh + (size_t)min(c + 1, p.NC - 1) * WS_CHUNK;
+    const uint8_t* wsn = wsh + (size_t)min(c + 1, p.c1 - 1) * WS_CHUNK;
     load_chunk_a(wsn, wave, lane, nxt);
     asm volatile("" ::: "memory");  // issue points of the next chunk's loads stay spread
 
@@ -572,15 +576,15 @@ extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
     }
   };
   ChunkOps ops0, ops1;
-  if (p.NC > 0) load_chunk(wsh, wave, lane, q4, v0, ops0);
+  if (p.c1 > p.c0) load_chunk(wsh + (size_t)p.c0 * WS_CHUNK, wave, lane, q4, v0, ops0);
   // pairs of steps with no branch between them, so that each operand set
   // keeps its registers around the loop; an odd last chunk after the loop
-  int c = 0;
-  for (; c + 1 < p.NC; c += 2) {
+  int c = p.c0;
+  for (; c + 1 < p.c1; c += 2) {
     step(c, std::integral_constant<int, 0>(), ops0, ops1);
     step(c + 1, std::integral_constant<int, 1>(), ops1, ops0);
   }
-  if (c < p.NC) step(c, std::integral_constant<int, 0>(), ops0, ops1);
+  if (c < p.c1) step(c, std::integral_constant<int, 0>(), ops0, ops1);
 
   if (p.st) {
 #pragma unroll
