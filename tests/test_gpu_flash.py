@@ -79,7 +79,7 @@ def test_flash_attn_fwd_signature(dev, causal, shape, dtype):
 
 
 # --- MFMA path: shapes, partial tiles, LSE ---------------------------------------
-@pytest.mark.parametrize("S", [1, 17, 64, 100, 128, 257])
+@pytest.mark.parametrize("S", [1, 17, 64, 100, 128, 257, 511, 777, 1025])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
