@@ -289,3 +289,54 @@ def test_kda_recurrent_unaligned_state_buffers(dev):
         torch.cuda.synchronize()
         _close(o.float().cpu().numpy(), o_ref, f"o, state offset {off}")
         _close(st.cpu().numpy(), st_ref, f"final state, state offset {off}")
+
+
+# --- reuse of one workspace and of a captured graph ------------------------------
+def _run_raw(dev, q, k, v, g, beta, workspace=None):
+    """One call through the plan (the device tensors are used as given)."""
+    B, T, H, _ = q.shape
+    o = torch.empty_like(v)
+    st = torch.empty(B, H, 128, 128, dtype=torch.float32, device=dev)
+    tm.plan_chunk_kda(q, k, v, g, beta, o, final_state=st, workspace=workspace)()
+    torch.cuda.synchronize()
+    return o, st
+
+
+def test_kda_workspace_reused_across_calls(dev):
+    """One workspace for three calls with different inputs: every chunk's
+    workspace is rewritten before it is read, so no call sees another's."""
+    B, T, H = 1, 700, 3
+    ins = [[t.to(dev) for t in kda_inputs(B, T, H, seed=s)] for s in (21, 22)]
+    ws = torch.empty(tm.kda_workspace_size(B, T, H), dtype=torch.uint8, device=dev)
+    fresh = [_run_raw(dev, *x) for x in ins]
+    for x, (o_ref, st_ref) in zip(ins + ins[:1], fresh + fresh[:1]):
+        o, st = _run_raw(dev, *x, workspace=ws)
+        assert torch.equal(o, o_ref) and torch.equal(st, st_ref)
+
+
+def test_kda_graph_replays_track_new_inputs(dev):
+    """The call captured in a HIP graph and replayed three times, new inputs
+    copied in and eager work in between: every replay equals the eager call on
+    the same inputs."""
+    B, T, H = 1, 1024, 16
+    q, k, v, g, beta = (t.to(dev) for t in kda_inputs(B, T, H, seed=31))
+    o = torch.empty_like(v)
+    st = torch.empty(B, H, 128, 128, dtype=torch.float32, device=dev)
+    plan = tm.plan_chunk_kda(q, k, v, g, beta, o, final_state=st)
+    plan()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=cap):
+        plan(torch.cuda.current_stream().cuda_stream)
+    for seed in (41, 42, 43):
+        new = [t.to(dev) for t in kda_inputs(B, T, H, seed=seed)]
+        for dst, src in zip((q, k, v, g, beta), new):
+            dst.copy_(src)
+        o_ref, st_ref = _run_raw(dev, *new)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref), f"replay with inputs {seed}: o"
+        assert torch.equal(st, st_ref), f"replay with inputs {seed}: final state"
+    del graph
