@@ -1517,6 +1517,42 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
     else wait_vm<0>();
     lds_barrier();  // all waves' copies of stage c, and stage (c - 1) % NS is free
     if (c + NS - 1 < NC) issue(c + NS - 1);
+    if constexpr (QB == 4) {
+      if (c == 0) {
+        // once: the scales / zero-points [row][group] as copied become
+        // [group][row], so that the 32 rows a wave reads per chunk are
+        // consecutive (read row-major they sit 2 ng bytes apart, all in 4 of
+        // the 64 banks).  Through registers: the LDS holds no second copy.
+        uint8_t* sl = lds + NS * ST;
+        const int ns = 128 * ng;  // entries per block
+        u4_t sv = {0u, 0u, 0u, 0u}, zv = {0u, 0u, 0u, 0u};
+        const int zper = ZDT == 3 ? 16 : 8;  // zero-points per thread
+        const bool hs = 8 * tid < ns, hz = ZDT >= 0 && zper * tid < ns;
+        if (hs) sv = *(const u4_t*)(sl + 16 * tid);
+        if (hz) zv = *(const u4_t*)(sl + 256 * ng + 16 * tid);
+        lds_barrier();
+        if (hs) {
+          const uint32_t w[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int i = 8 * tid + e, row = i / ng, g = i - row * ng;
+            ((uint16_t*)sl)[g * 128 + row] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+          }
+        }
+        if (hz) {
+          const uint32_t w[4] = {zv.x, zv.y, zv.z, zv.w};
+#pragma unroll
+          for (int e = 0; e < zper; ++e) {
+            const int i = zper * tid + e, row = i / ng, g = i - row * ng;
+            if constexpr (ZDT == 3)
+              (sl + 256 * ng)[g * 128 + row] = (uint8_t)(w[e >> 2] >> (8 * (e & 3)));
+            else
+              ((uint16_t*)(sl + 256 * ng))[g * 128 + row] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+          }
+        }
+        lds_barrier();
+      }
+    }
 
     const uint8_t* st = lds + (c % NS) * ST;
     u4_t braw[2];
@@ -1533,7 +1569,7 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
       bool frac = false;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const int gi = (64 * wn + 32 * t + r32) * ng + gg;
+        const int gi = gg * 128 + 64 * wn + 32 * t + r32;  // [group][row]
         const uint16_t sbits = ((const uint16_t*)sl)[gi];
         sf[t] = f16_bits_to_f32(sbits);
         zf[t] = 0.0f;
