@@ -604,7 +604,10 @@ extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
 // columns v0 .. v0+15 of one head (64-byte pieces of each state row): lane
 // 16 rg + c holds S[32 rg + r][v0 + c] (r < 32) in registers for all steps,
 // so both reductions over the key dimension (S^T k and S^T q) are 32 in-lane
-// FMAs and two shuffles.
+// FMAs and two shuffles.  The state is read and written once per call,
+// non-temporal: a call streams every state through once, and keeping the
+// reads and the write-backs out of the caches halves their interference
+// (B=16, H=16, one token: 14.4 -> 11.2 us).
 // Per step t:  S <- diag(exp(g_t)) S;  u = beta_t (v_t - S^T k_t);
 //              S <- S + k_t u^T;       o_t = S^T (scale q_t).
 // ----------------------------------------------------------------------------
@@ -617,7 +620,8 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent(KdaParams p) {
   const size_t sb = (size_t)bh * KD * VD;
   float S[RL];
 #pragma unroll
-  for (int r = 0; r < RL; ++r) S[r] = p.s0 ? p.s0[sb + (size_t)(i0 + r) * VD + col] : 0.0f;
+  for (int r = 0; r < RL; ++r)
+    S[r] = p.s0 ? __builtin_nontemporal_load(p.s0 + sb + (size_t)(i0 + r) * VD + col) : 0.0f;
   const long long rs = (long long)p.H * KD, rsv = (long long)p.H * VD;
   for (int t = 0; t < p.T; ++t) {
     const long long tk = ((long long)b * p.T + t) * rs + (long long)h * KD + i0;
@@ -654,7 +658,8 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent(KdaParams p) {
   }
   if (p.st) {
 #pragma unroll
-    for (int r = 0; r < RL; ++r) p.st[sb + (size_t)(i0 + r) * VD + col] = S[r];
+    for (int r = 0; r < RL; ++r)
+      __builtin_nontemporal_store(S[r], p.st + sb + (size_t)(i0 + r) * VD + col);
   }
 }
 
@@ -673,7 +678,8 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent_v4(KdaParams p) {
   f4_t S[RL];
 #pragma unroll
   for (int r = 0; r < RL; ++r)
-    S[r] = p.s0 ? *(const f4_t*)(p.s0 + sb + (size_t)(i0 + r) * VD + col) : f4_t{0.f, 0.f, 0.f, 0.f};
+    S[r] = p.s0 ? __builtin_nontemporal_load((const f4_t*)(p.s0 + sb + (size_t)(i0 + r) * VD + col))
+                : f4_t{0.f, 0.f, 0.f, 0.f};
   const long long rs = (long long)p.H * KD, rsv = (long long)p.H * VD;
   for (int t = 0; t < p.T; ++t) {
     const long long tk = ((long long)b * p.T + t) * rs + (long long)h * KD + i0;
@@ -716,5 +722,6 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent_v4(KdaParams p) {
   }
   if (p.st)
 #pragma unroll
-    for (int r = 0; r < RL; ++r) *(f4_t*)(p.st + sb + (size_t)(i0 + r) * VD + col) = S[r];
+    for (int r = 0; r < RL; ++r)
+      __builtin_nontemporal_store(S[r], (f4_t*)(p.st + sb + (size_t)(i0 + r) * VD + col));
 }
