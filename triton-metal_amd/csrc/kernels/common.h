@@ -139,6 +139,13 @@ TM_DEV void dma16(const void* g, uint32_t lds) {
                "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory", "m0");
 }
+// The same copy, non-temporal: for data read once (a weight or KV-cache
+// stream), so that it does not displace what is reused from the caches.
+TM_DEV void dma16_nt(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(g),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
+}
 // The same copy from a wave-uniform base plus a 32-bit byte offset per lane
 // (one VGPR per copy instead of a 64-bit address pair).
 TM_DEV void dma16s(const void* base, uint32_t off, uint32_t lds) {

@@ -192,10 +192,12 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
       const int pos = min(p0 + 32 * t + r, len - 1);  // rows past the end are masked
       e[i] = row_off(pos) + 8 * (sl ^ (r & (PR - 1)));
     }
+    // the cache is read once per call: non-temporal copies (B=8, S=8192:
+    // 56.4 -> 52.3 us contiguous, 63.8 -> 61.4 us paged)
 #pragma unroll
     for (int i = 0; i < NCP; ++i) {
-      dma16(p.k + e[i], st + 1024 * i);
-      dma16(p.v + e[i], st + TB + 1024 * i);
+      dma16_nt(p.k + e[i], st + 1024 * i);
+      dma16_nt(p.v + e[i], st + TB + 1024 * i);
     }
   };
 #pragma unroll
