@@ -198,11 +198,11 @@ def test_kda_config_c5_sampled_heads(dev):
 
 
 def test_kda_many_chunks_per_workgroup_partial_last_chunk(dev):
-    """More chunks than CUs (B=2, H=2, T=8300: 520 chunks, each head ending in
-    a 44-step chunk), so the intra-chunk workgroups walk several chunks each,
-    across head and batch boundaries: every (batch, head) against the fp64
-    recurrence."""
-    B, T, H = 2, 8300, 2
+    """More chunks than intra-chunk workgroups (two per CU: 512 on 256 CUs).
+    B=2, H=2, T=16556 gives 1036 chunks, each head ending in a 44-step chunk, so
+    every workgroup walks two or three chunks, across head and batch boundaries:
+    every (batch, head) against the fp64 recurrence."""
+    B, T, H = 2, 16556, 2
     q, k, v, g, beta = kda_inputs(B, T, H, seed=4)
     o, st = _run(dev, q, k, v, g, beta)
     for b in range(B):

@@ -103,10 +103,10 @@ extern "C" int tm_kda_chunk_fwd(const void* q, const void* k, const void* v, con
   p.beta_bf16 = beta_dtype == TM_DT_BF16 ? 1 : 0;
 
   if (nc > 0) {
-    // one workgroup per CU (its LDS admits no second), each walking its share of
-    // the chunks
+    // two workgroups per CU (their LDS and registers admit no third), each
+    // walking its share of the chunks
     p.c0 = 0; p.c1 = (int)nc;
-    const long long grid = std::min<long long>(bh * nc, (long long)cu_count());
+    const long long grid = std::min<long long>(bh * nc, 2LL * cu_count());
     const int rc = launch(intra_kernel(), dim3((unsigned)grid), dim3(256), 0, stream, p);
     if (rc) return rc;
   }

@@ -106,25 +106,34 @@ struct KdaParams {
 };
 
 // ----------------------------------------------------------------------------
-// kda_intra: chunk index = bh * NC + chunk; block = 256; any grid (at most one
-// workgroup fits a CU, so the host launches one per CU).  Each workgroup takes
-// chunks blockIdx.x, blockIdx.x + gridDim.x, ... and loads the next chunk's
-// g, k, v (after the current ones are staged in LDS) and q, beta (after the
-// current q is used) into registers while the current chunk computes, so the
-// loads, and the workspace stores of the chunk before, overlap its work.  The
-// inputs are read once, non-temporally, which leaves the Infinity Cache to the
-// workspace that kda_state reads back (C5, same box: 221 -> 214 us per call).
+// kda_intra: chunk index = bh * NC + chunk; block = 256; any grid (its 78 KB of
+// LDS and <= 256 registers per lane let two workgroups share a CU, so the host
+// launches two per CU: one wave per SIMD leaves every phase latency-bound, and
+// the second workgroup's phases fill those gaps; C5, same box: kda_intra
+// 117.5 -> 83.5 us).  Each workgroup takes chunks blockIdx.x, blockIdx.x +
+// gridDim.x, ... and loads the next chunk's g, k, v into registers once the
+// current ones are staged in LDS, so those loads overlap the current chunk's
+// work; q and beta are loaded at the start of their chunk (holding them too
+// would exceed 256 registers).  The inputs are read once, non-temporally,
+// which leaves the Infinity Cache to the workspace that kda_state reads back
+// (221 -> 214 us per call).
 // MFMA 16x16x32 bf16 layouts (lane l, q = l/16): A[l%16][8q+e], B[8q+e][l%16],
 // D[4q+e][l%16].  MFMA 16x16x4 fp32: A[l%16][l/16], B[l/16][l%16], same D.
 // ----------------------------------------------------------------------------
-extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void kda_intra(KdaParams p) {
   // LDS regions; the ones marked "then" are reused after a barrier.
   __shared__ __align__(16) unsigned char lds_g[KC * GP * 4];   // G log2(e), then T fp32 + R
   __shared__ __align__(16) unsigned char lds_k[KC * 136 * 2];  // k, then T bf16
   __shared__ __align__(16) unsigned char lds_v[KC * 136 * 2];  // v, then Aqk bf16
-  __shared__ __align__(16) float Af[KC][68];                   // scan totals, then A
-  __shared__ __align__(16) uint16_t Bt[KD + VD][72];           // [beta k e^G | beta v]^T
+  // scan totals, then A's ten lower-triangular 16x16 blocks: block (tb, sb),
+  // sb <= tb, at tb (tb + 1) / 2 + sb
+  __shared__ __align__(16) float Ap[10][16][17];
   __shared__ float bet[KC];
+  auto Af = [&](int t, int s) -> float& {
+    const int tb = t >> 4;
+    return Ap[(tb * (tb + 1) >> 1) + (s >> 4)][t & 15][s & 15];
+  };
 
   float(*Gs)[GP] = (float(*)[GP])lds_g;
   float(*Tf)[68] = (float(*)[68])lds_g;                      // 17408 B
@@ -133,16 +142,29 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
   uint16_t(*Tb)[72] = (uint16_t(*)[72])lds_k;
   uint16_t(*Vs)[136] = (uint16_t(*)[136])lds_v;
   uint16_t(*AQs)[72] = (uint16_t(*)[72])lds_v;
-  float(*tot)[KD] = (float(*)[KD]) & Af[0][0];               // [8][128]
+  float(*tot)[KD] = (float(*)[KD]) & Ap[0][0][0];            // [8][128]
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, q4 = lane >> 4;
+  // Lane ids are re-derived at the top of every chunk from an opaque copy of
+  // the thread index, so that the compiler recomputes the per-lane addresses
+  // in each chunk instead of holding them in registers across the loop (two
+  // workgroups per CU leave 256 registers per lane).
+  int tid, lane, wave, l16, q4, c4, seg, r0, trow;
+  auto set_ids = [&] {
+    tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    lane = tid & 63;
+    wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    l16 = lane & 15;
+    q4 = lane >> 4;
+    c4 = tid & 31;     // channels 4 c4 .. 4 c4 + 3
+    seg = tid >> 5;    // rows 8 seg .. 8 seg + 7
+    r0 = 16 * wave;    // first row of this wave's 16-row block
+    trow = r0 + l16;   // A-operand row of this lane
+  };
+  set_ids();
   const long long rs = (long long)p.H * KD;
   const long long rsv = (long long)p.H * VD;
   const u4_t z4 = {0u, 0u, 0u, 0u};
-  const int c4 = tid & 31, seg = tid >> 5;  // channels 4c4.., rows 8seg..8seg+7
-  const int r0 = 16 * wave;     // first row of this wave's 16-row block
-  const int trow = r0 + l16;    // A-operand row of this lane
   const int nsc = p.c1 - p.c0;  // chunks per (batch, head) in this launch
   const int total = p.B * p.H * nsc;
 
@@ -198,8 +220,9 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
   if (idx >= total) return;
   Chunk cur = locate(idx);
   load_gkv(cur);
-  load_qb(cur);
   for (;;) {
+  set_ids();
+  load_qb(cur);
   const int nidx = idx + (int)gridDim.x;
   const bool has_next = nidx < total;
   const Chunk nxt = locate(has_next ? nidx : idx);
@@ -252,25 +275,57 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
     qt_op[ks] = pack8_bf16(qt);
     *(u4_t*)(ws + WS_QD + frag_off(trow, 4 * ks + q4, 4)) = pack8_bf16(qd);
   }
-  if (has_next) load_qb(nxt);  // q and beta of this chunk are used
-  // (c, 8-step group) tasks: K_end^T to the workspace, B^T to LDS
+  // B = [beta k e^G | beta v] as the B^T operands of step 5, made by the lanes
+  // that multiply them (wave w: B^T rows c = 64 w + 16 cb + l16, steps
+  // 8 q4 .. +7 and 32 + 8 q4 .. +7); waves 2 and 3 also write K_end^T (one
+  // column c per thread, its 8 step groups) to the workspace, which balances
+  // the exponentials between the two halves.
+  u4_t bop[4][2];
+  if (wave < 2) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = tid + 256 * j, c = i & 127, tg = i >> 7;
-    const float gend = Gs[KC - 1][c];
-    float ke[8], bk[8], bvv[8];
+    for (int cb = 0; cb < 4; ++cb) {
+      const int c = 64 * wave + 16 * cb + l16;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int t = 8 * tg + e;
-      const float kf = bf16_bits_to_f32(Ks[t][c]);
-      const float gtc = Gs[t][c];
-      ke[e] = kf * ex2(gend - gtc);
-      bk[e] = bet[t] * kf * ex2(gtc);
-      bvv[e] = bet[t] * bf16_bits_to_f32(Vs[t][c]);
+      for (int h = 0; h < 2; ++h) {
+        float bk[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = 32 * h + 8 * q4 + e;
+          bk[e] = bet[t] * bf16_bits_to_f32(Ks[t][c]) * ex2(Gs[t][c]);
+        }
+        bop[cb][h] = pack8_bf16(bk);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // (keeps each group's LDS reads with it)
     }
-    *(u4_t*)(ws + WS_KT + frag_off(c, tg, 2)) = pack8_bf16(ke);
-    *(u4_t*)&Bt[c][8 * tg] = pack8_bf16(bk);
-    *(u4_t*)&Bt[KD + c][8 * tg] = pack8_bf16(bvv);
+  } else {
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const int c = 64 * (wave - 2) + 16 * cb + l16;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float bvv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = 32 * h + 8 * q4 + e;
+          bvv[e] = bet[t] * bf16_bits_to_f32(Vs[t][c]);
+        }
+        bop[cb][h] = pack8_bf16(bvv);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const int c = tid - 128;
+    const float gend = Gs[KC - 1][c];
+#pragma unroll
+    for (int tg = 0; tg < 8; ++tg) {
+      float ke[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = 8 * tg + e;
+        ke[e] = bf16_bits_to_f32(Ks[t][c]) * ex2(gend - Gs[t][c]);
+      }
+      *(u4_t*)(ws + WS_KT + frag_off(c, tg, 2)) = pack8_bf16(ke);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   if (tid < KD) ((float*)(ws + WS_GC))[tid] = ex2(Gs[KC - 1][tid]);
   const int slow = __syncthreads_or(!ok);  // also orders Vs reads before AQs writes
@@ -299,7 +354,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = r0 + 4 * q4 + e, s = 16 * sb + l16;
-      Af[t][s] = s < t ? bet[t] * acc_a[e] : 0.0f;
+      Af(t, s) = s < t ? bet[t] * acc_a[e] : 0.0f;
       AQs[t][s] = f32_to_bf16_bits(s <= t ? acc_q[e] : 0.0f);
     }
   }
@@ -321,7 +376,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
         const float qv = t < nt ? bf16_bits_to_f32(p.q[base_k + t * rs + c]) : 0.0f;
         aq += qv * ksv;
       }
-      if (s < t) Af[t][s] = bet[t] * a;
+      if (s < t) Af(t, s) = bet[t] * a;
       AQs[t][s] = f32_to_bf16_bits(p.scale * aq);
     }
   }
@@ -343,7 +398,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
     for (int m = 0; m < 16; ++m) {
       float acc = (m == j) ? 1.0f : 0.0f;
 #pragma unroll
-      for (int n = 0; n < m; ++n) acc -= Af[base + m][base + n] * x[n];
+      for (int n = 0; n < m; ++n) acc -= Af(base + m, base + n) * x[n];
       x[m] = acc;
     }
 #pragma unroll
@@ -359,7 +414,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
       for (int mb = jb; mb < ib; ++mb)
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk)
-          r = mfma_f32_16x16x4(Af[16 * ib + l16][16 * mb + 4 * kk + q4],
+          r = mfma_f32_16x16x4(Af(16 * ib + l16, 16 * mb + 4 * kk + q4),
                                Tf[16 * mb + 4 * kk + q4][16 * jb + l16], r);
 #pragma unroll
       for (int e = 0; e < 4; ++e) Rs[wave][4 * q4 + e][l16] = r[e];
@@ -393,9 +448,7 @@ extern "C" __global__ __launch_bounds__(256) void kda_intra(KdaParams p) {
   // (D = [step][column]), 4 consecutive steps of one column.
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
-    const int c = 64 * wave + 16 * cb + l16;  // B^T row this lane reads
-    const u4_t b0 = *(const u4_t*)&Bt[c][8 * q4];
-    const u4_t b1 = *(const u4_t*)&Bt[c][32 + 8 * q4];
+    const u4_t b0 = bop[cb][0], b1 = bop[cb][1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * i + l16;             // T row this lane reads
