@@ -148,10 +148,12 @@ extern "C" int tm_kda_recurrent_fwd(const void* q, const void* k, const void* v,
   p.B = batch; p.T = seq_len; p.H = heads;
   p.scale = scale;
   p.beta_bf16 = beta_dtype == TM_DT_BF16 ? 1 : 0;
-  // one wave per (head, 16 value columns); 16-byte state accesses when both
-  // state buffers (or null) are 16-byte aligned
+  // one wave per (head, 16 value columns), or per (head, 32 value columns)
+  // with 16-byte state accesses when both state buffers (or null) are 16-byte
+  // aligned
   const bool v4 = ((reinterpret_cast<uintptr_t>(initial_state) |
                     reinterpret_cast<uintptr_t>(final_state)) & 15) == 0;
-  return launch(v4 ? recurrent_v4_kernel() : recurrent_kernel(),
-                dim3((unsigned)((long long)batch * heads * (kValueDim / 16))), dim3(64), 0, stream, p);
+  const long long waves = (long long)batch * heads * (kValueDim / (v4 ? 32 : 16));
+  return launch(v4 ? recurrent_v4_kernel() : recurrent_kernel(), dim3((unsigned)waves), dim3(64),
+                0, stream, p);
 }
