@@ -288,6 +288,31 @@ def test_int8_shapes(dev, M, N, K, zeros):
     check_close(out.cpu(), ref)
 
 
+# --- int8 GEMV (M = 1, K = 4096): every zero-point form, both activation dtypes,
+# the full int8 range (-128 included) and a fused bias
+@pytest.mark.parametrize("zeros", [None, "f16", "u8"])
+@pytest.mark.parametrize("act", [torch.float16, torch.bfloat16])
+def test_int8_gemv_zero_forms(dev, zeros, act):
+    M, N, K = 1, 1040, 4096
+    g = _gen(77)
+    x = torch.randn(M, K, generator=g).to(act)
+    w = torch.randint(-128, 128, (N, K), generator=g, dtype=torch.int8)
+    w[:, :64] = -128
+    w[:, 64:128] = 127
+    s = (torch.rand(N, generator=g) * 0.019 + 0.001).to(act)
+    zi = torch.randint(0, 9, (N,), generator=g)
+    z = None if zeros is None else (zi.to(torch.uint8) if zeros == "u8" else (zi - 4).to(act))
+    bias = (torch.randn(N, generator=g) * 4).to(act)
+    out = torch.empty(M, N, dtype=act, device=dev)
+    tm.int8_matmul(x.to(dev), w.to(dev), out, s.to(dev), None if z is None else z.to(dev),
+                   M, N, K)
+    ref = oracle.int8_matmul(np32(x), w.numpy(), np32(s), np32(z), M, N, K)
+    check_close(out.cpu(), ref)
+    tm.int8_linear(x.to(dev), w.to(dev), bias.to(dev), out, s.to(dev),
+                   None if z is None else z.to(dev), M, N, K)
+    check_close(out.cpu(), ref + np32(bias)[None, :].astype(np.float64))
+
+
 # --- two-tile GEMV (int4, 2 <= M <= 6, K = 4096, N % 32 == 0) --------------------
 @pytest.mark.parametrize("M,N", [(2, 32), (3, 96), (5, 64), (6, 160)])
 @pytest.mark.parametrize("zeros", ["f16", "u8", None])

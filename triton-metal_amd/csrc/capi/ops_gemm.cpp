@@ -142,6 +142,14 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
                     Z, M, N, K, bias);
     }
   }
+  // linear int8 GEMV: M = 1, K = 4096, fp16 (VALU dot products, 1 KB of one
+  // row per load instruction)
+  if (fast && qbits == 8 && M == 1 && K == 4096 && adt == TM_DT_F16) {
+    char name[64];
+    snprintf(name, sizeof name, "wq_gemv8l_f16_z%c", zc);
+    return launch(kernel(name), dim3(N / 16), dim3(512), 0, stream, X, W, Y, S, Z, M, N, K,
+                  bias);
+  }
   // int8 GEMV: M = 1, K = 4096 (8 waves x 8 loads of 16 bytes per lane)
   if (fast && qbits == 8 && M == 1 && K == 4096) {
     char name[64];

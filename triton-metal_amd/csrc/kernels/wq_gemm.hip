@@ -649,6 +649,92 @@ __device__ __forceinline__ void wq_gemv4l_body(const uint16_t* __restrict__ X,
 }
 
 // ----------------------------------------------------------------------------
+// Linear int8 GEMV, M = 1, K = 4096, fp16 activations, per-channel scales:
+// the int4 linear GEMV's layout for int8 weights.  grid.x = N / 16, block =
+// 8 waves; wave w owns k = 1024 (w % 4) .. +1024 of the 8 rows 8 (w / 4) ..
+// of the workgroup's 16, so each of its 8 weight loads reads 1 KB of one row
+// (16 bytes per lane, non-temporal: the weights are read once).  x straight
+// from L2 (2 x 16 bytes per lane).  A byte q ^ 0x80 under the exponent byte
+// 0x64 is the exact half 1152 + q; pairs of those times pairs of x with
+// v_dot2_f32_f16, and per row s * (sum x (1152 + q) - (1152 + z) sum x).
+// The 8 rows' lane sums are halved across lanes (xor 32, then 16), each lane
+// row's remaining 2 with DPP, the 4 slices through LDS.
+// ----------------------------------------------------------------------------
+template <int ZDT>
+__device__ __forceinline__ void wq_gemv8l_body(const uint16_t* __restrict__ X,
+                                               const uint8_t* __restrict__ W,
+                                               uint16_t* __restrict__ Y,
+                                               const uint16_t* __restrict__ S,
+                                               const void* __restrict__ Z, int N,
+                                               const uint16_t* bias) {
+  constexpr int K = 4096, NS = 4, RW = 8;
+  __shared__ float red[NS][16];
+  __shared__ float xred[NS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = wave % NS, r0 = RW * (wave / NS);
+  const int n0 = blockIdx.x * 16;
+
+  const u4_t x0 = ldg128(X + 1024 * h + 16 * lane), x1 = ldg128(X + 1024 * h + 16 * lane + 8);
+  const uint8_t* wb = W + (size_t)(n0 + r0) * K + 1024 * h + 16 * lane;
+  u4_t wv[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i)
+    wv[i] = __builtin_nontemporal_load((const u4_t*)(wb + (size_t)i * K));
+
+  const uint32_t xd[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+  const h2_t one = {(half_t)1.0f, (half_t)1.0f};
+  float xs = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) xs = __builtin_amdgcn_fdot2(as_h2(xd[d]), one, xs, false);
+
+  const uint32_t e = vgpr_const(0x64646464u);
+  float part[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+    float a = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = wd[j] ^ 0x80808080u;  // q + 128
+      a = __builtin_amdgcn_fdot2(as_h2(perm_b32(e, u, 0x04010400u)), as_h2(xd[2 * j]), a, false);
+      a = __builtin_amdgcn_fdot2(as_h2(perm_b32(e, u, 0x04030402u)), as_h2(xd[2 * j + 1]), a,
+                                 false);
+    }
+    part[i] = a - 1152.0f * xs;
+  }
+  // rows 0..3 stay on lanes 0..31, 4..7 on lanes 32..63; then pairs by lane bit 4
+  const bool up32 = lane & 32, up16 = lane & 16;
+  float p4[4], p2[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    p4[i] = (up32 ? part[i + 4] : part[i]) + __shfl_xor(up32 ? part[i] : part[i + 4], 32, 64);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    p2[i] = (up16 ? p4[i + 2] : p4[i]) + __shfl_xor(up16 ? p4[i] : p4[i + 2], 16, 64);
+  p2[0] = row16_sum(p2[0]);
+  p2[1] = row16_sum(p2[1]);
+  if ((lane & 15) == 0) {
+    const int r = r0 + 4 * (lane >> 5) + 2 * ((lane >> 4) & 1);
+    red[h][r] = p2[0];
+    red[h][r + 1] = p2[1];
+  }
+  if constexpr (ZDT >= 0) {
+    xs = wave_sum(xs);
+    if (wave < NS && lane == 0) xred[h] = xs;
+  }
+  __syncthreads();
+  if (tid < 16) {
+    const int n = n0 + tid;
+    float y = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) y += red[s2][tid];
+    if constexpr (ZDT >= 0)
+      y -= ld_typed<ZDT>(Z, (size_t)n) * (xred[0] + xred[1] + xred[2] + xred[3]);
+    store_out(Y, n, ld_typed<TM_DT_F16>(S, (size_t)n) * y + bias_at(bias, n, false), false);
+  }
+}
+
+// ----------------------------------------------------------------------------
 // int8 GEMV, M <= 8 (the exact shape K = NW * PF * 64): the int4 GEMV's layout
 // for int8 weights.  grid.x = N / 16, block = NW waves; wave w owns
 // k = w*PF*64 .. +PF*64 of the workgroup's 16 columns.  Lane (n, q) loads
@@ -1855,3 +1941,14 @@ TM_GEMV4XN_Z(true, bf16, 2, 4)
   TM_GEMV8(BF, ACT, u, 3)
 TM_GEMV8_Z(false, f16)
 TM_GEMV8_Z(true, bf16)
+
+// Linear int8 GEMV (M = 1, K = 4096, fp16): wq_gemv8l_f16_z<zs>
+#define TM_GEMV8L(ZS, ZDT)                                                                     \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8))) void     \
+      wq_gemv8l_f16_z##ZS(const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S,  \
+                          const void* Z, int M, int N, int K, const uint16_t* bias) {           \
+    wq_gemv8l_body<ZDT>(X, W, Y, S, Z, N, bias);                                                \
+  }
+TM_GEMV8L(n, -1)
+TM_GEMV8L(s, TM_DT_F16)
+TM_GEMV8L(u, 3)
