@@ -213,6 +213,24 @@ def test_int4_gemv_shapes(dev, M, K, zeros, act):
     check_close(out.cpu(), ref)
 
 
+# The persistent GEMV (M = 1, K = 4096, G = 128) picks rows per wave RW from
+# {4, 7, 8, 11, 12, 14, 16} so that ceil(N / 4 RW) workgroups fit the CUs; these
+# N reach every RW on a 256-CU part, a grid of one workgroup, and a last
+# workgroup shifted back over its neighbour's rows (N not a multiple of 4 RW).
+@pytest.mark.parametrize("N", [16, 48, 1040, 4112, 8208, 11008, 12304, 14336, 16384])
+@pytest.mark.parametrize("zeros,act", [("f16", torch.float16), (None, torch.float16),
+                                       ("u8", torch.bfloat16), ("f16", torch.bfloat16)])
+def test_int4_persistent_gemv(dev, N, zeros, act):
+    K, G = 4096, 128
+    x, q, packed, s, z = make_int4_problem(1, N, K, G, seed=N + 7, zeros=zeros, act=act)
+    bias = (torch.randn(N, generator=_gen(N)) * 0.5).to(act)
+    out = torch.empty(1, N, dtype=act, device=dev)
+    tm.int4_linear(x.to(dev), packed.to(dev), bias.to(dev), out, s.to(dev),
+                   None if z is None else z.to(dev), 1, N, K, G)
+    ref = oracle.int4_matmul(np32(x), packed.numpy(), np32(s), np32(z), 1, N, K, G)
+    check_close(out.cpu(), ref + np32(bias)[None, :].astype(np.float64))
+
+
 @pytest.mark.parametrize("M", [1, 8, 32, 128])
 def test_w4a16_config_c3(dev, M):
     N, K, G = 14336, 4096, 128

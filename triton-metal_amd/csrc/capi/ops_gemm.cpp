@@ -121,6 +121,22 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
                     stream, X, W, Y, S, Z, M, N, K, bias);
     }
   }
+  // persistent int4 GEMV: M = 1, K = 4096, G = 128; one workgroup per CU owns
+  // 4 RW rows, RW the smallest instantiated count that keeps the grid within
+  // the CUs (a second round of workgroups would double the time)
+  if (fast && qbits == 4 && M == 1 && G == 128 && K == 4096) {
+    static const int kRW[] = {4, 7, 8, 11, 12, 14, 16};
+    const int cus = cu_count();
+    for (int rw : kRW) {
+      const int grid = (N + 4 * rw - 1) / (4 * rw);
+      if (N >= 4 * rw && grid <= cus) {
+        char name[64];
+        snprintf(name, sizeof name, "wq_gemv4p_%s_z%c_r%d", act, zc, rw);
+        return launch(kernel(name), dim3(grid), dim3(512), 0, stream, X, W, Y, S, Z, M, N, K,
+                      bias);
+      }
+    }
+  }
   // linear int4 GEMV: M = 1, G = 128, K = 4096 or 8192 (VALU dot products,
   // 1 KB of one row per load instruction)
   if (fast && qbits == 4 && M == 1 && G == 128 && (K == 4096 || K == 8192)) {

@@ -99,6 +99,19 @@ template <bool BF16> TM_DEV f16_t mfma32(u4_t a, u4_t b, f16_t c) {
                                                   __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
 }
 
+// v_mfma_f32_4x4x4_16b: 16 independent 4x4x4 blocks; block b = l / 4 takes A's
+// row l % 4 and B's column l % 4 (4 x 16-bit values each) from lane l, and
+// lane l receives D_b[e][l % 4] in element e.
+template <bool BF16> TM_DEV f4_t mfma4x4(u2_t a, u2_t b, f4_t c) {
+  typedef short s4_t __attribute__((ext_vector_type(4)));
+  if constexpr (BF16)
+    return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s4_t, a),
+                                                  __builtin_bit_cast(s4_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4_t, a),
+                                              __builtin_bit_cast(h4_t, b), c, 0, 0, 0);
+}
+
 // ---- packed 16-bit helpers ---------------------------------------------------
 // Byte permute: result byte i = byte sel_i of the 8-byte value {hi:lo}.
 TM_DEV uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
