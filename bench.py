@@ -434,7 +434,7 @@ def cpu_baseline():
                 configs={k: v for k, v in out.items() if k != "w4a16_m1"})
 
 
-TRAFFIC_PROFILE = ROOT / "profiles" / "wq_gemv4l_w4a16_m1_hbm_traffic.md"
+TRAFFIC_PROFILE = ROOT / "profiles" / "wq_gemv4p_w4a16_m1_hbm_traffic.md"
 
 
 def profiled_traffic():
