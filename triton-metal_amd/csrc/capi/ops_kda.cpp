@@ -111,7 +111,7 @@ extern "C" int tm_kda_chunk_fwd(const void* q, const void* k, const void* v, con
     if (rc) return rc;
   }
   p.c0 = 0; p.c1 = (int)nc;
-  return launch(state_kernel(), dim3((unsigned)(bh * (kValueDim / 16))), dim3(256), 0, stream, p);
+  return launch(state_kernel(), dim3((unsigned)(bh * (kValueDim / 16))), dim3(192), 0, stream, p);
 }
 
 extern "C" int tm_kda_recurrent_fwd(const void* q, const void* k, const void* v, const float* g,

@@ -46,9 +46,14 @@ constexpr float kExp2Range = 80.0f * kLog2e;  // |G_t - G_r| <= 80 in natural-lo
 // Workspace of one (head, chunk), bytes.  The matrices kda_state reads as
 // MFMA operands are stored in fragment order: 1 KB blocks, one per (16-row
 // block, 32-column step), in which lane l = 16 q + r of the reading wave finds
-// its 16 bytes (row r, columns 8q..8q+7 of the step) at 16 l - so every load
-// there is one contiguous 1 KB.
-constexpr size_t WS_WK = 0;                    // W_k [64][128]      fragments (16 blocks)
+// its 16 bytes at 16 l - so every load there is one contiguous 1 KB.  The 16
+// bytes hold row r, columns 4q..4q+3 and 16+4q..16+4q+3 of the step: the
+// reduction index of every product kda_state runs is taken in that order, in
+// which the rows 4q+e of two vertically adjacent 16x16 MFMA results are
+// exactly the 8 reduction positions 8q..8q+7 that lane 16q + n supplies as a
+// B operand; so a result feeds the next product from the lane's own
+// registers.
+constexpr size_t WS_WK = 0;                    // -W_k [64][128]     fragments (16 blocks)
 constexpr size_t WS_WV = WS_WK + KC * KD * 2;  // W_v [64/4][128][4] (4 steps of a column together)
 constexpr size_t WS_QD = WS_WV + KC * VD * 2;  // scale q exp(G) [64][128] fragments
 constexpr size_t WS_KT = WS_QD + KC * KD * 2;  // (k exp(G_C - G))^T [128][64] fragments
@@ -57,10 +62,12 @@ constexpr size_t WS_GC = WS_AQ + KC * KC * 2;  // exp(G_C), fp32 [128]
 constexpr size_t WS_CHUNK = WS_GC + KD * 4;
 static_assert(WS_CHUNK == 74240, "workspace layout is part of the C ABI");
 
-// Byte offset of (row, 8-column group cg) of a matrix with `steps` 32-column
-// steps per row, stored in fragment order.
-TM_DEV int frag_off(int row, int cg, int steps) {
-  return (((row >> 4) * steps + (cg >> 2)) * 64 + (cg & 3) * 16 + (row & 15)) * 16;
+// Byte offset of (row, 4-column group c4 = columns 4c4..4c4+3) of a matrix
+// with `steps` 32-column steps per row, stored in fragment order: in step
+// c4/8, group c4%8 = 4h + q goes to lane 16q + row%16, bytes 8h..8h+7.
+TM_DEV int frag_off(int row, int c4, int steps) {
+  return (((row >> 4) * steps + (c4 >> 3)) * 64 + (c4 & 3) * 16 + (row & 15)) * 16 +
+         8 * ((c4 >> 2) & 1);
 }
 
 TM_DEV u4_t pack8_bf16(const float* x) {
@@ -273,7 +280,9 @@ void kda_intra(KdaParams p) {
     }
     kt_op[ks] = pack8_bf16(kt);
     qt_op[ks] = pack8_bf16(qt);
-    *(u4_t*)(ws + WS_QD + frag_off(trow, 4 * ks + q4, 4)) = pack8_bf16(qd);
+    const u4_t qp = pack8_bf16(qd);
+    *(u2_t*)(ws + WS_QD + frag_off(trow, 8 * ks + 2 * q4, 4)) = u2_t{qp.x, qp.y};
+    *(u2_t*)(ws + WS_QD + frag_off(trow, 8 * ks + 2 * q4 + 1, 4)) = u2_t{qp.z, qp.w};
   }
   // B = [beta k e^G | beta v] as the B^T operands of step 5, made by the lanes
   // that multiply them (wave w: B^T rows c = 64 w + 16 cb + l16, steps
@@ -323,7 +332,9 @@ void kda_intra(KdaParams p) {
         const int t = 8 * tg + e;
         ke[e] = bf16_bits_to_f32(Ks[t][c]) * ex2(gend - Gs[t][c]);
       }
-      *(u4_t*)(ws + WS_KT + frag_off(c, tg, 2)) = pack8_bf16(ke);
+      const u4_t kp = pack8_bf16(ke);
+      *(u2_t*)(ws + WS_KT + frag_off(c, 2 * tg, 2)) = u2_t{kp.x, kp.y};
+      *(u2_t*)(ws + WS_KT + frag_off(c, 2 * tg + 1, 2)) = u2_t{kp.z, kp.w};
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -385,10 +396,12 @@ void kda_intra(KdaParams p) {
   // ---- 4. Aqk to the workspace; T = (I + A)^-1 -----------------------------
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    // fragment slot i: block i/64 = (row block, step), lane = 16 q + r
+    // fragment slot i: block i/64 = (row block, step), lane = 16 q + r;
+    // columns 32 step + 4q .. +3 and 32 step + 16 + 4q .. +3
     const int i = tid + 256 * j, blk = i >> 6, ln = i & 63;
-    const int row = 16 * (blk >> 1) + (ln & 15), cg = 4 * (blk & 1) + (ln >> 4);
-    *(u4_t*)(ws + WS_AQ + 16 * i) = *(const u4_t*)&AQs[row][8 * cg];
+    const int row = 16 * (blk >> 1) + (ln & 15), c = 32 * (blk & 1) + 4 * (ln >> 4);
+    const u2_t lo = *(const u2_t*)&AQs[row][c], hi = *(const u2_t*)&AQs[row][c + 16];
+    *(u4_t*)(ws + WS_AQ + 16 * i) = u4_t{lo.x, lo.y, hi.x, hi.y};
   }
   if (wave == 0) {
     // diagonal blocks by forward substitution: lane = (block, column)
@@ -465,9 +478,10 @@ void kda_intra(KdaParams p) {
       w.x = pack_bf16x2(acc[0], acc[1]);
       w.y = pack_bf16x2(acc[2], acc[3]);
       if (wave < 2) {
-        // W_k[t][c0 .. c0+3], c0 = 64w + 16cb + 4q4
+        // -W_k[t][c0 .. c0+3], c0 = 64w + 16cb + 4q4 (sign bits flipped:
+        // kda_state accumulates U = W_v + (-W_k) S onto W_v)
         const int c0 = 64 * wave + 16 * cb + 4 * q4;
-        *(u2_t*)(ws + WS_WK + frag_off(t, c0 >> 3, 4) + 2 * (c0 & 7)) = w;
+        *(u2_t*)(ws + WS_WK + frag_off(t, c0 >> 2, 4)) = w ^ 0x80008000u;
       } else {
         // W_v[t0 .. t0+3][cv], t0 = 16i + 4q4, cv = 64(w-2) + 16cb + l16
         const int cv = 64 * (wave - 2) + 16 * cb + l16, tq = 4 * i + q4;
@@ -483,60 +497,69 @@ void kda_intra(KdaParams p) {
 }
 
 // ----------------------------------------------------------------------------
-// kda_state: grid = B*H*(VD/16), block = 256 (4 waves).  The workgroup owns
+// kda_state: grid = B*H*(VD/16), block = 192 (3 waves).  The workgroup owns
 // value columns v0 .. v0+15 of one head and walks the chunks in order.
-// Wave w holds state rows 32w .. 32w+31 (two 16x16 tiles, fp32) and computes
-// U / O rows 16w .. 16w+15.  S and U are shared through LDS transposed
-// ([column][row], bf16) so that B-operand reads are 16 bytes.  The chunk
-// operands are read straight from the fragment-ordered workspace (one
-// contiguous 1 KB per load instruction) one chunk ahead, alternating two
-// register sets so that no prefetched value is ever copied (a copy would
-// wait for the load).  O is computed transposed (D = [column][step]) so that
-// each lane stores 4 consecutive columns.  When B*H is a multiple of 8 the 8
-// column slices of a head run on one XCD and share its L2.
+//  * Wave 0 runs the recurrence alone, in registers: it holds the whole
+//    128 x 16 state S (eight 16x16 fp32 MFMA results) and, per chunk,
+//        U = W_v - W_k S        (16 MFMAs: 4 row blocks x 4 steps)
+//        S = diag(exp(G_C)) S + K_end^T U     (16 MFMAs: 8 x 2)
+//    Because the workspace takes the reduction index in the order of the
+//    MFMA result rows (see the layout above), the bf16 B operand of each
+//    product is just the previous result packed in the lane's own registers:
+//    no LDS round trip and no barrier sits on the recurrence.  U accumulates
+//    onto W_v with the workspace's -W_k, and its operands come from LDS: the
+//    next chunk's W_k, exp(G_C) and W_v are read into the registers the U
+//    products have freed while the state update runs.
+//  * Wave 2 copies those operands (W_k, K_end^T, the slice of W_v, exp(G_C):
+//    35 copies of 1 KB) global -> LDS three chunks ahead into a ring of four
+//    slots, waiting on its own copies only, so that no load of the
+//    recurrence's wave waits for memory.
+//  * Wave 1 computes the output O = Qd S + Aqk U of the chunk from the
+//    packed S and U operands wave 0 leaves in LDS (double-buffered), one
+//    chunk behind, on another SIMD; its own operands (Qd, Aqk) load into
+//    registers one chunk ahead.  O is computed transposed (D = [column][step])
+//    so that each lane stores 4 consecutive columns.
+// One barrier per chunk (and one before the first) orders the three: at
+// barrier c wave 0 has written chunk c's S and U operands, and wave 2's copies
+// of chunk c+2 have landed.  When B*H is a multiple of 8 the 8 column slices
+// of a head run on one XCD and share its L2.
 // ----------------------------------------------------------------------------
 namespace {
-struct ChunkOps {
-  u4_t wk[4], qd[4], aq[2], kt[4];
-  f4_t gc[2];
-  u2_t wv;  // 4 raw bf16 values of W_v: converted where used
-};
+// One ring slot: W_k fragments, K_end^T fragments, W_v rows [16 groups of 4
+// steps][16 columns][4], exp(G_C) (twice; the second copy is padding).
+constexpr int SL_WK = 0, SL_KT = 16384, SL_WV = 32768, SL_GC = 34816, SL_BYTES = 35840;
+constexpr int kStateCopies = 35;  // copy instructions per chunk and slot
 
-// The loads of one chunk in three groups, so that a step can spread them
-// over its phases (the per-CU address path, not latency, bounds the step).
-TM_DEV void load_chunk_a(const uint8_t* ws, int wave, int lane, ChunkOps& o) {
+struct OutOps {
+  u4_t qd[16];  // Qd block (row block to, step ks) at 4 to + ks
+  u4_t aq[8];   // Aqk block (row block to, step ks) at 2 to + ks
+};
+TM_DEV void load_out(const uint8_t* ws, int lane, OutOps& o) {
   const uint8_t* lw = ws + 16 * lane;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) o.wk[ks] = ldg128(lw + WS_WK + 1024 * (4 * wave + ks));
+  for (int i = 0; i < 16; ++i) o.qd[i] = ldg128(lw + WS_QD + 1024 * i);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o.aq[i] = ldg128(lw + WS_AQ + 1024 * i);
 }
-TM_DEV void load_chunk_b(const uint8_t* ws, int wave, int lane, int q4, int v0, ChunkOps& o) {
-  const uint8_t* lw = ws + 16 * lane;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) o.kt[j] = ldg128(lw + WS_KT + 1024 * (4 * wave + j));
-  const float* gc = (const float*)(ws + WS_GC);
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) o.gc[tt] = *(const f4_t*)(gc + 32 * wave + 16 * tt + 4 * q4);
-  o.wv = ldg64(ws + WS_WV + 8 * ((4 * wave + q4) * VD + v0 + (lane & 15)));
-}
-TM_DEV void load_chunk_c(const uint8_t* ws, int wave, int lane, ChunkOps& o) {
-  const uint8_t* lw = ws + 16 * lane;
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) o.qd[ks] = ldg128(lw + WS_QD + 1024 * (4 * wave + ks));
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) o.aq[ks] = ldg128(lw + WS_AQ + 1024 * (2 * wave + ks));
-}
-TM_DEV void load_chunk(const uint8_t* ws, int wave, int lane, int q4, int v0, ChunkOps& o) {
-  load_chunk_a(ws, wave, lane, o);
-  load_chunk_b(ws, wave, lane, q4, v0, o);
-  load_chunk_c(ws, wave, lane, o);
+// The bf16 B operand of rows 32j .. 32j+31 of a stack of 16x16 results:
+// blocks 2j and 2j+1, rows 4q+e of each.
+TM_DEV u4_t pack_pair(f4_t a, f4_t b) {
+  u4_t r;
+  r.x = pack_bf16x2(a[0], a[1]);
+  r.y = pack_bf16x2(a[2], a[3]);
+  r.z = pack_bf16x2(b[0], b[1]);
+  r.w = pack_bf16x2(b[2], b[3]);
+  return r;
 }
 }  // namespace
 
-extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
-  __shared__ __align__(16) uint16_t Sbt[2][16][KD + 8];  // S^T bf16 (double-buffered)
-  __shared__ __align__(16) uint16_t Ubt[2][16][KC + 8];  // U^T bf16
+extern "C" __global__ __launch_bounds__(192) void kda_state(KdaParams p) {
+  __shared__ __align__(16) unsigned char ring[4][SL_BYTES];  // wave 0's operands
+  __shared__ __align__(16) u4_t Sx[2][4][64];  // packed S operands, by chunk parity
+  __shared__ __align__(16) u4_t Ux[2][2][64];  // packed U operands
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int q4 = lane >> 4, l16 = lane & 15;
   constexpr int nvs = VD / 16;
   const int BH = p.B * p.H;
@@ -552,103 +575,155 @@ extern "C" __global__ __launch_bounds__(256) void kda_state(KdaParams p) {
   const int b = bh / p.H, h = bh - b * p.H;
   const int v0 = vs * 16;
   const long long rsv = (long long)p.H * VD;
-
-  // state tiles: rows 32w + 16tt + 4q4 + e, column v0 + l16
-  f4_t S[2];
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = 32 * wave + 16 * tt + 4 * q4 + e;
-      S[tt][e] = p.s0 ? p.s0[((long long)bh * KD + row) * VD + v0 + l16] : 0.0f;
-    }
-
   const uint8_t* wsh = p.ws + (size_t)bh * p.NC * WS_CHUNK;
-  // One chunk step: consume `cur` (chunk c) and start loading chunk c+1
-  // into `nxt`.
-  auto step = [&](const int c, auto bufc, const ChunkOps& cur, ChunkOps& nxt) {
-    constexpr int BUF = decltype(bufc)::value;
-    const uint8_t* wsn = wsh + (size_t)min(c + 1, p.c1 - 1) * WS_CHUNK;
-    load_chunk_a(wsn, wave, lane, nxt);
-    asm volatile("" ::: "memory");  // issue points of the next chunk's loads stay spread
+  auto chunk_ws = [&](int c) { return wsh + (size_t)min(c, p.c1 - 1) * WS_CHUNK; };
 
-    // (a) S -> LDS as S^T bf16
+  if (wave == 0) {
+    // ---- the recurrence --------------------------------------------------
+    f4_t S[8];  // rows 16 tt + 4 q4 + e, column v0 + l16
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int row = 32 * wave + 16 * tt + 4 * q4;
-      u2_t w;
-      w.x = pack_bf16x2(S[tt][0], S[tt][1]);
-      w.y = pack_bf16x2(S[tt][2], S[tt][3]);
-      *(u2_t*)(&Sbt[BUF][l16][row]) = w;
-    }
-    lds_barrier();
-    load_chunk_b(wsn, wave, lane, q4, v0, nxt);
-    asm volatile("" ::: "memory");
-
-    // (b) U rows 16w.. : U = W_v - W_k S; O^T = S^T Qd^T (first part)
-    u4_t sb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) sb[ks] = *(const u4_t*)(&Sbt[BUF][l16][32 * ks + 8 * q4]);
-    f4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma16<true>(cur.wk[ks], sb[ks], acc);
-    const float wv[4] = {__uint_as_float(cur.wv.x << 16), __uint_as_float(cur.wv.x & 0xffff0000u),
-                         __uint_as_float(cur.wv.y << 16), __uint_as_float(cur.wv.y & 0xffff0000u)};
-    {
-      u2_t w;
-      w.x = pack_bf16x2(wv[0] - acc[0], wv[1] - acc[1]);
-      w.y = pack_bf16x2(wv[2] - acc[2], wv[3] - acc[3]);
-      *(u2_t*)(&Ubt[BUF][l16][16 * wave + 4 * q4]) = w;
-    }
-    f4_t o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) o = mfma16<true>(sb[ks], cur.qd[ks], o);
-    lds_barrier();
-    load_chunk_c(wsn, wave, lane, nxt);
-    asm volatile("" ::: "memory");
-
-    // (c) O^T += U^T Aqk^T; lane holds O[t][v0 + 4q4 .. +3], t = 64c + 16w + l16
-    u4_t ub[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) ub[ks] = *(const u4_t*)(&Ubt[BUF][l16][32 * ks + 8 * q4]);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) o = mfma16<true>(ub[ks], cur.aq[ks], o);
-    {
-      const int t = c * KC + 16 * wave + l16;
-      u2_t w;
-      w.x = pack_bf16x2(o[0], o[1]);
-      w.y = pack_bf16x2(o[2], o[3]);
-      if (t < p.T)
-        *(u2_t*)(p.o + ((long long)b * p.T + t) * rsv + (long long)h * VD + v0 + 4 * q4) = w;
-    }
-
-    // (d) S = diag(exp(G_C)) S + K_end^T U
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      S[tt] *= cur.gc[tt];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) S[tt] = mfma16<true>(cur.kt[2 * tt + ks], ub[ks], S[tt]);
-    }
-  };
-  ChunkOps ops0, ops1;
-  if (p.c1 > p.c0) load_chunk(wsh + (size_t)p.c0 * WS_CHUNK, wave, lane, q4, v0, ops0);
-  // pairs of steps with no branch between them, so that each operand set
-  // keeps its registers around the loop; an odd last chunk after the loop
-  int c = p.c0;
-  for (; c + 1 < p.c1; c += 2) {
-    step(c, std::integral_constant<int, 0>(), ops0, ops1);
-    step(c + 1, std::integral_constant<int, 1>(), ops1, ops0);
-  }
-  if (c < p.c1) step(c, std::integral_constant<int, 0>(), ops0, ops1);
-
-  if (p.st) {
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int tt = 0; tt < 8; ++tt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int row = 32 * wave + 16 * tt + 4 * q4 + e;
-        p.st[((long long)bh * KD + row) * VD + v0 + l16] = S[tt][e];
+        const int row = 16 * tt + 4 * q4 + e;
+        S[tt][e] = p.s0 ? p.s0[((long long)bh * KD + row) * VD + v0 + l16] : 0.0f;
       }
+    lds_barrier();  // the first two chunks' operands have landed
+    // this chunk's -W_k, exp(G_C), W_v (read one chunk ahead)
+    u4_t wk[16];
+    f4_t gc[8];
+    u2_t wv[4];
+    auto read_ahead = [&](const unsigned char* sl) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) wk[i] = *(const u4_t*)(sl + SL_WK + 1024 * i + 16 * lane);
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt) gc[tt] = *(const f4_t*)(sl + SL_GC + 4 * (16 * tt + 4 * q4));
+#pragma unroll
+      for (int tu = 0; tu < 4; ++tu)
+        wv[tu] = *(const u2_t*)(sl + SL_WV + 128 * (4 * tu + q4) + 8 * l16);
+    };
+    if (p.c1 > p.c0) read_ahead(ring[p.c0 & 3]);
+    for (int c = p.c0; c < p.c1; ++c) {
+      const int par = c & 1;
+      const unsigned char* sl = ring[c & 3];
+      u4_t sb[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) sb[ks] = pack_pair(S[2 * ks], S[2 * ks + 1]);
+      f4_t u[4];
+#pragma unroll
+      for (int tu = 0; tu < 4; ++tu) {
+        const u2_t w = wv[tu];
+        u[tu] = f4_t{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u),
+                     __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xffff0000u)};
+      }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int tu = 0; tu < 4; ++tu) u[tu] = mfma16<true>(wk[4 * tu + ks], sb[ks], u[tu]);
+      u4_t kt[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) kt[i] = *(const u4_t*)(sl + SL_KT + 1024 * i + 16 * lane);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) Sx[par][ks][lane] = sb[ks];
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt) S[tt] *= gc[tt];
+      u4_t ub[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) ub[ks] = pack_pair(u[2 * ks], u[2 * ks + 1]);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) S[tt] = mfma16<true>(kt[2 * tt + ks], ub[ks], S[tt]);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) Ux[par][ks][lane] = ub[ks];
+      if (c + 1 < p.c1) read_ahead(ring[(c + 1) & 3]);
+      lds_barrier();  // chunk c's S and U are in LDS for wave 1
+    }
+    if (p.st) {
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = 16 * tt + 4 * q4 + e;
+          p.st[((long long)bh * KD + row) * VD + v0 + l16] = S[tt][e];
+        }
+    }
+  } else if (wave == 2) {
+    // ---- wave 0's operands, global -> LDS, two chunks ahead ---------------
+    // lane offsets: 1 KB fragment blocks; W_v rows of the slice (16 pieces
+    // of 128 B, lane l of copy j takes piece 8j + l/8); exp(G_C) (lanes
+    // 32..63 repeat lanes 0..31 into the padding)
+    const uint32_t o16 = 16 * lane;
+    const uint32_t owv0 = WS_WV + 8 * ((lane >> 3) * VD + v0) + 16 * (lane & 7);
+    const uint32_t owv1 = owv0 + 8 * 8 * VD;
+    const uint32_t ogc = WS_GC + 16 * (lane & 31);
+    auto copy = [&](int c) {
+      const uint8_t* src = chunk_ws(c);
+      const uint32_t dst = lds_off(ring[c & 3]);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dma16s(src, WS_WK + 1024 * i + o16, dst + SL_WK + 1024 * i);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dma16s(src, WS_KT + 1024 * i + o16, dst + SL_KT + 1024 * i);
+      dma16s(src, owv0, dst + SL_WV);
+      dma16s(src, owv1, dst + SL_WV + 1024);
+      dma16s(src, ogc, dst + SL_GC);
+    };
+    if (p.c1 > p.c0) copy(p.c0);
+    if (p.c0 + 1 < p.c1) copy(p.c0 + 1);
+    if (p.c0 + 2 < p.c1) {
+      copy(p.c0 + 2);
+      wait_vm<kStateCopies>();  // chunks c0 and c0+1 have landed
+    } else {
+      wait_vm<0>();
+    }
+    asm volatile("s_barrier" ::: "memory");
+    for (int c = p.c0; c < p.c1; ++c) {
+      // slot (c+3) % 4 was last read by wave 0 in chunk c-1, before barrier
+      // c-1; wave 0 reads chunk c+2's slot after barrier c
+      if (c + 3 < p.c1) {
+        copy(c + 3);
+        wait_vm<kStateCopies>();  // chunk c+2's copies have landed
+      } else {
+        wait_vm<0>();
+      }
+      asm volatile("s_barrier" ::: "memory");
+    }
+  } else {
+    // ---- the output, one chunk behind ------------------------------------
+    lds_barrier();
+    auto out = [&](const int c, const OutOps& cur, OutOps& nxt) {
+      const int par = c & 1;
+      load_out(chunk_ws(c + 1), lane, nxt);
+      lds_barrier();  // wave 0 has left chunk c's operands
+      u4_t sb[4], ub[2];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) sb[ks] = Sx[par][ks][lane];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) ub[ks] = Ux[par][ks][lane];
+#pragma unroll
+      for (int to = 0; to < 4; ++to) {
+        f4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) o = mfma16<true>(sb[ks], cur.qd[4 * to + ks], o);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) o = mfma16<true>(ub[ks], cur.aq[2 * to + ks], o);
+        // lane holds O[t][v0 + 4 q4 .. +3], t = 64 c + 16 to + l16
+        const int t = c * KC + 16 * to + l16;
+        u2_t w;
+        w.x = pack_bf16x2(o[0], o[1]);
+        w.y = pack_bf16x2(o[2], o[3]);
+        if (t < p.T)
+          *(u2_t*)(p.o + ((long long)b * p.T + t) * rsv + (long long)h * VD + v0 + 4 * q4) = w;
+      }
+    };
+    OutOps ops0, ops1;
+    if (p.c1 > p.c0) load_out(chunk_ws(p.c0), lane, ops0);
+    int c = p.c0;
+    for (; c + 1 < p.c1; c += 2) {
+      out(c, ops0, ops1);
+      out(c + 1, ops1, ops0);
+    }
+    if (c < p.c1) out(c, ops0, ops1);
   }
 }
 

@@ -40,6 +40,15 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-file additions.  kda.hip: MFMA results in VGPRs rather than AGPRs (the
+# compiler's choice for kda_state, whose state update scales and packs every
+# result on the VALU, would move each one out of AGPRs and back every chunk;
+# the file's other kernels compile identically either way).
+EXTRA_FLAGS = {
+    "kda": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _run(cmd, verbose):
     if verbose:
         print("+", " ".join(str(c) for c in cmd), flush=True)
@@ -66,7 +75,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
     def compile_one(src: Path) -> Path:
         out = BUILD_DIR / (src.stem + ".hsaco")
-        _run([hipcc, *HIPCC_FLAGS, f"-I{CSRC / 'kernels'}", src, "-o", out], verbose)
+        _run([hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.stem, []), f"-I{CSRC / 'kernels'}", src,
+              "-o", out], verbose)
         return out
 
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
