@@ -107,6 +107,57 @@ def test_linear_shapes(dev, M, N, K, bias):
     np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
 
 
+# --- 32 x 32 tiles with K split over 4 waves (M, N % 32 == 0, K = 256 or 512) --------
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (1024, 512, 256), (96, 160, 512),
+                                   (32, 32, 256)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("out32", [False, True])
+def test_matmul_small_tiles(dev, M, N, K, dt, out32):
+    A, B = _rand((M, K), 21, dt), _rand((K, N), 22, dt)
+    C = torch.empty(M, N, dtype=torch.float32 if out32 else dt, device=dev)
+    tm.matmul(A.to(dev), B.to(dev), C, M, N, K)
+    ref = oracle.matmul(A.float().numpy(), B.float().numpy())
+    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=1e-3 if out32 else ATOL,
+                               rtol=1e-4 if out32 else RTOL)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 512), (64, 96, 256)])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_linear_small_tiles(dev, M, N, K, bias, dt):
+    x, W = _rand((M, K), 23, dt), _rand((N, K), 24, dt)
+    b = _rand((N,), 25, dt) if bias else None
+    C = torch.empty(M, N, dtype=dt, device=dev)
+    tm.fused_linear(x.to(dev), W.to(dev), C, None if b is None else b.to(dev), M, N, K)
+    ref = oracle.linear(x.float().numpy(), W.float().numpy(),
+                        None if b is None else b.float().numpy())
+    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("ldc_pad", [32, 2])
+def test_matmul_small_tiles_padded_leading_dims(dev, ldc_pad):
+    """The C ABI with row strides above the logical widths on the 32 x 32 K-split
+    kernel (ldc_pad 32), and with an ldc that is not a multiple of 4 (ldc_pad 2),
+    which the host sends to another kernel."""
+    import ctypes
+    from triton_metal_amd import _lib
+    M, N, K = 512, 256, 512
+    lda, ldb, ldc = K + 64, N + 128, N + ldc_pad
+    Ap, Bp = _rand((M, lda), 26, torch.float16), _rand((K, ldb), 27, torch.float16)
+    Cp = torch.zeros(M, ldc, dtype=torch.float16, device=dev)
+    Ad, Bd = Ap.to(dev), Bp.to(dev)
+    L = _lib.lib()
+    rc = L.tm_matmul(ctypes.c_void_p(Ad.data_ptr()), ctypes.c_void_p(Bd.data_ptr()),
+                     ctypes.c_void_p(Cp.data_ptr()), M, N, K, lda, ldb, ldc,
+                     _lib.TM_DT_F16, _lib.TM_DT_F16, None)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    ref = oracle.matmul(Ap[:, :K].float().numpy(), Bp[:, :N].float().numpy())
+    got = Cp.float().cpu().numpy()
+    np.testing.assert_allclose(got[:, :N], ref, atol=ATOL, rtol=RTOL)
+    assert (got[:, N:] == 0).all()  # the padding columns of C are untouched
+
+
 # --- 256 x 256 tiles (M, N multiples of 256 with at least 192 tiles, K % 64 == 0) ----
 def _sample(n, k, seed):
     return np.sort(np.random.default_rng(seed).choice(n, k, replace=False))

@@ -230,8 +230,19 @@ int dense(const void* A, const void* B, void* C, const void* bias, int M, int N,
       return launch(kernel(name), dim3((unsigned)t256), dim3(512), 0, stream, A, B, C, bias, M,
                     N, K, lda, ldb, ldc);
     }
-    const char* tile;
     long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+    // small aligned problems with K = 256 or 512 (C1): 32 x 32 tiles, K split
+    // over the workgroup's 4 waves, 16-byte copies and 8 / 16-byte stores
+    if (t128 < 256 && M % 32 == 0 && N % 32 == 0 && (K == 256 || K == 512) && aligned16(C) &&
+        ldc % 4 == 0) {
+      char name[96];
+      snprintf(name, sizeof name, "gemm_s32k%d_%s_%s_%s%s", K / 4, bt ? "nt" : "nn",
+               idt == TM_DT_BF16 ? "bf16" : "f16", odt == TM_DT_F32 ? "f32" : "same",
+               (bt && bias) ? "_bias" : "");
+      return launch(kernel(name), dim3((unsigned)((M / 32) * (N / 32))), dim3(256), 0, stream, A,
+                    B, C, bias, M, N, K, lda, ldb, ldc);
+    }
+    const char* tile;
     long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
     int bm;
     if (t128 >= 256) { tile = "t128"; bm = 128; }

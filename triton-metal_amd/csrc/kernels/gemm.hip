@@ -184,6 +184,114 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ A,
     }
 }
 
+// ----------------------------------------------------------------------------
+// Small problems, K = 4 KW with KW = 64 or 128, M % 32 == 0, N % 32 == 0 (C1,
+// 512^3: one workgroup per CU).  A workgroup owns a 32 x 32 output tile and
+// its 4 waves split K: wave w copies its own A slice [32][KW] and B slice
+// (nn: [KW][32], nt: [32][KW]) global -> LDS (2 KW / 16 copies of 1 KB) and
+// waits on those copies only, so nothing but the final sum needs a barrier;
+// then KW / 16 v_mfma_f32_32x32x16 in two accumulator chains, the row-major B
+// read with ds_read_b64_tr_b16 (lane l: column l % 32, k = 8 (l / 32) + e).
+// The four K partials meet in LDS (each wave parks its own in its own region)
+// and every thread sums 4 consecutive columns of one row and stores them in
+// one access.  A rows (and nt B rows) keep piece p at slot p ^ (r & 7).
+// Same box against the 32 x 32 whole-K tile it replaces there: 512^3
+// 4.24 -> 2.75 us, 1024 x 1024 x 512 10.8 -> 5.6 us.
+// ----------------------------------------------------------------------------
+namespace {
+typedef short gs_s4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) gs_s4_t gs_lds_s4_t;
+TM_DEV u2_t gs_tr16(const uint16_t* p) {
+  gs_s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((gs_lds_s4_t*)(p));
+  return __builtin_bit_cast(u2_t, v);
+}
+}  // namespace
+
+template <int KW, bool BT, bool BF16, int ODT, bool BIAS>
+__device__ __forceinline__ void gemm_s32_body(const uint16_t* __restrict__ A,
+                                              const uint16_t* __restrict__ B,
+                                              void* __restrict__ C,
+                                              const uint16_t* __restrict__ bias, int N, int lda,
+                                              int ldb, int ldc) {
+  static_assert(KW == 64 || KW == 128, "k per wave");
+  constexpr int NCP = KW / 16;           // 1 KB copies per operand and wave
+  constexpr int WREG = 2 * 32 * KW * 2;  // LDS bytes per wave: A slice, B slice
+  __shared__ __align__(16) uint8_t lds[4 * WREG];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_n = N >> 5;
+  const int m0 = (blockIdx.x / tiles_n) * 32, n0 = (blockIdx.x % tiles_n) * 32;
+  const int k0 = wave * KW;
+  uint8_t* wa = lds + wave * WREG;
+  uint8_t* wb = wa + 32 * KW * 2;
+  // copy i, lane l fills bytes 1024 i + 16 l of the slice: row r, slot sl
+#pragma unroll
+  for (int i = 0; i < NCP; ++i) {
+    const int o = 1024 * i + 16 * lane, r = o / (2 * KW), sl = (o % (2 * KW)) / 16;
+    dma16(A + (size_t)(m0 + r) * lda + k0 + 8 * (sl ^ (r & 7)), lds_off(wa) + 1024 * i);
+  }
+#pragma unroll
+  for (int i = 0; i < NCP; ++i) {
+    if constexpr (BT) {
+      const int o = 1024 * i + 16 * lane, r = o / (2 * KW), sl = (o % (2 * KW)) / 16;
+      dma16(B + (size_t)(n0 + r) * ldb + k0 + 8 * (sl ^ (r & 7)), lds_off(wb) + 1024 * i);
+    } else {
+      const int kr = 16 * i + (lane >> 2), pc = lane & 3;  // [KW][32]: 64-byte rows
+      dma16(B + (size_t)(k0 + kr) * ldb + n0 + 8 * pc, lds_off(wb) + 1024 * i);
+    }
+  }
+  wait_vm<0>();
+  const int l32 = lane & 31, h32 = lane >> 5;
+  const int tg = lane >> 4, tj = lane & 15;
+  const int tr_k = 8 * (tg >> 1) + (tj >> 2), tr_c = 16 * (tg & 1) + 4 * (tj & 3);
+  f16_t acc[2] = {f16_t{}, f16_t{}};
+#pragma unroll
+  for (int s = 0; s < KW / 16; ++s) {
+    const int p = 2 * s + h32;
+    const u4_t a = *(const u4_t*)(wa + l32 * (2 * KW) + 16 * (p ^ (l32 & 7)));
+    u4_t b;
+    if constexpr (BT) {
+      b = *(const u4_t*)(wb + l32 * (2 * KW) + 16 * (p ^ (l32 & 7)));
+    } else {
+      const int ka = 16 * s + tr_k;
+      const u2_t lo = gs_tr16((const uint16_t*)(wb + ka * 64) + tr_c);
+      const u2_t hi = gs_tr16((const uint16_t*)(wb + (ka + 4) * 64) + tr_c);
+      b = u4_t{lo.x, lo.y, hi.x, hi.y};
+    }
+    acc[s & 1] = mfma32<BF16>(a, b, acc[s & 1]);
+  }
+  // this wave's partial [e][lane] into its own region (its operand reads are
+  // done: the MFMAs consumed them); then the sum over the four waves
+  float* red = (float*)wa;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) red[e * 64 + lane] = acc[0][e] + acc[1][e];
+  __syncthreads();
+  const int row = tid >> 3, c4 = 4 * (tid & 7);
+  // D layout: row 8 (e / 4) + 4 h + e % 4, column l32 (lane l32 + 32 h)
+  const int e = 4 * (row >> 3) + (row & 3), hh = (row >> 2) & 1;
+  f4_t v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) v += *(const f4_t*)(lds + w * WREG + 4 * (e * 64 + 32 * hh + c4));
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      v[c] += BF16 ? bf16_bits_to_f32(bias[n0 + c4 + c]) : f16_bits_to_f32(bias[n0 + c4 + c]);
+  }
+  const size_t ci = (size_t)(m0 + row) * ldc + n0 + c4;
+  if constexpr (ODT == TM_DT_F32) {
+    *(f4_t*)((float*)C + ci) = v;
+  } else {
+    u2_t w;
+    if constexpr (ODT == TM_DT_BF16) {
+      w.x = pack_bf16x2(v[0], v[1]);
+      w.y = pack_bf16x2(v[2], v[3]);
+    } else {
+      w.x = pack_f16x2(v[0], v[1]);
+      w.y = pack_f16x2(v[2], v[3]);
+    }
+    *(u2_t*)((uint16_t*)C + ci) = w;
+  }
+}
+
 // General fallback: one thread per output, fp32 accumulation (any shape,
 // any alignment); the reference template's arithmetic.
 extern "C" __global__ __launch_bounds__(256) void gemm_general(
@@ -240,3 +348,23 @@ TM_GEMM_OUTS(true, nt, false, f16, false, )
 TM_GEMM_OUTS(true, nt, true, bf16, false, )
 TM_GEMM_OUTS(true, nt, false, f16, true, _bias)
 TM_GEMM_OUTS(true, nt, true, bf16, true, _bias)
+
+// gemm_s32k<KW>_<bt>_<in>_<out>[_bias]
+#define TM_GEMM_S32(KW, BT, BTN, BF, IN, ODT, OUT, BIAS, BN_)                                     \
+  extern "C" __global__ __launch_bounds__(256) void gemm_s32k##KW##_##BTN##_##IN##_##OUT##BN_(   \
+      const uint16_t* A, const uint16_t* B, void* C, const uint16_t* bias, int M, int N, int K,   \
+      int lda, int ldb, int ldc) {                                                                \
+    gemm_s32_body<KW, BT, BF, ODT, BIAS>(A, B, C, bias, N, lda, ldb, ldc);                        \
+  }
+#define TM_GEMM_S32_OUTS(KW, BT, BTN, BF, IN, BIAS, BN_)                             \
+  TM_GEMM_S32(KW, BT, BTN, BF, IN, (BF ? TM_DT_BF16 : TM_DT_F16), same, BIAS, BN_) \
+  TM_GEMM_S32(KW, BT, BTN, BF, IN, TM_DT_F32, f32, BIAS, BN_)
+#define TM_GEMM_S32_ALL(KW)                                   \
+  TM_GEMM_S32_OUTS(KW, false, nn, false, f16, false, )        \
+  TM_GEMM_S32_OUTS(KW, false, nn, true, bf16, false, )        \
+  TM_GEMM_S32_OUTS(KW, true, nt, false, f16, false, )         \
+  TM_GEMM_S32_OUTS(KW, true, nt, true, bf16, false, )         \
+  TM_GEMM_S32_OUTS(KW, true, nt, false, f16, true, _bias)     \
+  TM_GEMM_S32_OUTS(KW, true, nt, true, bf16, true, _bias)
+TM_GEMM_S32_ALL(64)
+TM_GEMM_S32_ALL(128)
