@@ -31,15 +31,44 @@
 
 namespace {
 
-// One transposed-butterfly stage over lane bit O: R rows per lane -> R / 2 (a
-// lane keeps the upper half of the rows when its bit O is set).
-template <int O, int R> TM_DEV void fold_stage(float (&v)[16], int lane) {
+// The lane folds run on the VALU's own cross-lane paths (DPP and the permlane
+// swaps), with no LDS round trip between stages (with __shfl_xor, six
+// dependent ds_bpermute stages: 7.31 -> 7.11 us per step).
+// One transposed-butterfly stage over lane bit O = 1 or 2 (quad DPP): R rows
+// per lane -> R / 2, a lane keeping the upper half when its bit O is set.
+template <int O, int R> TM_DEV void fold_dpp(float (&v)[16], int lane) {
   const bool up = lane & O;
   static_for<0, R / 2>([&](auto IC) {
     constexpr int i = decltype(IC)::value;
     const float keep = up ? v[i + R / 2] : v[i], send = up ? v[i] : v[i + R / 2];
-    v[i] = keep + __shfl_xor(send, O, 64);
+    const int got =
+        __builtin_amdgcn_mov_dpp(__float_as_int(send), O == 1 ? 0xB1 : 0x4E, 0xF, 0xF, false);
+    v[i] = keep + __int_as_float(got);
   });
+}
+// Sum over lane bits 0 and 1 (a quad), every lane receiving it.
+TM_DEV float sum_bits01(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+  return v;
+}
+// A transposed step over lane bit 4 (O = 16) or 5 (O = 32) for two rows: the
+// lanes with the bit clear return row lo summed with their partner lane's,
+// the others row hi (one permlane swap: it trades lo's upper lanes for hi's
+// lower ones).
+template <int O> TM_DEV float fold_swap(float lo, float hi) {
+  const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(lo),
+                                                            __float_as_uint(hi), false, false)
+                         : __builtin_amdgcn_permlane32_swap(__float_as_uint(lo),
+                                                            __float_as_uint(hi), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Sum over lane bits 2 and 3 (lanes i, i + 4, i + 8, i + 12 of a 16-lane row:
+// two row rotations).
+TM_DEV float sum_bits23(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+  return v;
 }
 
 }  // namespace
@@ -130,17 +159,11 @@ __device__ __forceinline__ void wq_gemv4p_body(const uint16_t* __restrict__ X,
     if (i < RW) v[i] = e == 0 ? acc[i][0] : e == 1 ? acc[i][1] : e == 2 ? acc[i][2] : acc[i][3];
     else v[i] = 0.0f;
   }
-  fold_stage<1, 16>(v, lane);
-  fold_stage<2, 8>(v, lane);
+  fold_dpp<1, 16>(v, lane);
+  fold_dpp<2, 8>(v, lane);
   // the group's sum x and sum x OFF
-  xsum += __shfl_xor(xsum, 1, 64);
-  xsum += __shfl_xor(xsum, 2, 64);
-  if constexpr (BF16) {
-    xoff = w4_offset<true>() * xsum;
-  } else {
-    xoff += __shfl_xor(xoff, 1, 64);
-    xoff += __shfl_xor(xoff, 2, 64);
-  }
+  xsum = sum_bits01(xsum);
+  xoff = BF16 ? w4_offset<true>() * xsum : sum_bits01(xoff);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     float zp = 0.0f;
@@ -148,14 +171,12 @@ __device__ __forceinline__ void wq_gemv4p_body(const uint16_t* __restrict__ X,
     const float p = raw_to_f32<SDT>(sraw[m]) * (v[m] - xoff - zp * xsum);
     v[m] = rq + m < RW ? p : 0.0f;
   }
-  fold_stage<4, 4>(v, lane);
-  fold_stage<8, 2>(v, lane);
-  float rs = v[0];
-  rs += __shfl_xor(rs, 16, 64);
-  rs += __shfl_xor(rs, 32, 64);
-  // lanes with bits 0..3 = (b0 b1 b2 b3) hold row 8 b0 + 4 b1 + 2 b2 + b3
-  const int r = 8 * (lane & 1) + 4 * ((lane >> 1) & 1) + 2 * ((lane >> 2) & 1) + ((lane >> 3) & 1);
-  if (lane < 16 && r < RW) red[h][RW * ws + r] = rs;
+  // rows rq + m -> over lane bits 4 and 5 -> row rq + 2 b4 + b5; then the sum
+  // over bits 2 and 3 (the remaining groups)
+  const float u0 = fold_swap<16>(v[0], v[2]), u1 = fold_swap<16>(v[1], v[3]);
+  const float rs = sum_bits23(fold_swap<32>(u0, u1));
+  const int r = rq + 2 * ((lane >> 4) & 1) + ((lane >> 5) & 1);
+  if ((lane & 12) == 0 && r < RW) red[h][RW * ws + r] = rs;
   lds_barrier();
   if (tid < 4 * RW) {
     const int n = n0 + tid;
