@@ -209,9 +209,33 @@ TM_DEV float row16_sum(float v) {
   return v;
 }
 
-// Wave-wide reductions (64 lanes).
+// A transposed butterfly step over lane bit 4 (O = 16) or 5 (O = 32) for two
+// values: the lanes with the bit clear return lo summed with their partner
+// lane's lo, the others hi summed with their partner's hi.  One permlane swap
+// (it trades lo's upper lanes for hi's lower ones), no LDS round trip.  With
+// lo == hi every lane gets the sum over the bit.
+template <int O> TM_DEV float fold_swap(float lo, float hi) {
+  static_assert(O == 16 || O == 32, "lane bit 4 or 5");
+  const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(lo),
+                                                            __float_as_uint(hi), false, false)
+                         : __builtin_amdgcn_permlane32_swap(__float_as_uint(lo),
+                                                            __float_as_uint(hi), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The same swap for a maximum over lane bit 4 or 5 (every lane receives it).
+template <int O> TM_DEV float max_swap(float v) {
+  static_assert(O == 16 || O == 32, "lane bit 4 or 5");
+  const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                            __float_as_uint(v), false, false)
+                         : __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                            __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Wave-wide sum (64 lanes, every lane receives it): DPP within rows of 16,
+// then the two permlane swaps.
 TM_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v = row16_sum(v);
+  v = fold_swap<16>(v, v);
+  return fold_swap<32>(v, v);
 }

@@ -242,8 +242,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
     float mx = sc[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) mx = fmaxf(mx, sc[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = max_swap<32>(max_swap<16>(mx));
     const float m_new = fmaxf(m_run, mx);
     const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;
@@ -280,8 +279,8 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
     }
   }
   wait_vm<0>();
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = fold_swap<16>(l_run, l_run);
+  l_run = fold_swap<32>(l_run, l_run);
   if (!hvalid) return;
   // lane holds O^T[16 dt + 4 q4 + e][head l16]
   if (p.nsplit == 1) {

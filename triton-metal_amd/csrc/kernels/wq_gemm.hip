@@ -499,8 +499,9 @@ __device__ __forceinline__ void wq_gemv4l_body(const uint16_t* __restrict__ X,
 // from L2 (2 x 16 bytes per lane).  A byte q ^ 0x80 under the exponent byte
 // 0x64 is the exact half 1152 + q; pairs of those times pairs of x with
 // v_dot2_f32_f16, and per row s * (sum x (1152 + q) - (1152 + z) sum x).
-// The 8 rows' lane sums are halved across lanes (xor 32, then 16), each lane
-// row's remaining 2 with DPP, the 4 slices through LDS.
+// The 8 rows' lane sums are halved across lanes (permlane swaps over lane
+// bits 5, then 4), each lane row's remaining 2 with DPP, the 4 slices through
+// LDS.
 // ----------------------------------------------------------------------------
 template <int ZDT>
 __device__ __forceinline__ void wq_gemv8l_body(const uint16_t* __restrict__ X,
@@ -545,14 +546,11 @@ __device__ __forceinline__ void wq_gemv8l_body(const uint16_t* __restrict__ X,
     part[i] = a - 1152.0f * xs;
   }
   // rows 0..3 stay on lanes 0..31, 4..7 on lanes 32..63; then pairs by lane bit 4
-  const bool up32 = lane & 32, up16 = lane & 16;
   float p4[4], p2[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    p4[i] = (up32 ? part[i + 4] : part[i]) + __shfl_xor(up32 ? part[i] : part[i + 4], 32, 64);
+  for (int i = 0; i < 4; ++i) p4[i] = fold_swap<32>(part[i], part[i + 4]);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-    p2[i] = (up16 ? p4[i + 2] : p4[i]) + __shfl_xor(up16 ? p4[i] : p4[i + 2], 16, 64);
+  for (int i = 0; i < 2; ++i) p2[i] = fold_swap<16>(p4[i], p4[i + 2]);
   p2[0] = row16_sum(p2[0]);
   p2[1] = row16_sum(p2[1]);
   if ((lane & 15) == 0) {

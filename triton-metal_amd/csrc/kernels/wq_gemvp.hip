@@ -52,17 +52,6 @@ TM_DEV float sum_bits01(float v) {
   v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
   return v;
 }
-// A transposed step over lane bit 4 (O = 16) or 5 (O = 32) for two rows: the
-// lanes with the bit clear return row lo summed with their partner lane's,
-// the others row hi (one permlane swap: it trades lo's upper lanes for hi's
-// lower ones).
-template <int O> TM_DEV float fold_swap(float lo, float hi) {
-  const auto r = O == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(lo),
-                                                            __float_as_uint(hi), false, false)
-                         : __builtin_amdgcn_permlane32_swap(__float_as_uint(lo),
-                                                            __float_as_uint(hi), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 // Sum over lane bits 2 and 3 (lanes i, i + 4, i + 8, i + 12 of a 16-lane row:
 // two row rotations).
 TM_DEV float sum_bits23(float v) {
