@@ -232,6 +232,13 @@ template <int O> TM_DEV float max_swap(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Sum over lane bits 2 and 3, every lane receiving it (lanes i, i + 4, i + 8, i + 12 of a 16-lane row:
+// two row rotations).
+TM_DEV float sum_bits23(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+  return v;
+}
 // Wave-wide sum (64 lanes, every lane receives it): DPP within rows of 16,
 // then the two permlane swaps.
 TM_DEV float wave_sum(float v) {

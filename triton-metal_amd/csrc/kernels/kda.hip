@@ -773,8 +773,8 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent(KdaParams p) {
       S[r] *= ex2(gd[r] * kLog2e);
       dot = __builtin_fmaf(S[r], kf[r], dot);
     }
-#pragma unroll
-    for (int o = CW; o < 64; o <<= 1) dot += __shfl_xor(dot, o, 64);
+    dot = fold_swap<16>(dot, dot);
+    dot = fold_swap<32>(dot, dot);
     const float u = beta * (vj - dot);
     float od = 0.0f;
 #pragma unroll
@@ -782,8 +782,8 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent(KdaParams p) {
       S[r] = __builtin_fmaf(kf[r], u, S[r]);
       od = __builtin_fmaf(S[r], qf[r], od);
     }
-#pragma unroll
-    for (int o = CW; o < 64; o <<= 1) od += __shfl_xor(od, o, 64);
+    od = fold_swap<16>(od, od);
+    od = fold_swap<32>(od, od);
     if (rg == 0) p.o[tv + col] = f32_to_bf16_bits(od * p.scale);
   }
   if (p.st) {
@@ -798,7 +798,8 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent(KdaParams p) {
 // S[8 rg + r][v0 + 4 cq + e] (r < 8, e < 4) of each, so every state row piece
 // of 16 bytes moves in one access (8 loads and 8 stores per lane and slice
 // instead of 32), and the reductions over the key dimension are 8 in-lane
-// FMAs per column and four shuffles.  Both slices' state loads are issued
+// FMAs per column and four cross-lane steps (two DPP row rotations, two
+// permlane swaps).  Both slices' state loads are issued
 // first, and the first slice is updated and stored while the second is still
 // arriving (B=16, H=16, one token, same box: 11.15 -> 10.8 us; four slices
 // per wave measured slower).
@@ -846,9 +847,11 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent_v4(KdaParams p) {
         }
       }
 #pragma unroll
-      for (int o = 4; o < 64; o <<= 1)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dot[e] += __shfl_xor(dot[e], o, 64);
+      for (int e = 0; e < 4; ++e) {
+        dot[e] = sum_bits23(dot[e]);
+        dot[e] = fold_swap<16>(dot[e], dot[e]);
+        dot[e] = fold_swap<32>(dot[e], dot[e]);
+      }
       float u[4], od[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) u[e] = beta * (vj[e] - dot[e]);
@@ -859,13 +862,12 @@ extern "C" __global__ __launch_bounds__(64) void kda_recurrent_v4(KdaParams p) {
           S[sl][r][e] = __builtin_fmaf(kf[r], u[e], S[sl][r][e]);
           od[e] = __builtin_fmaf(S[sl][r][e], qf[r], od[e]);
         }
-#pragma unroll
-      for (int o = 4; o < 64; o <<= 1)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) od[e] += __shfl_xor(od[e], o, 64);
-      if (rg == 0)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) p.o[tv + col + e] = f32_to_bf16_bits(od[e] * p.scale);
+      // transposed fold of the 4 column sums: lane bit 5 picks columns
+      // {0, 1} / {2, 3}, bit 4 one of those, then the sum over bits 2 and 3
+      const float oe = sum_bits23(
+          fold_swap<16>(fold_swap<32>(od[0], od[2]), fold_swap<32>(od[1], od[3])));
+      if ((lane & 12) == 0)
+        p.o[tv + col + 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1)] = f32_to_bf16_bits(oe * p.scale);
     }
     if (p.st)
 #pragma unroll

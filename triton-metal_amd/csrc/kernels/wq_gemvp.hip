@@ -52,13 +52,6 @@ TM_DEV float sum_bits01(float v) {
   v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
   return v;
 }
-// Sum over lane bits 2 and 3 (lanes i, i + 4, i + 8, i + 12 of a 16-lane row:
-// two row rotations).
-TM_DEV float sum_bits23(float v) {
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
-  return v;
-}
 
 }  // namespace
 
