@@ -953,7 +953,12 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
     f4_t y[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) y[t] = f4_t{0.f, 0.f, 0.f, 0.f};
-    float xtot = 0.f;  // int8: sum x over the slice, row 16p + l16
+    // row sums of X (element e: row 4 q + e) from MFMAs against an all-ones
+    // B operand, already in the accumulator layout: int8 over the pass, int4
+    // per chunk
+    const uint32_t one2 = vgpr_const(BF16 ? 0x3F803F80u : 0x3C003C00u);
+    const u4_t ones = {one2, one2, one2, one2};
+    f4_t xacc = f4_t{0.f, 0.f, 0.f, 0.f};
     static_for<0, NCH>([&](auto IC) {
       constexpr int i = decltype(IC)::value;
       __builtin_amdgcn_sched_barrier(0);
@@ -999,16 +1004,11 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
           acc[t] = mfma16<BF16>(xop, wop, acc[t]);
         }
       }
-      // sum x of the chunk for row 16p + l16 (all four lane quarters)
-      float xs = 0.0f;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) xs += xsum8(xo[j], BF16);
-      xs += __shfl_xor(xs, 16, 64);
-      xs += __shfl_xor(xs, 32, 64);
       if constexpr (QB == 4) {
-        float xr[4];
+        // the chunk's X row sums (the permutation of k does not change them)
+        f4_t xr = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) xr[e] = __shfl(xs, 4 * q + e, 64);
+        for (int j = 0; j < NJ; ++j) xr = mfma16<BF16>(perm_x8(xo[j]), ones, xr);
         const int g = nwv * i + wave;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
@@ -1024,7 +1024,8 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
           for (int e = 0; e < 4; ++e) y[t][e] += sc * (acc[t][e] - zb * xr[e]);
         }
       } else {
-        xtot += xs;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) xacc = mfma16<BF16>(xo[j], ones, xacc);
 #pragma unroll
         for (int t = 0; t < NT; ++t) y[t] += acc[t];
       }
@@ -1034,9 +1035,7 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
       for (int t = 0; t < NT; ++t) asm volatile("" : "+v"(y[t]));
     });
     if constexpr (QB == 8) {
-      float xr[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xr[e] = __shfl(xtot, 4 * q + e, 64);
+      const f4_t xr = xacc;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int c = 16 * t + l16;
