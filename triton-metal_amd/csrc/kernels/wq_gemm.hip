@@ -386,7 +386,7 @@ __device__ __forceinline__ void wq_gemv4_body(const uint16_t* __restrict__ X,
 // 0x5400 at bits 4..7 it is 64 + q; bf16: under 0x4300 it is 128 + q) times
 // pairs of x with v_dot2_f32_{f16,bf16} into fp32, then per row
 // s * (sum x (OFF + q) - sum x OFF - z sum x).  The 64 lanes of a row are
-// summed with DPP / shuffles and the NS slices through LDS.
+// summed with DPP / permlane swaps and the NS slices through LDS.
 // ----------------------------------------------------------------------------
 template <bool BF16, int ZDT, int NS>
 __device__ __forceinline__ void wq_gemv4l_body(const uint16_t* __restrict__ X,
@@ -470,12 +470,7 @@ __device__ __forceinline__ void wq_gemv4l_body(const uint16_t* __restrict__ X,
   }
   // sum each row's 64 lanes: DPP within rows of 16, then across the 4 rows
 #pragma unroll
-  for (int i = 0; i < RW; ++i) {
-    float v = row16_sum(part[i]);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    part[i] = v;
-  }
+  for (int i = 0; i < RW; ++i) part[i] = wave_sum(part[i]);
   if (lane == 0) {
 #pragma unroll
     for (int i = 0; i < RW; ++i) red[h][r0 + i] = part[i];
