@@ -132,6 +132,21 @@ int tm_int8_linear(const void* input, const void* weight, const void* bias, void
 int tm_int4_linear(const void* input, const void* weight, const void* bias, void* output,
                    const void* scales, const void* zeros, int M, int N, int K, int group_size,
                    int act_dtype, int scale_dtype, int zero_dtype, void* stream);
+/* Kernel selection of the four entry points above, without launching: the
+ * name of the gfx950 kernel a call with these sizes and dtypes would run, its
+ * grid, block and dynamic LDS bytes, for a device with cu_count CUs and
+ * max_lds bytes of dynamic LDS per workgroup (MI355X: 256, 163840).
+ * align_flags: TM_WQ_ALIGN_* bits for the pointer alignments of the call.  A
+ * diagnostic with no counterpart in the reference (which compiles one kernel
+ * per template); it lets tests show which kernel family a shape reaches.
+ * Touches no device. */
+#define TM_WQ_ALIGN_XW16 1u /* input and weight 16-byte aligned */
+#define TM_WQ_ALIGN_S16 2u  /* scales 16-byte aligned */
+#define TM_WQ_ALIGN_Z16 4u  /* zeros 16-byte aligned (or no zeros) */
+#define TM_WQ_ALIGN_SZ4 8u  /* scales and zeros 4-byte aligned */
+int tm_wq_plan(int qbits, int M, int N, int K, int group_size, int act_dtype, int scale_dtype,
+               int zero_dtype, unsigned align_flags, int cu_count, size_t max_lds, char* name,
+               size_t name_len, unsigned* grid, unsigned* block, unsigned* lds_bytes);
 /* Dequantised weight tile out[n, k] = round_out((float(q) - z) * s), the
  * per-element arithmetic of _msl_templates.py:2671 (int8) / 2738-2739 (int4).
  * qbits 4 or 8; out_dtype F32/F16/BF16. */
@@ -170,6 +185,22 @@ int tm_wq_repack_awq(const void* qweight, const void* qzeros, const void* scales
  * 475-476) or F32; out_dtype F32/F16/BF16. */
 int tm_matmul(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb,
               int ldc, int in_dtype, int out_dtype, void* stream);
+/* Dense matmul with its sizes in device memory: C[M, N] = A[M, K] @ B[K, N],
+ * row-major with leading dimensions K, N, N; M, N, K are one uint32 each on
+ * the device, the buffer(3..5) arguments of make_matmul_2d_kernel
+ * (_msl_templates.py:588-679) and make_matmul_swizzled_kernel (682-781).
+ * max_m / max_n: the host-known capacity the launch covers; sizes read on
+ * the device are clamped to it (rows / columns beyond are not written), so a
+ * captured launch serves any M <= max_m, N <= max_n.  in_dtype F32, F16 or
+ * BF16; out_dtype in_dtype or F32; fp32 accumulation.  tm_matmul_2d walks
+ * the output tiles on a 2-D grid; tm_matmul_swizzled in runs of group_size
+ * tile rows (64-row tiles), column by column within a run. */
+int tm_matmul_2d(const void* A, const void* B, void* C, const unsigned* M, const unsigned* N,
+                 const unsigned* K, int max_m, int max_n, int in_dtype, int out_dtype,
+                 void* stream);
+int tm_matmul_swizzled(const void* A, const void* B, void* C, const unsigned* M,
+                       const unsigned* N, const unsigned* K, int max_m, int max_n,
+                       int group_size, int in_dtype, int out_dtype, void* stream);
 /* tl.dot in general form: the strided dot template of the reference,
  * _lower_dot_via_prebuilt_template (triton_metal/codegen/_lowerer_templates.py:
  * 1116-1540), with the epilogue detection of _detect_dot_epilogue
@@ -243,7 +274,9 @@ int tm_flash_attention(const void* q, const void* k, const void* v, void* o, flo
  * the cache's (an fp32 query over a 16-bit cache, as
  * make_fp16_kv_attention_kernel, _msl_templates.py:2558-2576, computes it) the
  * MFMA kernels carry the query and the softmax weights as hi + lo pairs of
- * cache-dtype operands, keeping fp32-level accuracy. */
+ * cache-dtype operands, keeping fp32-level accuracy.  Over an fp16 cache the
+ * pair spans |q| <= 131008 (hi saturates at 65504 and lo carries the rest);
+ * query elements beyond that saturate at +-131008. */
 size_t tm_decode_attention_workspace_size(int batch, int q_heads, int kv_heads, int head_dim,
                                           int seq_len, int page_size);
 int tm_decode_attention(const void* q, const void* k_cache, const void* v_cache, void* o,

@@ -60,15 +60,18 @@ def _attention(Q, K, V, S, D, scale, causal):
     return out
 
 
-def matmul_kat(name, test, seed, M, N, K, dist, lo, hi, tol, in_dtype="fp32", spot=1):
+def matmul_kat(name, test, seed, M, N, K, dist, lo, hi, tol, in_dtype="fp32", spot=1,
+               kind="matmul", spot_m=None, extra=None):
     random.seed(seed)
     draw = (lambda: random.uniform(lo, hi)) if dist == "uniform" else (
         lambda: random.gauss(lo, hi))
     A = [draw() for _ in range(M * K)]
     B = [draw() for _ in range(K * N)]
     C = _ref_matmul(A, B, M, N, K)
-    return name, dict(kind="matmul", test=test, seed=seed, M=M, N=N, K=K, tol=tol,
-                      in_dtype=in_dtype, spot=spot), dict(A=A, B=B, expected=C)
+    # checked entries: rows ::spot_m (default spot), columns ::spot
+    meta = dict(kind=kind, test=test, seed=seed, M=M, N=N, K=K, tol=tol, in_dtype=in_dtype,
+                spot=spot, spot_m=spot if spot_m is None else spot_m, **(extra or {}))
+    return name, meta, dict(A=A, B=B, expected=C)
 
 
 def linear_kat(name, test, seed, M, N, K, bias, tol):
@@ -204,6 +207,21 @@ def all_kats():
     kats.append(matmul_kat("simdgroup_f16_seed808",
                            "test_emitter.py:1408 test_simdgroup_matmul_fp16_64x64", 808,
                            64, 64, 64, "uniform", -0.5, 0.5, 0.15, in_dtype="fp16", spot=4))
+    # the sizes-in-device-memory templates (2-D dispatch and grouped order)
+    kats.append(matmul_kat("matmul2d_seed1001", "test_emitter.py:651 test_matmul_2d_small", 1001,
+                           16, 16, 16, "uniform", -1.0, 1.0, 1e-2, kind="matmul_2d"))
+    kats.append(matmul_kat("matmul2d_seed1002", "test_emitter.py:705 test_matmul_2d_multi_tile",
+                           1002, 64, 64, 64, "uniform", -0.5, 0.5, 1e-1, spot=8,
+                           kind="matmul_2d"))
+    kats.append(matmul_kat("matmul2d_seed1003", "test_emitter.py:758 test_matmul_2d_rectangular",
+                           1003, 48, 64, 32, "uniform", -1.0, 1.0, 1e-1, spot=8, spot_m=6,
+                           kind="matmul_2d"))
+    kats.append(matmul_kat("swizzled_seed2001", "test_emitter.py:815 test_matmul_swizzled_small",
+                           2001, 16, 16, 16, "uniform", -1.0, 1.0, 1e-2, kind="matmul_swizzled",
+                           extra=dict(group_size=4)))
+    kats.append(matmul_kat("swizzled_seed2002", "test_emitter.py:869 test_matmul_swizzled_large",
+                           2002, 128, 128, 64, "uniform", -0.5, 0.5, 1e-1, spot=16,
+                           kind="matmul_swizzled", extra=dict(group_size=4)))
     kats.append(linear_kat("linear_seed1111", "test_emitter.py:2402 test_fused_linear_no_bias",
                            1111, 32, 32, 32, False, 1e-2))
     kats.append(linear_kat("linear_seed2222", "test_emitter.py:2439 test_fused_linear_with_bias",

@@ -235,3 +235,28 @@ def test_reference_wrappers_capacity_beyond_seq_len(dev):
     ref, _ = oracle.decode_attention(Q[None].float().numpy(), Kr[None].float().numpy(),
                                      Vr[None].float().numpy(), [S], 0.2)
     np.testing.assert_allclose(O.float().cpu().numpy(), ref[0], atol=2e-2, rtol=1e-2)
+
+
+def test_decode_fp32_query_beyond_fp16_range(dev):
+    """An fp32 query with elements past the largest finite half (65504) over an
+    fp16 cache stays finite and exact: the hi part saturates at 65504 and the
+    lo part carries the remainder (70000 = 65504 + 4496, -100000 = -65504 -
+    34496, both halves exact), as the reference's fp32 arithmetic gives."""
+    g = _gen(31)
+    B, Hq, Hkv, D, S = 1, 4, 1, 64, 200
+    q = torch.randn(B, Hq, D, generator=g)
+    q[0, 0, 3] = 70000.0
+    q[0, 1, 10] = -100000.0
+    q[0, 2, 0] = 65504.0
+    k = torch.randn(B, Hkv, S, D, generator=g).half()
+    v = torch.randn(B, Hkv, S, D, generator=g).half()
+    scale = 1e-5
+    o = torch.empty(B, Hq, D, dtype=torch.float32, device=dev)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=dev)
+    tm.decode_attention(q.to(dev), k.to(dev), v.to(dev), scale=scale, o=o, lse=lse)
+    ref, ref_l = oracle.decode_attention(q.numpy(), k.float().numpy(), v.float().numpy(),
+                                         [S], scale)
+    got = o.cpu().numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ref, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_l, atol=1e-4, rtol=1e-5)

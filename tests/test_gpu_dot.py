@@ -131,6 +131,35 @@ def test_dot_add_cols_in_place_rejected_for_many_rows(dev):
         tm.dot(da, db, c, "add-cols", z=c)
 
 
+def test_dot_add_matrix_aliasing_view_rejected(dev):
+    """add-matrix in place is defined only when Z is C element for element; a
+    transposed view of C as Z would race between workgroups and is refused."""
+    M = N = K = 64
+    da, db, _, _ = _views(M, N, K, torch.float16, "row", seed=43)
+    c = torch.zeros(M, N, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="add-matrix"):
+        tm.dot(da, db, c, "add-matrix", z=c.t())
+    wide = torch.zeros(M, N + 1, dtype=torch.float16, device=dev)
+    with pytest.raises(RuntimeError, match="add-matrix"):
+        tm.dot(da, db, wide[:, :N], "add-matrix", z=wide[:, 1:])
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("side", ["a", "b"])
+def test_dot_batch_one_broadcast_3d(dev, dt, side):
+    """A 3-D operand of batch 1 is broadcast over the other operand's batch
+    (np.matmul's rule, which oracle.dot follows): [1, M, K] @ [B, K, N] and
+    [B, M, K] @ [1, K, N]."""
+    B, M, N, K = 3, 70, 40, 96
+    a = _rand((1 if side == "a" else B, M, K), 51, dt)
+    b = _rand((B if side == "a" else 1, K, N), 52, dt)
+    c = torch.empty(B, M, N, dtype=torch.float32, device=dev)
+    tm.dot(a.to(dev), b.to(dev), c)
+    ref = oracle.dot(_np(a), _np(b))
+    assert ref.shape == (B, M, N)
+    _check(c, ref, torch.float32, np.abs(_np(a)), np.abs(_np(b)))
+
+
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("N", [40, 1500])
 def test_dot_softmax(dev, dt, N):

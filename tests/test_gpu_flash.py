@@ -153,3 +153,44 @@ def test_flash_config_c4(dev, causal):
         ref_lse = mx[:, 0] + np.log(p.sum(1))
         np.testing.assert_allclose(o[b, h, rows].float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
         np.testing.assert_allclose(lse[b, h, rows].cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
+
+
+# --- the second signature: _fa_fwd_strided_kernel (tests/test_cpp_backend.py) ---
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fa_fwd_strided_signature(dev, D, dtype):
+    """The reference's N_CTX = 64 cases (test_cpp_flash_attention_head32 /
+    head64: seed 42, [N_CTX, D] fp32, sm_scale 1/sqrt(D), no mask) against
+    the oracle; fp32 within the reference's 5e-2 and within 1e-4."""
+    N = 64
+    torch.manual_seed(42)
+    q, k, v = (torch.randn(N, D) for _ in range(3))
+    q, k, v = (t.to(dtype).to(dev) for t in (q, k, v))
+    out = torch.zeros(N, D, dtype=dtype, device=dev)
+    tm.fa_fwd_strided(q, k, v, out, q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+                      v.stride(0), v.stride(1), out.stride(0), out.stride(1),
+                      1.0 / math.sqrt(D), N, D, 32, 32)
+    ref, _ = _ref(q[None, None], k[None, None], v[None, None], False)
+    err = np.abs(out.float().cpu().numpy() - ref[0, 0])
+    assert err.max() < 5e-2
+    if dtype == torch.float32:
+        assert err.max() < 1e-4
+    else:
+        assert np.all(err <= ATOL + RTOL * np.abs(ref[0, 0]))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_attn_fwd_strided_head_dim(dev, causal):
+    """stride_qk / stride_kk / stride_vk / stride_ok other than 1 (the head
+    dimension interleaved with another tensor, and a column-major output)."""
+    Z, H, N, D = 2, 3, 80, 64
+    qk2 = _rand((Z, H, N, D, 2), 11, torch.bfloat16, dev)   # q and k interleaved per element
+    q, k = qk2[..., 0], qk2[..., 1]
+    v = _rand((Z, H, N, D), 12, torch.bfloat16, dev)
+    obuf = torch.zeros(Z, H, D, N, dtype=torch.bfloat16, device=dev)
+    out = obuf.transpose(2, 3)  # [Z, H, N, D] with stride_ok = N
+    assert q.stride(3) == 2 and out.stride(3) == N
+    tm.flash_attn_fwd(q, k, v, out, *q.stride(), *k.stride(), *v.stride(), *out.stride(),
+                      Z, H, N, HEAD_DIM=D, IS_CAUSAL=causal)
+    ref, _ = _ref(q, k, v, causal)
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)

@@ -45,6 +45,67 @@ def test_matmul_reference_kat(kats, dev, name, out_dtype):
         np.testing.assert_allclose(C16.cpu().numpy(), ref, atol=1e-3, rtol=1e-4)
 
 
+DEVICE_SIZE_KATS = ["matmul2d_seed1001", "matmul2d_seed1002", "matmul2d_seed1003",
+                    "swizzled_seed2001", "swizzled_seed2002"]
+
+
+@pytest.mark.parametrize("name", DEVICE_SIZE_KATS)
+@pytest.mark.parametrize("sizes", ["device", "int", "capacity"])
+def test_device_sizes_reference_kat(kats, dev, name, sizes):
+    """make_matmul_2d_kernel / make_matmul_swizzled_kernel with M, N, K in
+    uint32 device buffers (the templates' buffer(3..5)), as Python ints, and
+    with a larger launch capacity than the sizes on the device; the reference
+    tests' tolerance on their sampled entries, and every entry within 1e-4 of
+    the oracle (fp32 in, fp32 out)."""
+    m, a = kats[name]
+    M, N, K = m["M"], m["N"], m["K"]
+    A = torch.tensor(a["A"], dtype=torch.float32, device=dev)
+    B = torch.tensor(a["B"], dtype=torch.float32, device=dev)
+    if m["kind"] == "matmul_2d":
+        kern = tm.make_matmul_2d_kernel(32, 32, 32)
+    else:
+        kern = tm.make_matmul_swizzled_kernel(32, 32, 32, group_size=m["group_size"])
+    if sizes == "int":
+        C = torch.empty(M * N, dtype=torch.float32, device=dev)
+        kern(A, B, C, M, N, K)
+    else:
+        u32 = lambda v: torch.tensor([v], dtype=torch.int32, device=dev).view(torch.uint32)
+        if sizes == "device":
+            C = torch.empty(M * N, dtype=torch.float32, device=dev)
+            kern(A, B, C, u32(M), u32(N), u32(K))
+        else:
+            C = torch.full((200 * 200,), 7.0, dtype=torch.float32, device=dev)
+            kern(A, B, C, u32(M), u32(N), u32(K), max_m=200, max_n=200)
+            assert torch.all(C[M * N:] == 7.0)  # nothing written past M x N
+            C = C[:M * N]
+    got = C.cpu().numpy().astype(np.float64)
+    sel = np.zeros((M, N), bool)
+    sel[::m["spot_m"], ::m["spot"]] = True
+    assert np.abs(got - a["expected"])[sel.ravel()].max() < m["tol"]
+    ref = oracle.matmul(a["A"].reshape(M, K), a["B"].reshape(K, N)).ravel()
+    np.testing.assert_allclose(got, ref, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dt,out", [(torch.float16, torch.float16), (torch.bfloat16, torch.float32),
+                                    (torch.float32, torch.float32)])
+@pytest.mark.parametrize("group", [0, 1, 3])
+def test_device_sizes_shapes(dev, dt, out, group):
+    """Ragged sizes across several 64 x 64 tiles, both tile orders (a run of
+    3 tile rows leaves a shorter last run), against the oracle; sizes on the
+    device smaller than the capacity."""
+    M, N, K = 200, 150, 77
+    A = _rand((M, K), 61, dt)
+    B = _rand((K, N), 62, dt)
+    C = torch.empty(256 * 160, dtype=out, device=dev)  # holds the capacity
+    dims = torch.tensor([M, N, K], dtype=torch.int32, device=dev)
+    tm.matmul_device_sizes(A.to(dev), B.to(dev), C, dims[0:1], dims[1:2], dims[2:3],
+                           max_m=256, max_n=160, group_size=group)
+    ref = oracle.matmul(A.double().numpy(), B.double().numpy())
+    tol = (1e-4, 1e-4) if out == torch.float32 else (ATOL, RTOL)
+    np.testing.assert_allclose(C[:M * N].double().cpu().numpy().reshape(M, N), ref,
+                               atol=tol[0], rtol=tol[1])
+
+
 @pytest.mark.parametrize("name", ["linear_seed1111", "linear_seed2222"])
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16])
 def test_fused_linear_reference_kat(kats, dev, name, dt):

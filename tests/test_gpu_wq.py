@@ -501,3 +501,57 @@ def test_act_order_checkpoint_rejected(dev):
     tm.from_gptq(qw, None, s, group_size=G, g_idx=trivial)
     with pytest.raises(ValueError):
         tm.from_gptq(qw, None, s, group_size=G, g_idx=trivial.flip(0))
+
+
+# --- every W-only kernel the dispatcher can select (tests/wq_cases.py) -----------
+from wq_cases import CASES, case_id, plan  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def cu_count(dev):
+    return torch.cuda.get_device_properties(dev).multi_processor_count
+
+
+@pytest.mark.parametrize("case", CASES, ids=case_id)
+def test_dispatch_case(dev, cu_count, case):
+    """Each case against the oracle (a column sample when N is large), with the
+    bias form on alternate cases; the kernel it reaches is named by tm_wq_plan
+    for this device, and on a 256-CU part is the kernel the CPU coverage test
+    counts."""
+    qbits, M, N, K, G, act, zeros = case
+    name = plan(case, cu_count)
+    if cu_count == 256:
+        assert name == plan(case)
+    print(f"[wq case] {case_id(case)} -> {name}", flush=True)
+    seed = (M * 131 + N * 7 + K) % 100003
+    use_bias = seed % 2 == 0
+    bias = (torch.randn(N, generator=_gen(seed)) * 0.5).to(act) if use_bias else None
+    out = torch.empty(M, N, dtype=act, device=dev)
+    cols = _cols(N) if N > 2048 else np.arange(N)
+    if qbits == 4:
+        zk = {None: None, "s": "f16", "u8": "u8"}[zeros]
+        x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=seed, act=act, zeros=zk)
+        args = (packed.to(dev), out, s.to(dev), None if z is None else z.to(dev), M, N, K, G)
+        if use_bias:
+            tm.int4_linear(x.to(dev), args[0], bias.to(dev), *args[1:])
+        else:
+            tm.int4_matmul(x.to(dev), *args)
+        ref = oracle.int4_matmul(np32(x), packed.numpy()[cols], np32(s)[cols],
+                                 None if z is None else np32(z)[cols], M, len(cols), K, G)
+    else:
+        x, w, s, _ = make_int8_problem(M, N, K, seed=seed, act=act)
+        z = None
+        if zeros == "s":
+            z = torch.randint(-3, 4, (N,), generator=_gen(seed + 1)).to(act)
+        elif zeros == "u8":
+            z = torch.randint(0, 5, (N,), generator=_gen(seed + 1)).to(torch.uint8)
+        args = (w.to(dev), out, s.to(dev), None if z is None else z.to(dev), M, N, K)
+        if use_bias:
+            tm.int8_linear(x.to(dev), args[0], bias.to(dev), *args[1:])
+        else:
+            tm.int8_matmul(x.to(dev), *args)
+        ref = oracle.int8_matmul(np32(x), w.numpy()[cols], np32(s)[cols],
+                                 None if z is None else np32(z)[cols], M, len(cols), K)
+    if use_bias:
+        ref = ref + np32(bias)[cols][None, :].astype(np.float64)
+    check_close(out.cpu()[:, cols], ref)

@@ -6,7 +6,9 @@ import oracle
 
 MATMUL_KATS = ["matmul_seed789", "matmul_seed101r", "matmul_seed202", "matmul_seed42",
                "matmul_seed101g", "simdgroup_seed88", "simdgroup_seed303", "simdgroup_seed404",
-               "simdgroup_seed505", "simdgroup_f16_seed707", "simdgroup_f16_seed808"]
+               "simdgroup_seed505", "simdgroup_f16_seed707", "simdgroup_f16_seed808",
+               "matmul2d_seed1001", "matmul2d_seed1002", "matmul2d_seed1003",
+               "swizzled_seed2001", "swizzled_seed2002"]
 
 
 @pytest.mark.parametrize("name", MATMUL_KATS)

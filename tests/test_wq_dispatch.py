@@ -1,0 +1,104 @@
+"""W-only kernel selection and code-object hygiene, on the CPU.
+
+* Every W-only matmul kernel built into libtm_hip.so is reachable: some case of
+  tests/wq_cases.py (each of which tests/test_gpu_wq.py runs on the GPU)
+  selects it through tm_wq_plan, the selection the launch path uses.
+* No hot-path kernel uses scratch memory (private_segment_fixed_size == 0, so
+  no register spills to memory), read from the built code objects' metadata.
+"""
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+from wq_cases import CASES, case_id, plan
+
+ROOT = Path(__file__).resolve().parent.parent
+BUILD = ROOT / "triton-metal_amd" / "_build"
+LLVM = Path("/opt/rocm/llvm/bin")
+
+# fallback kernels that hold per-lane arrays indexed at run time (the general
+# FlashAttention kernel for head dims other than 32 / 64 / 128 layouts)
+SCRATCH_ALLOWED = {"flash_fwd_general_d64", "flash_fwd_general_d128"}
+
+
+def _kernel_metadata(hsaco: Path, tmp: Path):
+    """[(name, private_segment_fixed_size, vgpr_count)] of a bundled code object."""
+    bundler, readelf = LLVM / "clang-offload-bundler", LLVM / "llvm-readelf"
+    if not (bundler.exists() and readelf.exists()):
+        pytest.skip("ROCm LLVM tools not found")
+    co = tmp / (hsaco.stem + ".co")
+    subprocess.run([str(bundler), "--unbundle", "--type=o", f"--input={hsaco}",
+                    f"--output={co}", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950"], check=True)
+    notes = subprocess.run([str(readelf), "--notes", str(co)], check=True, capture_output=True,
+                           text=True).stdout
+    out, cur = [], {}
+    for line in notes.splitlines():
+        m = re.match(r"\s+\.(name|private_segment_fixed_size|vgpr_count):\s+(\S+)", line)
+        if not m:
+            continue
+        k, v = m.groups()
+        if k == "name" and "name" in cur:
+            out.append(cur)
+            cur = {}
+        cur[k] = v
+    if cur:
+        out.append(cur)
+    return [(d["name"], int(d.get("private_segment_fixed_size", 0)), int(d.get("vgpr_count", 0)))
+            for d in out if "name" in d]
+
+
+def _built(stem):
+    p = BUILD / f"{stem}.hsaco"
+    if not p.exists():
+        pytest.skip(f"{p} not built (run __graft_entry__.build())")
+    return p
+
+
+@pytest.fixture(scope="module")
+def wq_kernels(tmp_path_factory):
+    tmp = tmp_path_factory.mktemp("co")
+    names = set()
+    for stem in ("wq_gemm", "wq_gemvp"):
+        names |= {n for n, _, _ in _kernel_metadata(_built(stem), tmp)}
+    return {n for n in names if n != "wq_dequant"}
+
+
+def test_cases_cover_every_wq_kernel(wq_kernels):
+    reached = {plan(c) for c in CASES}
+    missing = sorted(wq_kernels - reached)
+    assert not missing, f"W-only kernels no GPU case reaches: {missing}"
+    assert reached <= wq_kernels, sorted(reached - wq_kernels)
+
+
+@pytest.mark.parametrize("c", [c for c in CASES if c[1] == 1 and c[3] == 4096 and c[0] == 4],
+                         ids=case_id)
+def test_m1_k4096_branches(c):
+    """int4 M = 1, K = 4096: the persistent kernel up to N = 16384 on 256 CUs,
+    the linear GEMV beyond."""
+    name = plan(c)
+    assert name.startswith("wq_gemv4p_" if c[2] <= 16384 else "wq_gemv4l_"), name
+
+
+def test_plan_depends_on_cu_count():
+    # 14336 rows need 256 workgroups of 56; with 128 CUs the persistent grid
+    # would take a second round, so the plan moves to the linear GEMV
+    c = (4, 1, 14336, 4096, 128, torch.float16, "s")
+    assert plan(c, 256) == "wq_gemv4p_f16_zs_r14"
+    assert plan(c, 128).startswith("wq_gemv4l_")
+
+
+def test_no_scratch_in_hot_path_kernels(tmp_path):
+    if shutil.which(str(LLVM / "llvm-readelf")) is None and not (LLVM / "llvm-readelf").exists():
+        pytest.skip("llvm-readelf not found")
+    bad = []
+    for hsaco in sorted(BUILD.glob("*.hsaco")):
+        for name, priv, _ in _kernel_metadata(hsaco, tmp_path):
+            if priv and name not in SCRATCH_ALLOWED:
+                bad.append((hsaco.stem, name, priv))
+    if not list(BUILD.glob("*.hsaco")):
+        pytest.skip("code objects not built")
+    assert not bad, bad

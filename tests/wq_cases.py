@@ -1,0 +1,63 @@
+"""One W-only matmul case per kernel the dispatcher of tm_int4_matmul /
+tm_int8_matmul can select (ops_gemm.cpp wq_plan), for torch-allocated
+(aligned) buffers on a 256-CU MI355X.
+
+Each case is (qbits, M, N, K, G, act, zeros); zeros is None, "s" (the scale
+dtype) or "u8".  tests/test_wq_dispatch.py checks on the CPU that the cases
+reach every instantiated W-only kernel; tests/test_gpu_wq.py runs every case
+on the GPU against the oracle.
+"""
+import torch
+
+ACTS = (torch.float16, torch.bfloat16)
+ZEROS = (None, "s", "u8")
+
+
+def _each(qbits, M, N, K, G=128, acts=ACTS, zeros=ZEROS):
+    return [(qbits, M, N, K, G, a, z) for a in acts for z in zeros]
+
+
+CASES = []
+# wide kernels (fp16 activations, M > 64): int4 every zero form, int8 none
+CASES += _each(4, 80, 256, 1024, acts=(torch.float16,))
+CASES += _each(8, 80, 256, 512, acts=(torch.float16,), zeros=(None,))
+# two-tile int4 GEMV, 2 <= M <= 6, K = 4096
+CASES += _each(4, 3, 64, 4096)
+# streaming kernels: x8s (M <= 8), x16s (M <= 16), x16m (M <= 64 / 128)
+for M, K in ((8, 1024), (12, 2048), (40, 512)):
+    CASES += _each(4, M, 64, K)
+    CASES += _each(8, M, 48, K)
+# persistent int4 GEMV, M = 1, K = 4096: one N per rows-per-wave count
+for N in (1024, 7168, 8192, 11264, 12288, 14336, 16384):
+    CASES += _each(4, 1, N, 4096)
+# linear int4 GEMV: K = 4096 past the persistent kernel's reach (N > 16384 on
+# 256 CUs, e.g. a fused gate/up projection), and K = 8192
+CASES += _each(4, 1, 16400, 4096)
+CASES += _each(4, 1, 28672, 4096, acts=(torch.float16,))
+CASES += _each(4, 1, 64, 8192)
+# int4 GEMV at K = 8192, 2 <= M <= 8
+CASES += _each(4, 4, 64, 8192)
+# int8 GEMVs, M = 1, K = 4096: linear (fp16) and 8-wave (bf16)
+CASES += _each(8, 1, 64, 4096)
+# skinny (M <= 8, other K): int4 without and with vector scale loads, int8
+CASES += _each(4, 1, 64, 1024)
+CASES += _each(4, 2, 64, 12288)
+CASES += _each(8, 1, 64, 1024)
+# tiled (K past the streaming kernel's 4096, M > 8)
+CASES += _each(4, 9, 64, 4352)
+CASES += _each(8, 9, 64, 4352)
+# general fp32 kernel
+CASES += [(4, 3, 40, 100, 32, torch.float32, None), (8, 3, 40, 100, 1, torch.float32, "s")]
+
+
+def case_id(c):
+    q, M, N, K, G, a, z = c
+    return f"q{q}-M{M}-N{N}-K{K}-G{G}-{str(a).split('.')[-1]}-z{z}"
+
+
+def plan(c, cu_count=256):
+    """Kernel name for a case (tm_wq_plan through wq_kernel_for)."""
+    import triton_metal_amd as tm
+    q, M, N, K, G, a, z = c
+    zdt = None if z is None else (torch.uint8 if z == "u8" else a)
+    return tm.wq_kernel_for(q, M, N, K, G, act_dtype=a, zero_dtype=zdt, cu_count=cu_count)[0]

@@ -96,14 +96,22 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
 
   // A bias read in place from the output (Z overlapping C), as the
   // reference's test kernels do: add-matrix reads and writes each element in
-  // one thread; add-rows reads its row's element in the row's own workgroup
-  // (dot_rows) before any store; add-cols across rows would race.
+  // one thread, which is only race-free when Z is C element for element (same
+  // base, dtype and strides); add-rows reads its row's element in the row's
+  // own workgroup (dot_rows) before any store; add-cols across rows would race.
   bool rows_kernel = epilogue == TM_EPI_SOFTMAX || chain || in_dtype == TM_DT_F32 || K == 0;
-  if (add && epilogue != TM_EPI_ADD_MATRIX) {
+  if (add) {
     uintptr_t zl, zh, cl, ch;
     extent(Z, elem_size(z_dtype), batch, M, N, st[9], st[10], st[11], &zl, &zh);
     extent(C, elem_size(out_dtype), batch, M, NC, st[6], st[7], st[8], &cl, &ch);
-    if (zl < ch && cl < zh) {
+    const bool overlap = zl < ch && cl < zh;
+    if (overlap && epilogue == TM_EPI_ADD_MATRIX) {
+      const bool same_b = st[9] == st[6] || batch == 1;
+      if (Z != C || z_dtype != out_dtype || !same_b || st[10] != st[7] || st[11] != st[8])
+        return fail(TM_ERR_INVALID_ARG,
+                    "%s: add-matrix with Z overlapping C needs Z to be C itself (same "
+                    "dtype and strides)", op);
+    } else if (overlap) {
       if (epilogue == TM_EPI_ADD_COLS && (long long)batch * M > 1)
         return fail(TM_ERR_INVALID_ARG,
                     "%s: add-cols with Z overlapping C is only defined for one row", op);

@@ -39,6 +39,133 @@ Kernel& kernel(const std::string& name) {
   return *k;
 }
 
+// ---- W-only kernel selection ------------------------------------------------
+// A pure function of the problem (sizes, dtypes, pointer alignment, the
+// device's CU count and LDS limit): the launch path and tm_wq_plan share it.
+enum { WQ_ARGS_STD = 0, WQ_ARGS_G = 1, WQ_ARGS_GENERAL = 2 };
+struct WqPlan {
+  char name[64];
+  unsigned grid, block, lds;
+  int form;  // argument list: WQ_ARGS_*
+};
+
+void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, unsigned align,
+             int cus, size_t max_lds, WqPlan* pl) {
+  auto set = [&](unsigned grid, unsigned block, size_t lds, int form) {
+    pl->grid = grid;
+    pl->block = block;
+    pl->lds = (unsigned)lds;
+    pl->form = form;
+  };
+  const bool a16 = align & TM_WQ_ALIGN_XW16, s16 = align & TM_WQ_ALIGN_S16,
+             z16 = align & TM_WQ_ALIGN_Z16, sz4 = align & TM_WQ_ALIGN_SZ4;
+  const int CK = qbits == 4 ? 128 : 64;
+  const bool fast = is_half(adt) && sdt == adt &&
+                    (zdt == TM_DT_NONE || zdt == sdt || zdt == TM_DT_U8) &&
+                    (qbits == 8 || G % 128 == 0) && N % 16 == 0 && K > 0 && a16;
+  const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
+  const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
+  // wide kernel: fp16 activations, M > 64, 64 x 128 output blocks
+  if (fast && adt == TM_DT_F16 && M > 64 && N % 128 == 0 && s16 && z16 &&
+      ((qbits == 4 && G == 128 && K % 512 == 0 && K <= 4096) ||
+       (qbits == 8 && zdt == TM_DT_NONE && K % 128 == 0))) {
+    const int ns = qbits == 4 ? 3 : 4, ck = qbits == 4 ? 64 : 32;
+    size_t wl = (size_t)ns * 4 * (64 * 2 * ck + 4096);  // ring stages
+    if (qbits == 4)  // scales and zero-points of the 128 columns
+      wl += (size_t)2 * K + (zdt == TM_DT_NONE ? 0 : zdt == TM_DT_U8 ? (size_t)K : (size_t)2 * K);
+    if (wl <= max_lds) {
+      snprintf(pl->name, sizeof pl->name, "wq_wide_q%d_f16_z%c", qbits, zc);
+      const int mtl = (M + 63) / 64, ntl = N / 128;
+      return set(8 * mtl * ((ntl + 7) / 8), 512, wl, WQ_ARGS_STD);
+    }
+  }
+  // two-tile int4 GEMV: 2 <= M <= 6 at K = 4096 (from M = 7 on the streaming
+  // kernel is as fast or faster), 32 columns per workgroup
+  if (fast && qbits == 4 && M >= 2 && M <= 6 && G == 128 && K == 4096 && N % 32 == 0 && s16 &&
+      z16) {
+    // X, then the scales and zero-points of 32 columns; at least the
+    // reduction's 7 waves x 2 tiles x 1 KB
+    size_t glds = (size_t)M * (K + 8) * 2 + (size_t)4 * 32 * (K / 128);
+    glds = std::max(glds, (size_t)7 * 2 * 1024);
+    if (glds <= max_lds) {
+      snprintf(pl->name, sizeof pl->name, "wq_gemv4x2_%s_z%c_w8p4", act, zc);
+      return set(N / 32, 512, glds, WQ_ARGS_STD);
+    }
+  }
+  // streaming kernel: 1 < M <= 64 (int4: 128), K-slices of 512 per wave (at
+  // most 8); past 64 rows the int8 tiled kernel is the faster one
+  if (fast && M > 1 && M <= (qbits == 4 ? 128 : 64) && K % 512 == 0 && K <= 4096 && sz4 &&
+      (qbits == 8 || G == 128)) {
+    const int nwv = K / 512;
+    const int nt = qbits == 4 ? 4 : 3;           // 16-column tiles per workgroup
+    const int xr = M <= 8 ? 8 : 16;              // X rows staged per chunk
+    const int rs = qbits == 4 ? 2 : 3;           // ring slots per wave
+    const int slot = nt * 1024 + xr * (qbits == 4 ? 256 : 128);
+    // per wave: ring, scales / zero-points (int4 2 KB, int8 1 KB); reduction
+    const size_t slds = (size_t)nwv * (rs * slot + (qbits == 4 ? 2048 : 1024)) +
+                        (size_t)nwv * 8 * 64 * sizeof(float);
+    if (slds <= max_lds) {
+      snprintf(pl->name, sizeof pl->name, "wq_stream_q%d_%s_z%c_x%d%c", qbits, act, zc, xr,
+               M <= 16 ? 's' : 'm');
+      const int tiles = N / 16;
+      return set((tiles + nt - 1) / nt, 64 * nwv, slds, WQ_ARGS_STD);
+    }
+  }
+  // persistent int4 GEMV: M = 1, K = 4096, G = 128; one workgroup per CU owns
+  // 4 RW rows, RW the smallest instantiated count that keeps the grid within
+  // the CUs (a second round of workgroups would double the time)
+  if (fast && qbits == 4 && M == 1 && G == 128 && K == 4096) {
+    static const int kRW[] = {4, 7, 8, 11, 12, 14, 16};
+    for (int rw : kRW) {
+      const int grid = (N + 4 * rw - 1) / (4 * rw);
+      if (N >= 4 * rw && grid <= cus) {
+        snprintf(pl->name, sizeof pl->name, "wq_gemv4p_%s_z%c_r%d", act, zc, rw);
+        return set(grid, 512, 0, WQ_ARGS_STD);
+      }
+    }
+  }
+  // linear int4 GEMV: M = 1, G = 128, K = 4096 (N past the persistent
+  // kernel's reach) or 8192 (VALU dot products, 1 KB of one row per load)
+  if (fast && qbits == 4 && M == 1 && G == 128 && (K == 4096 || K == 8192)) {
+    snprintf(pl->name, sizeof pl->name, "wq_gemv4l_%s_z%c_k%d", act, zc, K / 2048);
+    return set(N / 16, 512, 0, WQ_ARGS_STD);
+  }
+  // exact-shape int4 GEMV: K = 8 waves x 8 chunks x 128 = 8192, G = 128,
+  // 2 <= M <= 8 (M = 1 took the linear GEMV above)
+  if (fast && qbits == 4 && M <= 8 && G == 128 && K == 8192 && s16 && z16) {
+    // X, two [chunk][8] float sums (sum x, sum x * offset), scales + zero-points
+    size_t glds = (size_t)M * (K + 8) * 2 + 2 * (size_t)(K / 128) * 8 * 4 + (size_t)(K / 128) * 64;
+    if (glds <= max_lds) {
+      snprintf(pl->name, sizeof pl->name, "wq_gemv4_%s_z%c_w8p8", act, zc);
+      return set(N / 16, 512, glds, WQ_ARGS_STD);
+    }
+  }
+  // linear int8 GEMV: M = 1, K = 4096, fp16 (VALU dot products, 1 KB of one
+  // row per load instruction)
+  if (fast && qbits == 8 && M == 1 && K == 4096 && adt == TM_DT_F16) {
+    snprintf(pl->name, sizeof pl->name, "wq_gemv8l_f16_z%c", zc);
+    return set(N / 16, 512, 0, WQ_ARGS_STD);
+  }
+  // int8 GEMV: M = 1, K = 4096, bf16 (8 waves x 8 loads of 16 bytes per lane)
+  if (fast && qbits == 8 && M == 1 && K == 4096 && adt == TM_DT_BF16) {
+    snprintf(pl->name, sizeof pl->name, "wq_gemv8_%s_z%c_w8p8", act, zc);
+    return set(N / 16, 512, (size_t)(K + 8) * 2, WQ_ARGS_STD);
+  }
+  const size_t lds = (size_t)M * (K + 8) * 2 + (size_t)M * (K / 128) * 4;
+  if (fast && M <= 8 && K % (4 * CK) == 0 && lds <= max_lds) {
+    const bool vs = qbits == 4 && G == 128 && K % 4096 == 0;
+    snprintf(pl->name, sizeof pl->name, "wq_skinny_q%d_%s_z%c%s", qbits, act, zc, vs ? "_v" : "");
+    return set(N / 16, 256, lds, WQ_ARGS_G);
+  }
+  if (fast && K % 256 == 0 && N % 64 == 0) {
+    snprintf(pl->name, sizeof pl->name, "wq_tiled_q%d_%s_z%c", qbits, act, zc);
+    const int tiles = ((M + 63) / 64) * (N / 64);
+    return set((tiles + 7) / 8 * 8, 256, 0, WQ_ARGS_G);
+  }
+  snprintf(pl->name, sizeof pl->name, "wq_general");
+  set((N + 3) / 4, 256, 0, WQ_ARGS_GENERAL);
+}
+
 int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, const void* Z,
               int M, int N, int K, int G, int adt, int sdt, int zdt, const void* bias,
               void* stream) {
@@ -59,139 +186,24 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
   if (!api()) return TM_ERR_NO_RUNTIME;
   clear_error();
 
-  const int CK = qbits == 4 ? 128 : 64;
-  bool fast = is_half(adt) && sdt == adt &&
-              (zdt == TM_DT_NONE || zdt == sdt || zdt == TM_DT_U8) &&
-              (qbits == 8 || G % 128 == 0) && N % 16 == 0 && K > 0 && aligned16(X) &&
-              aligned16(W);
-  const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
-  const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
-  // wide kernel: fp16 activations, M > 64, 64 x 128 output blocks
-  if (fast && adt == TM_DT_F16 && M > 64 && N % 128 == 0 && aligned16(S) &&
-      (!Z || aligned16(Z)) &&
-      ((qbits == 4 && G == 128 && K % 512 == 0 && K <= 4096) ||
-       (qbits == 8 && zdt == TM_DT_NONE && K % 128 == 0))) {
-    const int ns = qbits == 4 ? 3 : 4, ck = qbits == 4 ? 64 : 32;
-    size_t wl = (size_t)ns * 4 * (64 * 2 * ck + 4096);  // ring stages
-    if (qbits == 4)  // scales and zero-points of the 128 columns
-      wl += (size_t)2 * K + (zdt == TM_DT_NONE ? 0 : zdt == TM_DT_U8 ? (size_t)K : (size_t)2 * K);
-    if (wl <= (size_t)max_dynamic_lds()) {
-      char name[64];
-      snprintf(name, sizeof name, "wq_wide_q%d_f16_z%c", qbits, zc);
-      const int mtl = (M + 63) / 64, ntl = N / 128;
-      const int grid = 8 * mtl * ((ntl + 7) / 8);
-      return launch(kernel(name), dim3(grid), dim3(512), (unsigned)wl, stream, X, W, Y, S, Z, M,
-                    N, K, bias);
-    }
+  unsigned align = 0;
+  if (aligned16(X) && aligned16(W)) align |= TM_WQ_ALIGN_XW16;
+  if (aligned16(S)) align |= TM_WQ_ALIGN_S16;
+  if (!Z || aligned16(Z)) align |= TM_WQ_ALIGN_Z16;
+  if (((uintptr_t)S & 3u) == 0 && (!Z || ((uintptr_t)Z & 3u) == 0)) align |= TM_WQ_ALIGN_SZ4;
+  WqPlan pl;
+  wq_plan(qbits, M, N, K, G, adt, sdt, zdt, align, cu_count(), (size_t)max_dynamic_lds(), &pl);
+  Kernel& k = kernel(pl.name);
+  const dim3 grid(pl.grid), block(pl.block);
+  switch (pl.form) {
+    case WQ_ARGS_G:
+      return launch(k, grid, block, pl.lds, stream, X, W, Y, S, Z, M, N, K, G, bias);
+    case WQ_ARGS_GENERAL:
+      return launch(k, grid, block, pl.lds, stream, X, (const uint8_t*)W, Y, S, Z, M, N, K,
+                    qbits == 4 ? G : 1, qbits, adt, sdt, zdt, bias);
+    default:
+      return launch(k, grid, block, pl.lds, stream, X, W, Y, S, Z, M, N, K, bias);
   }
-  // two-tile int4 GEMV: 2 <= M <= 6 at K = 4096 (from M = 7 on the streaming
-  // kernel is as fast or faster), 32 columns per workgroup
-  if (fast && qbits == 4 && M >= 2 && M <= 6 && G == 128 && K == 4096 && N % 32 == 0 &&
-      aligned16(S) && (!Z || aligned16(Z))) {
-    // X, then the scales and zero-points of 32 columns; at least the
-    // reduction's 7 waves x 2 tiles x 1 KB
-    size_t glds = (size_t)M * (K + 8) * 2 + (size_t)4 * 32 * (K / 128);
-    glds = std::max(glds, (size_t)7 * 2 * 1024);
-    if (glds <= (size_t)max_dynamic_lds()) {
-      char name[64];
-      snprintf(name, sizeof name, "wq_gemv4x2_%s_z%c_w8p4", act, zc);
-      return launch(kernel(name), dim3(N / 32), dim3(512), (unsigned)glds, stream, X, W, Y, S,
-                    Z, M, N, K, bias);
-    }
-  }
-  // streaming kernel: 1 < M <= 64 (int4: 128), K-slices of 512 per wave (at
-  // most 8); past 64 rows the int8 tiled kernel is the faster one
-  const bool aligned4 = ((uintptr_t)S & 3u) == 0 && (!Z || ((uintptr_t)Z & 3u) == 0);
-  if (fast && M > 1 && M <= (qbits == 4 ? 128 : 64) && K % 512 == 0 && K <= 4096 && aligned4 &&
-      (qbits == 8 || G == 128)) {
-    const int nwv = K / 512;
-    const int nt = qbits == 4 ? 4 : 3;           // 16-column tiles per workgroup
-    const int xr = M <= 8 ? 8 : 16;              // X rows staged per chunk
-    const int rs = qbits == 4 ? 2 : 3;           // ring slots per wave
-    const int slot = nt * 1024 + xr * (qbits == 4 ? 256 : 128);
-    // per wave: ring, scales / zero-points (int4 2 KB, int8 1 KB); reduction
-    const size_t slds = (size_t)nwv * (rs * slot + (qbits == 4 ? 2048 : 1024)) +
-                        (size_t)nwv * 8 * 64 * sizeof(float);
-    if (slds <= (size_t)max_dynamic_lds()) {
-      char name[64];
-      snprintf(name, sizeof name, "wq_stream_q%d_%s_z%c_x%d%c", qbits, act, zc, xr,
-               M <= 16 ? 's' : 'm');
-      const int tiles = N / 16;
-      return launch(kernel(name), dim3((tiles + nt - 1) / nt), dim3(64 * nwv), (unsigned)slds,
-                    stream, X, W, Y, S, Z, M, N, K, bias);
-    }
-  }
-  // persistent int4 GEMV: M = 1, K = 4096, G = 128; one workgroup per CU owns
-  // 4 RW rows, RW the smallest instantiated count that keeps the grid within
-  // the CUs (a second round of workgroups would double the time)
-  if (fast && qbits == 4 && M == 1 && G == 128 && K == 4096) {
-    static const int kRW[] = {4, 7, 8, 11, 12, 14, 16};
-    const int cus = cu_count();
-    for (int rw : kRW) {
-      const int grid = (N + 4 * rw - 1) / (4 * rw);
-      if (N >= 4 * rw && grid <= cus) {
-        char name[64];
-        snprintf(name, sizeof name, "wq_gemv4p_%s_z%c_r%d", act, zc, rw);
-        return launch(kernel(name), dim3(grid), dim3(512), 0, stream, X, W, Y, S, Z, M, N, K,
-                      bias);
-      }
-    }
-  }
-  // linear int4 GEMV: M = 1, G = 128, K = 4096 or 8192 (VALU dot products,
-  // 1 KB of one row per load instruction)
-  if (fast && qbits == 4 && M == 1 && G == 128 && (K == 4096 || K == 8192)) {
-    char name[64];
-    snprintf(name, sizeof name, "wq_gemv4l_%s_z%c_k%d", act, zc, K / 2048);
-    return launch(kernel(name), dim3(N / 16), dim3(512), 0, stream, X, W, Y, S, Z, M, N, K,
-                  bias);
-  }
-  // exact-shape int4 GEMV: K = NW * PF * 128, G = 128
-  if (fast && qbits == 4 && M <= 8 && G == 128 && (K == 4096 || K == 8192) && aligned16(S) &&
-      (!Z || aligned16(Z))) {
-    // X, two [chunk][8] float sums (sum x, sum x * offset), scales + zero-points
-    size_t glds = (size_t)M * (K + 8) * 2 + 2 * (size_t)(K / 128) * 8 * 4 + (size_t)(K / 128) * 64;
-    if (glds <= (size_t)max_dynamic_lds()) {
-      const int pf = K == 4096 ? 4 : 8;
-      char name[64];
-      snprintf(name, sizeof name, "wq_gemv4_%s_z%c_w8p%d", act, zc, pf);
-      return launch(kernel(name), dim3(N / 16), dim3(512), (unsigned)glds, stream, X, W, Y, S,
-                    Z, M, N, K, bias);
-    }
-  }
-  // linear int8 GEMV: M = 1, K = 4096, fp16 (VALU dot products, 1 KB of one
-  // row per load instruction)
-  if (fast && qbits == 8 && M == 1 && K == 4096 && adt == TM_DT_F16) {
-    char name[64];
-    snprintf(name, sizeof name, "wq_gemv8l_f16_z%c", zc);
-    return launch(kernel(name), dim3(N / 16), dim3(512), 0, stream, X, W, Y, S, Z, M, N, K,
-                  bias);
-  }
-  // int8 GEMV: M = 1, K = 4096 (8 waves x 8 loads of 16 bytes per lane)
-  if (fast && qbits == 8 && M == 1 && K == 4096) {
-    char name[64];
-    snprintf(name, sizeof name, "wq_gemv8_%s_z%c_w8p8", act, zc);
-    return launch(kernel(name), dim3(N / 16), dim3(512), (unsigned)((K + 8) * 2), stream, X, W,
-                  Y, S, Z, M, N, K, bias);
-  }
-  size_t lds = (size_t)M * (K + 8) * 2 + (size_t)M * (K / 128) * 4;
-  if (fast && M <= 8 && K % (4 * CK) == 0 && lds <= (size_t)max_dynamic_lds()) {
-    char name[64];
-    const bool vs = qbits == 4 && G == 128 && K % 4096 == 0;
-    snprintf(name, sizeof name, "wq_skinny_q%d_%s_z%c%s", qbits, act, zc, vs ? "_v" : "");
-    return launch(kernel(name), dim3(N / 16), dim3(256), (unsigned)lds, stream, X, W, Y, S, Z, M,
-                  N, K, G, bias);
-  }
-  if (fast && K % 256 == 0 && N % 64 == 0) {
-    char name[64];
-    snprintf(name, sizeof name, "wq_tiled_q%d_%s_z%c", qbits, act, zc);
-    int tiles = ((M + 63) / 64) * (N / 64);
-    int grid = (tiles + 7) / 8 * 8;
-    return launch(kernel(name), dim3(grid), dim3(256), 0, stream, X, W, Y, S, Z, M, N, K, G,
-                  bias);
-  }
-  int Gg = qbits == 4 ? G : 1;
-  return launch(kernel("wq_general"), dim3((N + 3) / 4), dim3(256), 0, stream, X,
-                (const uint8_t*)W, Y, S, Z, M, N, K, Gg, qbits, adt, sdt, zdt, bias);
 }
 
 int dense(const void* A, const void* B, void* C, const void* bias, int M, int N, int K, int lda,
@@ -294,6 +306,25 @@ int tm_int4_linear(const void* input, const void* weight, const void* bias, void
                    scale_dtype, zero_dtype, bias, stream);
 }
 
+
+int tm_wq_plan(int qbits, int M, int N, int K, int group_size, int act_dtype, int scale_dtype,
+               int zero_dtype, unsigned align_flags, int cu_count, size_t max_lds, char* name,
+               size_t name_len, unsigned* grid, unsigned* block, unsigned* lds_bytes) {
+  if ((qbits != 4 && qbits != 8) || M <= 0 || N <= 0 || K <= 0 || cu_count <= 0 ||
+      (qbits == 4 && group_size <= 0))
+    return fail(TM_ERR_INVALID_ARG, "tm_wq_plan: qbits=%d M=%d N=%d K=%d G=%d cus=%d", qbits, M,
+                N, K, group_size, cu_count);
+  clear_error();
+  WqPlan pl;
+  wq_plan(qbits, M, N, K, qbits == 4 ? group_size : 1, act_dtype, scale_dtype, zero_dtype,
+          align_flags, cu_count, max_lds, &pl);
+  if (name && name_len) snprintf(name, name_len, "%s", pl.name);
+  if (grid) *grid = pl.grid;
+  if (block) *block = pl.block;
+  if (lds_bytes) *lds_bytes = pl.lds;
+  return 0;
+}
+
 namespace {
 // GPTQ / AWQ int4 checkpoints -> the int4 layout of tm_int4_matmul.
 int repack(bool awq, const void* qweight, const void* qzeros, const void* scales, int N, int K,
@@ -365,6 +396,48 @@ int tm_wq_dequant(const void* weight, const void* scales, const void* zeros, voi
   return launch(kernel("wq_dequant"), dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                 stream, (const uint8_t*)weight, scales, zeros, out, N, K, G, qbits, scale_dtype,
                 zero_dtype, out_dtype);
+}
+
+namespace {
+int matmul_dd(const char* op, const void* A, const void* B, void* C, const unsigned* Mp,
+              const unsigned* Np, const unsigned* Kp, int max_m, int max_n, int group_m,
+              int idt, int odt, void* stream) {
+  if (max_m < 0 || max_n < 0 || group_m < 0)
+    return fail(TM_ERR_INVALID_ARG, "%s: max_m=%d max_n=%d group=%d", op, max_m, max_n, group_m);
+  if (max_m == 0 || max_n == 0) return 0;
+  if (!A || !B || !C || !Mp || !Np || !Kp)
+    return fail(TM_ERR_INVALID_ARG, "%s: null buffer", op);
+  if (!is_float(idt) || !(odt == idt || odt == TM_DT_F32))
+    return fail(TM_ERR_INVALID_ARG, "%s: dtypes %s -> %s", op, dt_name(idt), dt_name(odt));
+  const long long ntr = (max_m + 63) / 64, ntc = (max_n + 63) / 64;
+  if (group_m == 0 ? ntr > 65535 : ntr * ntc > 0x7fffffffLL)
+    return fail(TM_ERR_UNSUPPORTED, "%s: capacity %d x %d", op, max_m, max_n);
+  if (!api()) return TM_ERR_NO_RUNTIME;
+  clear_error();
+  char name[64];
+  snprintf(name, sizeof name, "gemm_dd_%s_%s", dt_name(idt),
+           odt == idt ? "same" : "f32");
+  const dim3 grid = group_m == 0 ? dim3((unsigned)ntc, (unsigned)ntr)
+                                 : dim3((unsigned)(ntr * ntc));
+  return launch(kernel(name), grid, dim3(256), 0, stream, A, B, C, Mp, Np, Kp, max_m, max_n,
+                group_m);
+}
+}  // namespace
+
+int tm_matmul_2d(const void* A, const void* B, void* C, const unsigned* M, const unsigned* N,
+                 const unsigned* K, int max_m, int max_n, int in_dtype, int out_dtype,
+                 void* stream) {
+  return matmul_dd("tm_matmul_2d", A, B, C, M, N, K, max_m, max_n, 0, in_dtype, out_dtype,
+                   stream);
+}
+
+int tm_matmul_swizzled(const void* A, const void* B, void* C, const unsigned* M,
+                       const unsigned* N, const unsigned* K, int max_m, int max_n,
+                       int group_size, int in_dtype, int out_dtype, void* stream) {
+  if (group_size <= 0)
+    return fail(TM_ERR_INVALID_ARG, "tm_matmul_swizzled: group_size=%d", group_size);
+  return matmul_dd("tm_matmul_swizzled", A, B, C, M, N, K, max_m, max_n, group_size, in_dtype,
+                   out_dtype, stream);
 }
 
 int tm_matmul(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb,

@@ -75,15 +75,20 @@ TM_DEV u2_t tr16(const uint16_t* p) {
 
 // Eight fp32 values as hi + lo pairs of 16-bit operands: hi = round(f),
 // lo = round(f - hi) (f - hi is exact in fp32).
-template <bool BF16> TM_DEV void split_pack(const float* f, u4_t& hi, u4_t& lo) {
-  float r[8];
+template <bool BF16> TM_DEV void split_pack(const float* in, u4_t& hi, u4_t& lo) {
+  // fp16: hi saturates at the largest finite half, so lo carries what lies
+  // beyond 65504; |x| <= 131008 stays finite (larger values saturate there)
+  float f[8], r[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    r[e] = BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(f[e])) : f16_bits_to_f32(f32_to_f16_bits(f[e]));
+  for (int e = 0; e < 8; ++e) {
+    f[e] = BF16 ? in[e] : fminf(fmaxf(in[e], -131008.f), 131008.f);
+    const float h = BF16 ? f[e] : fminf(fmaxf(f[e], -65504.f), 65504.f);
+    r[e] = BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(h)) : f16_bits_to_f32(f32_to_f16_bits(h));
+  }
   uint32_t h[4], l[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    h[i] = BF16 ? pack_bf16x2(f[2 * i], f[2 * i + 1]) : pack_f16x2(f[2 * i], f[2 * i + 1]);
+    h[i] = BF16 ? pack_bf16x2(r[2 * i], r[2 * i + 1]) : pack_f16x2(r[2 * i], r[2 * i + 1]);
     const float d0 = f[2 * i] - r[2 * i], d1 = f[2 * i + 1] - r[2 * i + 1];
     l[i] = BF16 ? pack_bf16x2(d0, d1) : pack_f16x2(d0, d1);
   }

@@ -368,3 +368,104 @@ TM_GEMM_OUTS(true, nt, true, bf16, true, _bias)
   TM_GEMM_S32_OUTS(KW, true, nt, true, bf16, true, _bias)
 TM_GEMM_S32_ALL(64)
 TM_GEMM_S32_ALL(128)
+
+// ----------------------------------------------------------------------------
+// Matmul with its sizes in device memory: C[M, N] = A[M, K] @ B[K, N], all
+// row-major with leading dimensions K, N, N (make_matmul_2d_kernel,
+// _msl_templates.py:588-679, and make_matmul_swizzled_kernel, 682-781, which
+// read M, N, K from `device const uint*` buffers).  The grid covers a
+// host-known capacity (max_m x max_n); workgroups whose tile lies past the
+// sizes read on the device return at once, so one launch (or one captured
+// graph node) serves any M <= max_m, N <= max_n.
+//
+// 64 x 64 output tile per 256-thread workgroup, K in steps of 16 through LDS
+// ([k][row] fp32, so each thread's 4 x 4 outputs take 8 LDS reads per k),
+// fp32 accumulation, inputs fp32 / fp16 / bf16.  Tile order: group_m = 0 is
+// the 2-D grid (blockIdx.x -> tile column, blockIdx.y -> tile row);
+// group_m > 0 is the grouped order of the swizzled template on a 1-D grid -
+// runs of group_m tile rows, the tiles of one run taken column by column, so
+// that consecutive workgroups share B's columns.
+// ----------------------------------------------------------------------------
+template <int IDT, int ODT>
+__device__ __forceinline__ void gemm_dd_body(const void* __restrict__ A,
+                                             const void* __restrict__ B, void* __restrict__ C,
+                                             const unsigned* __restrict__ Mp,
+                                             const unsigned* __restrict__ Np,
+                                             const unsigned* __restrict__ Kp, int max_m,
+                                             int max_n, int group_m) {
+  __shared__ float As[16][64 + 4];
+  __shared__ float Bs[16][64 + 4];
+  const int M = (int)min(Mp[0], (unsigned)max_m), N = (int)min(Np[0], (unsigned)max_n);
+  const int K = (int)min(Kp[0], 0x7fffffffu);
+  const int ntr = (M + 63) / 64, ntc = (N + 63) / 64;
+  int tr, tc;
+  if (group_m <= 0) {
+    tc = blockIdx.x;
+    tr = blockIdx.y;
+  } else {
+    const long long pid = blockIdx.x;
+    if (pid >= (long long)ntr * ntc) return;
+    const long long per_group = (long long)group_m * ntc;
+    const int gid = (int)(pid / per_group);
+    const int first = gid * group_m;
+    const int rows = min(ntr - first, group_m);
+    const int in_group = (int)(pid - (long long)gid * per_group);
+    tr = first + in_group % rows;
+    tc = in_group / rows;
+  }
+  if (tr >= ntr || tc >= ntc) return;
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int m0 = tr * 64, n0 = tc * 64;
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  for (int k0 = 0; k0 < K; k0 += 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i;
+      const int r = e >> 4, kk = e & 15, gm = m0 + r, gk = k0 + kk;
+      As[kk][r] = (gm < M && gk < K) ? load_as_f32<IDT>(A, (size_t)gm * K + gk) : 0.0f;
+      const int kb = e >> 6, c = e & 63, gn = n0 + c, gkb = k0 + kb;
+      Bs[kb][c] = (gkb < K && gn < N) ? load_as_f32<IDT>(B, (size_t)gkb * N + gn) : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int gm = m0 + ty + 16 * i;
+    if (gm >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gn = n0 + tx + 16 * j;
+      if (gn < N) store_from_f32<ODT>(C, (size_t)gm * N + gn, acc[i][j]);
+    }
+  }
+}
+
+// gemm_dd_<in>_<out>: out "same" (the input dtype, as the templates) or f32
+#define TM_GEMM_DD(IN, IDT, OUT, ODT)                                                           \
+  extern "C" __global__ __launch_bounds__(256) void gemm_dd_##IN##_##OUT(                       \
+      const void* A, const void* B, void* C, const unsigned* Mp, const unsigned* Np,            \
+      const unsigned* Kp, int max_m, int max_n, int group_m) {                                  \
+    gemm_dd_body<IDT, ODT>(A, B, C, Mp, Np, Kp, max_m, max_n, group_m);                        \
+  }
+TM_GEMM_DD(f32, TM_DT_F32, same, TM_DT_F32)
+TM_GEMM_DD(f16, TM_DT_F16, same, TM_DT_F16)
+TM_GEMM_DD(f16, TM_DT_F16, f32, TM_DT_F32)
+TM_GEMM_DD(bf16, TM_DT_BF16, same, TM_DT_BF16)
+TM_GEMM_DD(bf16, TM_DT_BF16, f32, TM_DT_F32)

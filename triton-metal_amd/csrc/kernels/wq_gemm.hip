@@ -1623,10 +1623,12 @@ extern "C" __global__ __launch_bounds__(256) void wq_dequant(
 // Scales have the activation dtype; zero-points: n = none, s = scale dtype,
 // u = uint8.
 // ----------------------------------------------------------------------------
-#define TM_WQ_ATTR_skinny __attribute__((amdgpu_waves_per_eu(4)))
-#define TM_WQ_ATTR_tiled
+// skinny: int8 at 4 waves per SIMD (<= 128 VGPRs); int4 (more operand
+// registers per weight word) at 3 (<= 168 VGPRs), free of scratch spills.
+#define TM_WQ_ATTR_skinny(QB) __attribute__((amdgpu_waves_per_eu(QB == 4 ? 3 : 4)))
+#define TM_WQ_ATTR_tiled(QB)
 #define TM_WQ_INST(KIND, QB, BF, ACT, ZS, ZDT, SUF, ...)                                        \
-  extern "C" __global__ __launch_bounds__(256) TM_WQ_ATTR_##KIND void                           \
+  extern "C" __global__ __launch_bounds__(256) TM_WQ_ATTR_##KIND(QB) void                       \
       wq_##KIND##_q##QB##_##ACT##_z##ZS##SUF(const uint16_t* X, const uint8_t* W, uint16_t* Y,   \
                                              const void* S, const void* Z, int M, int N, int K,  \
                                              int G, const uint16_t* bias) {                       \
@@ -1684,13 +1686,11 @@ TM_STREAM_Z(4, true, bf16, 4)
 TM_STREAM_Z(8, false, f16, 3)
 TM_STREAM_Z(8, true, bf16, 3)
 
-// GEMV (int4, exact K = NW * PF * 128, G = 128): wq_gemv4_<act>_z<zs>_w<NW>p<PF>
-// Occupancy of the K = 4096 variant: 8 waves per SIMD (<= 64 VGPRs), so that
-// a whole N = 14336 grid (896 workgroups of 8 waves) is resident at once
-// instead of leaving a second, partial round of workgroups.
+// GEMV (int4, exact K = NW * PF * 128, G = 128): wq_gemv4_<act>_z<zs>_w<NW>p<PF>.
+// Instantiated for K = 8192 (2 <= M <= 8); at K = 4096 the two-tile GEMV and
+// the streaming kernel cover the same rows.
 #define TM_GEMV4(BF, ACT, ZS, ZDT, NW, PF)                                                     \
   extern "C" __global__ __launch_bounds__(NW * 64)                                              \
-  __attribute__((amdgpu_waves_per_eu(NW == 8 && PF == 4 ? 8 : 1)))                             \
   void wq_gemv4_##ACT##_z##ZS##_w##NW##p##PF(                                                   \
       const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S, const void* Z, int M, \
       int N, int K, const uint16_t* bias) {                                                     \
@@ -1700,16 +1700,15 @@ TM_STREAM_Z(8, true, bf16, 3)
   TM_GEMV4(BF, ACT, n, -1, NW, PF)                                    \
   TM_GEMV4(BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), NW, PF)         \
   TM_GEMV4(BF, ACT, u, 3, NW, PF)
-TM_GEMV4_Z(false, f16, 8, 4)
-TM_GEMV4_Z(true, bf16, 8, 4)
-TM_GEMV4_Z(false, f16, 4, 8)
-TM_GEMV4_Z(true, bf16, 4, 8)
 TM_GEMV4_Z(false, f16, 8, 8)
 TM_GEMV4_Z(true, bf16, 8, 8)
 
 // Linear GEMV (int4, M = 1, K = 2048 * NS, G = 128): wq_gemv4l_<act>_z<zs>_k<NS>
+// K = 4096: 8 waves per SIMD (<= 64 VGPRs); K = 8192 holds twice the rows per
+// wave and runs at 4 (<= 128 VGPRs), which keeps it free of scratch spills.
 #define TM_GEMV4L(BF, ACT, ZS, ZDT, NS)                                                         \
-  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8))) void     \
+  extern "C" __global__ __launch_bounds__(512)                                                  \
+  __attribute__((amdgpu_waves_per_eu(NS == 4 ? 4 : 8))) void                                    \
       wq_gemv4l_##ACT##_z##ZS##_k##NS(const uint16_t* X, const uint8_t* W, uint16_t* Y,         \
                                       const uint16_t* S, const void* Z, int M, int N, int K,    \
                                       const uint16_t* bias) {                                   \
@@ -1740,8 +1739,9 @@ TM_GEMV4L_Z(true, bf16, 4)
 TM_GEMV4XN_Z(false, f16, 2, 4)
 TM_GEMV4XN_Z(true, bf16, 2, 4)
 
-// int8 GEMV (K = 4096): wq_gemv8_<act>_z<zs>_w8p8; 8 waves per SIMD (<= 64
-// VGPRs), so the whole grid is resident.
+// int8 GEMV (K = 4096, bf16 activations; fp16 runs on the linear int8 GEMV):
+// wq_gemv8_<act>_z<zs>_w8p8; 8 waves per SIMD (<= 64 VGPRs), so the whole
+// grid is resident.
 #define TM_GEMV8(BF, ACT, ZS, ZDT)                                                              \
   extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(8))) void     \
       wq_gemv8_##ACT##_z##ZS##_w8p8(const uint16_t* X, const uint8_t* W, uint16_t* Y,           \
@@ -1753,7 +1753,6 @@ TM_GEMV4XN_Z(true, bf16, 2, 4)
   TM_GEMV8(BF, ACT, n, -1)                               \
   TM_GEMV8(BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16))    \
   TM_GEMV8(BF, ACT, u, 3)
-TM_GEMV8_Z(false, f16)
 TM_GEMV8_Z(true, bf16)
 
 // Linear int8 GEMV (M = 1, K = 4096, fp16): wq_gemv8l_f16_z<zs>

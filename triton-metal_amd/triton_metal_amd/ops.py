@@ -189,6 +189,26 @@ def plan_int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size=1
     return Launch(_lib.lib().tm_int4_matmul, args, "int4_matmul", dev, stream)
 
 
+def wq_kernel_for(qbits, M, N, K, group_size=128, act_dtype=torch.float16, scale_dtype=None,
+                  zero_dtype=None, align=_lib.TM_WQ_ALIGN_ALL, cu_count=256,
+                  max_lds=160 * 1024):
+    """Name, grid, block and dynamic LDS bytes of the kernel that an int4 /
+    int8 matmul of these sizes and dtypes runs (tm_wq_plan; no device is
+    touched).  ``zero_dtype`` is a torch dtype or None (no zero-points);
+    ``align`` the TM_WQ_ALIGN_* bits of the call's pointers; the defaults
+    describe torch allocations on one MI355X."""
+    dts = {None: TM_DT_NONE, torch.uint8: _lib.TM_DT_U8, **_FLOAT_DT}
+    adt = dts[act_dtype]
+    sdt = dts[scale_dtype if scale_dtype is not None else act_dtype]
+    name = C.create_string_buffer(64)
+    grid, block, lds = C.c_uint(), C.c_uint(), C.c_uint()
+    rc = _lib.lib().tm_wq_plan(qbits, M, N, K, group_size, adt, sdt, dts[zero_dtype], align,
+                               cu_count, max_lds, name, 64, C.byref(grid), C.byref(block),
+                               C.byref(lds))
+    _lib.check(rc, "wq_kernel_for")
+    return name.value.decode(), grid.value, block.value, lds.value
+
+
 def int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size=128):
     """output[M,N] = input[M,K] @ dequant(weight)^T with per-group scale/zero.
 
@@ -347,6 +367,111 @@ def matmul(A, B, C, M, N, K):
     return C
 
 
+_TEMPLATE_DT = {"fp32": torch.float32, "f32": torch.float32, "fp16": torch.float16,
+                "f16": torch.float16, "bf16": torch.bfloat16}
+
+
+def _size_arg(v, dev, what):
+    """A size of the device-sizes matmul: a uint32 / int32 device tensor (the
+    template's `device const uint*` buffer; its first element is read) or a
+    Python int (written to a new one-element device tensor).  Returns the
+    tensor and the value when it is known on the host (None otherwise)."""
+    if isinstance(v, int):
+        if v < 0:
+            raise ValueError(f"{what}={v}")
+        return torch.tensor([v], dtype=torch.int32, device=dev), v
+    if not isinstance(v, torch.Tensor) or v.dtype not in (torch.int32, torch.uint32):
+        raise TypeError(f"{what} must be an int or a uint32 / int32 device tensor")
+    if v.device != dev or v.numel() < 1:
+        raise ValueError(f"{what} must be a non-empty tensor on {dev}")
+    return v, None
+
+
+def plan_matmul_device_sizes(A, B, C, M_buf, N_buf, K_buf, max_m=None, max_n=None,
+                             group_size=0, stream=None) -> Launch:
+    """Validate and bind a matmul whose sizes live in device memory (see
+    matmul_device_sizes)."""
+    dev = _device_of(A, B, C)
+    for t, w in ((A, "A"), (B, "B"), (C, "C")):
+        _need_contig(t, w)
+    if A.dtype != B.dtype:
+        raise TypeError("A and B must share a dtype")
+    if C.dtype not in (A.dtype, torch.float32):
+        raise TypeError(f"C must be {A.dtype} or float32, got {C.dtype}")
+    (mb, m), (nb, n), (kb, k) = (_size_arg(M_buf, dev, "M"), _size_arg(N_buf, dev, "N"),
+                                 _size_arg(K_buf, dev, "K"))
+    if max_m is None or max_n is None:
+        # the capacity is the sizes themselves: read them (a synchronising copy
+        # for device tensors)
+        m = int(mb[0].item()) if m is None else m
+        n = int(nb[0].item()) if n is None else n
+        k = int(kb[0].item()) if k is None else k
+        max_m = m if max_m is None else max_m
+        max_n = n if max_n is None else max_n
+    if m is not None and n is not None and k is not None:
+        _numel_at_least(A, m * k, "A")
+        _numel_at_least(B, k * n, "B")
+        _numel_at_least(C, min(m, max_m) * min(n, max_n), "C")
+    else:
+        _numel_at_least(C, max_m * max_n, "C")
+    args = (_ptr(A), _ptr(B), _ptr(C), _ptr(mb), _ptr(nb), _ptr(kb), int(max_m), int(max_n))
+    if group_size:
+        f, args = _lib.lib().tm_matmul_swizzled, args + (int(group_size),)
+    else:
+        f = _lib.lib().tm_matmul_2d
+    args += (_dt(A, "A"), _dt(C, "C"))
+    launch = Launch(f, args, "matmul_swizzled" if group_size else "matmul_2d", dev, stream)
+    launch._keep = (mb, nb, kb)
+    return launch
+
+
+def matmul_device_sizes(A, B, C, M_buf, N_buf, K_buf, max_m=None, max_n=None, group_size=0):
+    """C[M,N] = A[M,K] @ B[K,N] with M, N, K read on the device: the buffer
+    order of make_matmul_2d_kernel / make_matmul_swizzled_kernel
+    (_msl_templates.py:588-781; A, B, C, M_buf, N_buf, K_buf, row-major with
+    leading dimensions K, N, N).  The sizes are one-element uint32 / int32
+    device tensors or ints.  max_m / max_n bound the launch (sizes read on the
+    device are clamped to them; C must then hold max_m * max_n elements);
+    left out, they are the sizes themselves, read with one synchronising copy.
+    group_size 0 walks the output tiles on a 2-D grid, > 0 in runs of that many
+    tile rows (the swizzled template's grouped order).  fp32 accumulation; C is
+    A's dtype or float32."""
+    _run(plan_matmul_device_sizes(A, B, C, M_buf, N_buf, K_buf, max_m, max_n, group_size))
+    return C
+
+
+def _check_template_dtype(A, dtype):
+    want = _TEMPLATE_DT.get(dtype)
+    if want is None:
+        raise ValueError(f"dtype must be one of {sorted(_TEMPLATE_DT)}, got {dtype!r}")
+    if A.dtype != want:
+        raise TypeError(f"kernel built for {dtype}, got {A.dtype} inputs")
+
+
+def make_matmul_2d_kernel(block_m=32, block_n=32, block_k=32, dtype="fp32"):
+    """The 2-D-dispatch matmul template (_msl_templates.py:588-679): call with
+    (A, B, C, M_buf, N_buf, K_buf[, max_m, max_n]).  Tile sizes are the
+    library's; the arguments are kept for the reference signature."""
+    def run(A, B, C, M_buf, N_buf, K_buf, max_m=None, max_n=None):
+        _check_template_dtype(A, dtype)
+        return matmul_device_sizes(A, B, C, M_buf, N_buf, K_buf, max_m, max_n, 0)
+    return Kernel("matmul_2d", run, {"dtype": dtype})
+
+
+def make_matmul_swizzled_kernel(block_m=32, block_n=32, block_k=32, group_size=4,
+                                dtype="fp32"):
+    """The grouped-order matmul template (_msl_templates.py:682-781): call with
+    (A, B, C, M_buf, N_buf, K_buf[, max_m, max_n]); runs of group_size tile
+    rows.  Tile sizes are the library's."""
+    if group_size <= 0:
+        raise ValueError(f"group_size must be positive, got {group_size}")
+
+    def run(A, B, C, M_buf, N_buf, K_buf, max_m=None, max_n=None):
+        _check_template_dtype(A, dtype)
+        return matmul_device_sizes(A, B, C, M_buf, N_buf, K_buf, max_m, max_n, group_size)
+    return Kernel("matmul_swizzled", run, {"dtype": dtype, "group_size": group_size})
+
+
 def fused_linear(input, weight, C, bias, M, N, K):
     """C[M,N] = input[M,K] @ weight[N,K]^T (+ bias[N]).
 
@@ -416,9 +541,11 @@ def plan_dot(a, b, c, epilogue="none", z=None, w=None, fp8_format=None, stream=N
     for nb, what in ((ba, "a"), (bb, "b"), (bc, "c")):
         if nb not in (1, batch) or (nb == 1 and what == "c" and batch > 1):
             raise ValueError(f"{what}: batch {nb} does not match {batch}")
-    if ba == 1 and a.dim() == 2:
+    # an operand with batch 1 is broadcast over the batch: its batch stride is
+    # zero whether it is a 2-D view or a 3-D [1, ., .] view
+    if ba == 1:
         sa = (0,) + sa[1:]
-    if bb == 1 and b.dim() == 2:
+    if bb == 1:
         sb = (0,) + sb[1:]
     idt = _in_dt(a, "a", fp8_format)
     if _in_dt(b, "b", fp8_format) != idt:
@@ -562,18 +689,49 @@ def flash_attn_fwd(Q, K, V, Out,
     (line 54).  BLOCK_M / BLOCK_N are accepted for signature compatibility;
     the library picks its own tiles."""
     D = HEAD_DIM if HEAD_DIM is not None else Q.shape[-1]
-    if stride_qk != 1 or stride_kk != 1 or stride_vk != 1 or stride_ok != 1:
-        raise ValueError("the head dimension must be contiguous (stride_*k == 1)")
 
-    def view(t, sz, sh, sm):
-        return torch.as_strided(t, (Z, H, N_CTX, D), (sz, sh, sm, 1), t.storage_offset())
+    def view(t, sz, sh, sm, sk):
+        return torch.as_strided(t, (Z, H, N_CTX, D), (sz, sh, sm, sk), t.storage_offset())
 
-    q = view(Q, stride_qz, stride_qh, stride_qm)
-    k = view(K, stride_kz, stride_kh, stride_kn)
-    v = view(V, stride_vz, stride_vh, stride_vn)
-    o = view(Out, stride_oz, stride_oh, stride_om)
-    _run(plan_flash_attention(q, k, v, o, lse=lse, causal=IS_CAUSAL,
-                              scale=1.0 / math.sqrt(D)))
+    q = view(Q, stride_qz, stride_qh, stride_qm, stride_qk)
+    k = view(K, stride_kz, stride_kh, stride_kn, stride_kk)
+    v = view(V, stride_vz, stride_vh, stride_vn, stride_vk)
+    o = view(Out, stride_oz, stride_oh, stride_om, stride_ok)
+    _attention_any_strides(q, k, v, o, 1.0 / math.sqrt(D), IS_CAUSAL, lse)
+    return Out
+
+
+def _attention_any_strides(q, k, v, o, scale, causal, lse=None):
+    """Flash attention on [B, H, S, D] views whose head dimension may be
+    strided: the kernels read rows of contiguous head elements, so a view with
+    a head-dimension stride other than 1 goes through a contiguous device
+    copy (and the output comes back through a strided device copy)."""
+    qc, kc, vc = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    if o.stride(-1) == 1:
+        _run(plan_flash_attention(qc, kc, vc, o, lse=lse, causal=causal, scale=scale))
+    else:
+        oc = torch.empty(o.shape, dtype=o.dtype, device=o.device)
+        _run(plan_flash_attention(qc, kc, vc, oc, lse=lse, causal=causal, scale=scale))
+        o.copy_(oc)
+    return o
+
+
+def fa_fwd_strided(Q, K, V, Out, stride_qm, stride_qk, stride_kn, stride_kk, stride_vn,
+                   stride_vk, stride_om, stride_ok, sm_scale, N_CTX, HEAD_DIM, BLOCK_M=None,
+                   BLOCK_N=None):
+    """The signature of the reference's second FlashAttention kernel,
+    _fa_fwd_strided_kernel (tests/test_cpp_backend.py:567-576): one head of
+    N_CTX queries and keys, [N_CTX, HEAD_DIM] with a row and a head-dimension
+    stride per tensor, softmax scale sm_scale, no causal mask.  BLOCK_M /
+    BLOCK_N are accepted for the signature; the library picks its own tiles."""
+    D = HEAD_DIM
+
+    def view(t, sm, sk):
+        return torch.as_strided(t, (1, 1, N_CTX, D), (0, 0, sm, sk), t.storage_offset())
+
+    _attention_any_strides(view(Q, stride_qm, stride_qk), view(K, stride_kn, stride_kk),
+                           view(V, stride_vn, stride_vk), view(Out, stride_om, stride_ok),
+                           float(sm_scale), False)
     return Out
 
 
