@@ -257,8 +257,62 @@ def hbm_copy(dev, nbytes=512 << 20):
                                       "bytes_written": nbytes})
 
 
+def w4a16_read_twin(dev, weights_only=False, K=4096, N=14336, G=128):
+    """The headline GEMV's pure-read twin (wq_read_twin_r14, wq_gemvp.hip): the
+    same grid of 256 workgroups x 56 rows and the same weight loads, plus the
+    scale and zero-point rows (or the weights alone), reduced to nothing - the
+    time that streaming the GEMV's bytes with its grid takes by itself.  Bytes:
+    what it reads.  Weight sets rotated as the headline."""
+    import torch
+    from triton_metal_amd.driver import HipUtils
+    ng = K // G
+    rw = 14
+    per = N * K // 2 + 2 * N * ng * 2
+    R = _nsets(per)
+    g = torch.Generator(device=dev).manual_seed(2)
+    Ws = [torch.randint(0, 256, (N, K // 2), device=dev, dtype=torch.uint8, generator=g)
+          for _ in range(R)]
+    Ss = [(torch.rand(N, ng, device=dev, generator=g) * 0.019 + 0.001).half() for _ in range(R)]
+    Zs = [torch.randint(0, 16, (N, ng), device=dev, generator=g).half() for _ in range(R)]
+    grid = -(-N // (4 * rw))
+    sink = torch.zeros(grid, device=dev, dtype=torch.int32)
+    hu = HipUtils()
+    name = f"wq_read_twin_{'w_' if weights_only else ''}r{rw}"
+    fn = hu.builtin_function(name, dev)
+
+    class Twin:
+        def __init__(self, j):
+            self.j = j
+
+        def __call__(self, stream=None):
+            hu.launch(fn, (grid,), (512,), [Ws[self.j], Ss[self.j], Zs[self.j], sink, N], 0,
+                      stream)
+    nbytes = N * K // 2 + (0 if weights_only else 2 * N * ng * 2)
+    return dict(launches=[Twin(j) for j in range(R)], keep=(Ws, Ss, Zs, sink), bytes=nbytes,
+                flops=0, bound="hbm", dtype="u8",
+                config={"workload": "w4a16_m1_read_twin" + ("_w" if weights_only else ""),
+                        "kernel": name, "grid": grid, "rows_per_workgroup": 4 * rw, "K": K,
+                        "N": N, "weight_sets_rotated": R})
+
+
+def w4a16_wide_k(dev, M, K=14336, N=4096, G=128):
+    """A W4A16 shape off the bench configurations: the down projection
+    (K = 14336 -> N = 4096) of the same model family, M = 1 or 16, to measure
+    the kernels that shapes other than K = 4096 reach."""
+    import torch
+    import triton_metal_amd as tm
+    w = w4a16(dev, M, K=K, N=N, G=G)
+    w["config"]["workload"] = f"w4a16_m{M}_k{K}"
+    w["config"]["kernel"] = tm.wq_kernel_for(4, M, N, K, G, zero_dtype=torch.float16)[0]
+    return w
+
+
 # opt-in workloads (--only NAME), not part of the default run
-EXTRA = {"hbm_copy": hbm_copy}
+EXTRA = {"hbm_copy": hbm_copy,
+         "w4a16_m1_read_twin": lambda d: w4a16_read_twin(d),
+         "w4a16_m1_read_twin_w": lambda d: w4a16_read_twin(d, weights_only=True),
+         "w4a16_m1_k14336": lambda d: w4a16_wide_k(d, 1),
+         "w4a16_m16_k14336": lambda d: w4a16_wide_k(d, 16)}
 
 
 def time_workload(w, steps, warmup, graph=True, budget_s=2.0, min_replays=100):

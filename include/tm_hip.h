@@ -90,6 +90,12 @@ int tm_module_unload(tm_module_t module);
  * (private segment bytes per lane) and n_max_threads.  NULL outs ignored. */
 int tm_module_get_function(tm_module_t module, const char* name, tm_function_t* out,
                            int* n_regs, int* n_spills, int* max_threads, int* shared_bytes);
+/* A kernel of the library's own embedded code objects by name, resolved on
+ * the current device (loading them there on first use), for launching with
+ * tm_launch: the built-in counterpart of tm_module_get_function, as
+ * MetalUtils.load_binary (triton_metal/backend/driver.py:114-162) returns a
+ * function from a compiled library. */
+int tm_builtin_get_function(const char* name, tm_function_t* out);
 /* Launch with kernel arguments as an array of pointers to each argument
  * (hipModuleLaunchKernel's kernelParams convention). */
 int tm_launch(tm_function_t fn, unsigned grid_x, unsigned grid_y, unsigned grid_z,

@@ -9,6 +9,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <vector>
 
 // Code objects embedded by embed.S (generated at build time): for each
@@ -265,6 +266,26 @@ const char* tm_last_error(void) { return g_err.c_str(); }
 const char* tm_version(void) { return "tm_hip 0.1 (gfx950)"; }
 
 int tm_num_builtin_modules(void) { return kNumModules; }
+
+int tm_builtin_get_function(const char* name, tm_function_t* out) {
+  if (!name || !out) return fail(TM_ERR_INVALID_ARG, "tm_builtin_get_function: null argument");
+  if (!api()) return TM_ERR_NO_RUNTIME;
+  clear_error();
+  static std::mutex mu;
+  static std::map<std::string, Kernel*> table;
+  Kernel* k;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = table.find(name);
+    if (it == table.end()) it = table.emplace(name, new Kernel(strdup(name))).first;
+    k = it->second;
+  }
+  hipFunction_t f = nullptr;
+  const int rc = k->get(&f);
+  if (rc) return rc;
+  *out = (tm_function_t)f;
+  return 0;
+}
 
 const char* tm_builtin_module_name(int i) {
   return (i >= 0 && i < kNumModules) ? kModules[i].name : nullptr;

@@ -185,3 +185,61 @@ TM_GEMV4P_RW(11)
 TM_GEMV4P_RW(12)
 TM_GEMV4P_RW(14)
 TM_GEMV4P_RW(16)
+
+// ----------------------------------------------------------------------------
+// Pure-read twin of wq_gemv4p (a measurement kernel, not part of any matmul):
+// the same grid, the same rows per workgroup and the same weight loads (1 KB
+// of one row per instruction, non-temporal, RW / 2 + 1 rows first and the rest
+// after two rows), plus (SZ) the workgroup's scale and zero-point rows read
+// contiguously, 16 bytes per lane.  The words read are XOR-reduced and
+// written only if the reduction equals a fixed value, so the reads cannot be
+// dropped and nothing is written for any ordinary data.  Its time per call
+// is the floor that streaming these bytes with this grid sets under the GEMV.
+// Arguments: W [N, 2048] bytes, S and Z [N, 32] 16-bit, sink uint32 [grid].
+// ----------------------------------------------------------------------------
+template <int RW, bool SZ>
+__device__ __forceinline__ void wq_read_twin_body(const uint8_t* __restrict__ W,
+                                                  const uint16_t* __restrict__ S,
+                                                  const uint16_t* __restrict__ Z,
+                                                  uint32_t* __restrict__ sink, int N) {
+  constexpr int K = 4096, RB = K / 2, NG = K / 128;
+  constexpr int R1 = RW / 2 + 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = wave >> 2, ws = wave & 3;
+  const int n0 = min((int)blockIdx.x * 4 * RW, N - 4 * RW), r0 = n0 + RW * ws;
+  uint32_t acc = 0;
+  if constexpr (SZ) {
+    // 4 RW rows x 64 B of scales and of zero-points
+    if (tid < 16 * RW) {
+      const u4_t a = ldg128(S + (size_t)n0 * NG + 8 * tid);
+      const u4_t b = ldg128(Z + (size_t)n0 * NG + 8 * tid);
+      acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w;
+    }
+  }
+  const uint8_t* wb = W + (size_t)r0 * RB + 1024 * h + 16 * lane;
+  u4_t wv[RW];
+#pragma unroll
+  for (int i = 0; i < R1; ++i) wv[i] = __builtin_nontemporal_load((const u4_t*)(wb + (size_t)i * RB));
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    if (i == 2) {
+#pragma unroll
+      for (int i2 = R1; i2 < RW; ++i2)
+        wv[i2] = __builtin_nontemporal_load((const u4_t*)(wb + (size_t)i2 * RB));
+    }
+    acc ^= wv[i].x ^ wv[i].y ^ wv[i].z ^ wv[i].w;
+  }
+  if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+// wq_read_twin_r<RW> (weights, scales, zero-points), wq_read_twin_w_r<RW>
+// (weights only)
+#define TM_READ_TWIN(RW)                                                                        \
+  extern "C" __global__ __launch_bounds__(512) void wq_read_twin_r##RW(                         \
+      const uint8_t* W, const uint16_t* S, const uint16_t* Z, uint32_t* sink, int N) {          \
+    wq_read_twin_body<RW, true>(W, S, Z, sink, N);                                              \
+  }                                                                                             \
+  extern "C" __global__ __launch_bounds__(512) void wq_read_twin_w_r##RW(                       \
+      const uint8_t* W, const uint16_t* S, const uint16_t* Z, uint32_t* sink, int N) {          \
+    wq_read_twin_body<RW, false>(W, S, Z, sink, N);                                             \
+  }
+TM_READ_TWIN(14)

@@ -38,6 +38,7 @@ SIGNATURES = {
     "tm_module_unload": [vp],
     "tm_module_get_function": [vp, C.c_char_p, C.POINTER(vp), C.POINTER(i32), C.POINTER(i32),
                                C.POINTER(i32), C.POINTER(i32)],
+    "tm_builtin_get_function": [C.c_char_p, C.POINTER(vp)],
     "tm_launch": [vp, u32, u32, u32, u32, u32, u32, u32, vp, C.POINTER(vp)],
     "tm_synchronize": [vp],
     "tm_int8_matmul": [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp],

@@ -53,6 +53,16 @@ class HipUtils:
                                       f"{_lib.last_error()}", code=rc)
         return mod, fn, regs.value, spills.value, maxt.value
 
+    def builtin_function(self, name, device=None):
+        """A kernel of the library's embedded code objects by name (resolved
+        on ``device`` or the current device), for ``launch``."""
+        fn = C.c_void_p()
+        with _device_ctx(device):
+            rc = self._lib.tm_builtin_get_function(name.encode(), C.byref(fn))
+        if rc:
+            raise KernelLoadError(f"built-in kernel '{name}': {_lib.last_error()}", code=rc)
+        return fn
+
     def unload(self, module):
         _lib.check(self._lib.tm_module_unload(module), "tm_module_unload")
 
