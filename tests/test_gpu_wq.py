@@ -529,8 +529,13 @@ def test_dispatch_case(dev, cu_count, case):
     out = torch.empty(M, N, dtype=act, device=dev)
     cols = _cols(N) if N > 2048 else np.arange(N)
     if qbits == 4:
-        zk = {None: None, "s": "f16", "u8": "u8"}[zeros]
-        x, q, packed, s, z = make_int4_problem(M, N, K, G, seed=seed, act=act, zeros=zk)
+        g = _gen(seed)
+        x = torch.randn(M, K, generator=g).to(act)
+        packed = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
+        ng = (K + G - 1) // G
+        s = (torch.rand(N, ng, generator=g) * 0.019 + 0.001).to(act)
+        zi = torch.randint(0, 16, (N, ng), generator=g)
+        z = None if zeros is None else zi.to(torch.uint8 if zeros == "u8" else act)
         args = (packed.to(dev), out, s.to(dev), None if z is None else z.to(dev), M, N, K, G)
         if use_bias:
             tm.int4_linear(x.to(dev), args[0], bias.to(dev), *args[1:])

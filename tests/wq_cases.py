@@ -30,17 +30,26 @@ for M, K in ((8, 1024), (12, 2048), (40, 512)):
 # persistent int4 GEMV, M = 1, K = 4096: one N per rows-per-wave count
 for N in (1024, 7168, 8192, 11264, 12288, 14336, 16384):
     CASES += _each(4, 1, N, 4096)
-# linear int4 GEMV: K = 4096 past the persistent kernel's reach (N > 16384 on
-# 256 CUs, e.g. a fused gate/up projection), and K = 8192
+# persistent int4 GEMV for other K: KS segments of 2048 k (the last one
+# partial for K = 1536, 2176, 9216, 11008) and RG row groups; per KS one N per
+# rows-per-wave count (4, 8, 16), the last workgroup shifted back (N not a
+# multiple of the workgroup's rows)
+GEMV4K = {1: (1536, 8), 2: (2176, 4), 3: (6144, 4), 4: (8192, 4), 5: (9216, 3),
+          6: (11008, 2), 7: (14336, 2), 8: (16384, 2)}  # KS: (K, RG)
+for ks, (K, rg) in GEMV4K.items():
+    for N in (1024 * rg - 48, 2048 * rg - 32, 4096 * rg - 16):
+        CASES += _each(4, 1, N, K)
+# linear int4 GEMV: K = 4096 / 8192 past the persistent kernels' reach (N >
+# 16384 / 16384 on 256 CUs, e.g. a fused gate/up projection)
 CASES += _each(4, 1, 16400, 4096)
 CASES += _each(4, 1, 28672, 4096, acts=(torch.float16,))
-CASES += _each(4, 1, 64, 8192)
+CASES += _each(4, 1, 16400, 8192)
 # int4 GEMV at K = 8192, 2 <= M <= 8
 CASES += _each(4, 4, 64, 8192)
 # int8 GEMVs, M = 1, K = 4096: linear (fp16) and 8-wave (bf16)
 CASES += _each(8, 1, 64, 4096)
 # skinny (M <= 8, other K): int4 without and with vector scale loads, int8
-CASES += _each(4, 1, 64, 1024)
+CASES += _each(4, 2, 64, 5120)
 CASES += _each(4, 2, 64, 12288)
 CASES += _each(8, 1, 64, 1024)
 # tiled (K past the streaming kernel's 4096, M > 8)

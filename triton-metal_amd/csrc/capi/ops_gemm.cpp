@@ -124,8 +124,23 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
       }
     }
   }
-  // linear int4 GEMV: M = 1, G = 128, K = 4096 (N past the persistent
-  // kernel's reach) or 8192 (VALU dot products, 1 KB of one row per load)
+  // persistent int4 GEMV for other K (K % 128 == 0, K <= 16384): KS segments
+  // of 2048 k x RG row groups of RW rows, the smallest RW that keeps the grid
+  // within the CUs
+  if (fast && qbits == 4 && M == 1 && G == 128 && K != 4096 && K % 128 == 0 && K <= 16384) {
+    const int ks = (K + 2047) / 2048;
+    const int rg = ks == 1 ? 8 : std::min(4, 16 / ks);
+    static const int kRWk[] = {4, 8, 16};
+    for (int rw : kRWk) {
+      const int rows = rg * rw, grid = (N + rows - 1) / rows;
+      if (N >= rows && grid <= cus) {
+        snprintf(pl->name, sizeof pl->name, "wq_gemv4k_%s_z%c_s%d_r%d", act, zc, ks, rw);
+        return set(grid, 64 * ks * rg, 0, WQ_ARGS_STD);
+      }
+    }
+  }
+  // linear int4 GEMV: M = 1, G = 128, K = 4096 or 8192 with N past the
+  // persistent kernels' reach (VALU dot products, 1 KB of one row per load)
   if (fast && qbits == 4 && M == 1 && G == 128 && (K == 4096 || K == 8192)) {
     snprintf(pl->name, sizeof pl->name, "wq_gemv4l_%s_z%c_k%d", act, zc, K / 2048);
     return set(N / 16, 512, 0, WQ_ARGS_STD);

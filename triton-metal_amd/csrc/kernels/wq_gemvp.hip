@@ -55,31 +55,45 @@ TM_DEV float sum_bits01(float v) {
 
 }  // namespace
 
-// RW rows per wave (4 <= RW <= 16).  Preconditions (host-checked): K = 4096,
-// G = 128, 512 threads, gridDim.x = ceil(N / (4 RW)), N >= 4 RW; X, W 16-byte
-// aligned.  The last workgroup is shifted back to end at row N: it recomputes
-// rows of its neighbour and writes the same values.
-template <bool BF16, int ZDT, int RW>
+// RW rows per wave (4 <= RW <= 16); the row's K in KS segments of 2048 k (1 KB
+// of weights: one 16-byte load per lane), the last one partial when K <
+// 2048 KS; RG groups of RW rows; KS x RG waves.  Wave w takes segment
+// s = w / RG of rows RW (w % RG) .. + RW - 1 (for K = 4096: the two K halves
+// of 4 row groups, 512 threads).  Preconditions (host-checked): K % 128 == 0,
+// 2048 (KS - 1) < K <= 2048 KS, G = 128, 64 KS RG threads, gridDim.x =
+// ceil(N / (RG RW)), N >= RG RW; X, W 16-byte aligned.  The last workgroup is
+// shifted back to end at row N: it recomputes rows of its neighbour and writes
+// the same values.  EXACT: K == 2048 KS as a compile-time constant.
+template <bool BF16, int ZDT, int RW, int KS, int RG, bool EXACT>
 __device__ __forceinline__ void wq_gemv4p_body(const uint16_t* __restrict__ X,
                                                const uint8_t* __restrict__ W,
                                                uint16_t* __restrict__ Y,
                                                const uint16_t* __restrict__ S,
-                                               const void* __restrict__ Z, int N,
+                                               const void* __restrict__ Z, int N, int Kr,
                                                const uint16_t* bias) {
   static_assert(RW >= 4 && RW <= 16, "rows per wave");
-  constexpr int K = 4096, RB = K / 2, NG = K / 128;
+  static_assert(KS * RG <= 16, "at most 16 waves");
+  const int K = EXACT ? 2048 * KS : Kr;
+  const int RB = K / 2, NG = K / 128;
   constexpr int SDT = BF16 ? TM_DT_BF16 : TM_DT_F16;
   constexpr int R1 = RW / 2 + 1;  // rows issued before the first dot products
-  __shared__ float red[2][4 * RW];
+  constexpr int NR = RG * RW;     // rows per workgroup
+  __shared__ float red[KS][NR];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = wave >> 2, ws = wave & 3;
-  const int n0 = min((int)blockIdx.x * 4 * RW, N - 4 * RW), r0 = n0 + RW * ws;
+  const int h = wave / RG, ws = wave % RG;
+  const int n0 = min((int)blockIdx.x * NR, N - NR), r0 = n0 + RW * ws;
   const int g = 16 * h + (lane >> 2);  // the quantisation group of the lane's 32 k
+  // lanes past the end of a partial last segment hold no k (whole groups:
+  // K % 128 == 0); they read nothing and contribute zeros
+  const bool live = EXACT || h < KS - 1 || 2048 * h + 32 * lane < K;
 
   // X first (L2), then the scales / zero-points, then the weights (HBM)
   u4_t xr[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) xr[j] = ldg128(X + 2048 * h + 32 * lane + 8 * j);
+  for (int j = 0; j < 4; ++j) {
+    xr[j] = u4_t{0u, 0u, 0u, 0u};
+    if (live) xr[j] = ldg128(X + 2048 * h + 32 * lane + 8 * j);
+  }
   // scales / zero-points of the 4 rows this lane scales after the first two
   // fold stages: rows 8 b0 + 4 b1 + m (b0, b1 = lane bits 0, 1), group g
   const int rq = 8 * (lane & 1) + 4 * ((lane >> 1) & 1);
@@ -87,14 +101,21 @@ __device__ __forceinline__ void wq_gemv4p_body(const uint16_t* __restrict__ X,
   typename Raw<ZDT>::T zraw[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const size_t gi = (size_t)(r0 + min(rq + m, RW - 1)) * NG + g;
-    sraw[m] = ld_raw<SDT>(S, gi);
-    zraw[m] = ld_raw<ZDT>(Z, gi);
+    sraw[m] = 0;
+    zraw[m] = 0;
+    if (live) {
+      const size_t gi = (size_t)(r0 + min(rq + m, RW - 1)) * NG + g;
+      sraw[m] = ld_raw<SDT>(S, gi);
+      zraw[m] = ld_raw<ZDT>(Z, gi);
+    }
   }
   const uint8_t* wb = W + (size_t)r0 * RB + 1024 * h + 16 * lane;
   u4_t wv[RW];
 #pragma unroll
-  for (int i = 0; i < R1; ++i) wv[i] = __builtin_nontemporal_load((const u4_t*)(wb + (size_t)i * RB));
+  for (int i = 0; i < R1; ++i) {
+    wv[i] = u4_t{0u, 0u, 0u, 0u};
+    if (live) wv[i] = __builtin_nontemporal_load((const u4_t*)(wb + (size_t)i * RB));
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // x in the operand element order n0 n4 n1 n5 n2 n6 n3 n7 of each 8-k word,
@@ -117,8 +138,10 @@ __device__ __forceinline__ void wq_gemv4p_body(const uint16_t* __restrict__ X,
     if (i == 2) {  // the remaining rows
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i2 = R1; i2 < RW; ++i2)
-        wv[i2] = __builtin_nontemporal_load((const u4_t*)(wb + (size_t)i2 * RB));
+      for (int i2 = R1; i2 < RW; ++i2) {
+        wv[i2] = u4_t{0u, 0u, 0u, 0u};
+        if (live) wv[i2] = __builtin_nontemporal_load((const u4_t*)(wb + (size_t)i2 * RB));
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
@@ -151,7 +174,7 @@ __device__ __forceinline__ void wq_gemv4p_body(const uint16_t* __restrict__ X,
     float zp = 0.0f;
     if constexpr (ZDT >= 0) zp = raw_to_f32<ZDT>(zraw[m]);
     const float p = raw_to_f32<SDT>(sraw[m]) * (v[m] - xoff - zp * xsum);
-    v[m] = rq + m < RW ? p : 0.0f;
+    v[m] = (live && rq + m < RW) ? p : 0.0f;
   }
   // rows rq + m -> over lane bits 4 and 5 -> row rq + 2 b4 + b5; then the sum
   // over bits 2 and 3 (the remaining groups)
@@ -160,18 +183,22 @@ __device__ __forceinline__ void wq_gemv4p_body(const uint16_t* __restrict__ X,
   const int r = rq + 2 * ((lane >> 4) & 1) + ((lane >> 5) & 1);
   if ((lane & 12) == 0 && r < RW) red[h][RW * ws + r] = rs;
   lds_barrier();
-  if (tid < 4 * RW) {
+  if (tid < NR) {
     const int n = n0 + tid;
-    store_out(Y, n, red[0][tid] + red[1][tid] + bias_at(bias, n, BF16), BF16);
+    float y = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2) y += red[s2][tid];
+    store_out(Y, n, y + bias_at(bias, n, BF16), BF16);
   }
 }
 
-// wq_gemv4p_<act>_z<zs>_r<RW>
+// K = 4096 (the headline): wq_gemv4p_<act>_z<zs>_r<RW>, 2 segments x 4 row
+// groups, K a compile-time constant.
 #define TM_GEMV4P(BF, ACT, ZS, ZDT, RW)                                                         \
   extern "C" __global__ __launch_bounds__(512) void wq_gemv4p_##ACT##_z##ZS##_r##RW(            \
       const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S, const void* Z, int M, \
       int N, int K, const uint16_t* bias) {                                                     \
-    wq_gemv4p_body<BF, ZDT, RW>(X, W, Y, S, Z, N, bias);                                        \
+    wq_gemv4p_body<BF, ZDT, RW, 2, 4, true>(X, W, Y, S, Z, N, K, bias);                         \
   }
 #define TM_GEMV4P_Z(BF, ACT, RW)                               \
   TM_GEMV4P(BF, ACT, n, -1, RW)                                \
@@ -185,6 +212,33 @@ TM_GEMV4P_RW(11)
 TM_GEMV4P_RW(12)
 TM_GEMV4P_RW(14)
 TM_GEMV4P_RW(16)
+
+// Other K (K % 128 == 0, K <= 16384): wq_gemv4k_<act>_z<zs>_s<KS>_r<RW>, KS
+// segments of 2048 k (the last one partial when K < 2048 KS) x RG row groups,
+// RG = min(4, 16 / KS) (4, 4, 4, 4, 3, 2, 2, 2 for KS = 1 .. 8 with KS = 1
+// taking 8), K at run time.
+#define TM_GEMV4K(BF, ACT, ZS, ZDT, KS, RG, RW)                                                 \
+  extern "C" __global__ __launch_bounds__(64 * KS * RG) void                                    \
+      wq_gemv4k_##ACT##_z##ZS##_s##KS##_r##RW(const uint16_t* X, const uint8_t* W, uint16_t* Y, \
+                                             const uint16_t* S, const void* Z, int M, int N,   \
+                                             int K, const uint16_t* bias) {                    \
+    wq_gemv4p_body<BF, ZDT, RW, KS, RG, false>(X, W, Y, S, Z, N, K, bias);                      \
+  }
+#define TM_GEMV4K_Z(BF, ACT, KS, RG, RW)                               \
+  TM_GEMV4K(BF, ACT, n, -1, KS, RG, RW)                                \
+  TM_GEMV4K(BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), KS, RG, RW)     \
+  TM_GEMV4K(BF, ACT, u, 3, KS, RG, RW)
+#define TM_GEMV4K_RW(KS, RG, RW) TM_GEMV4K_Z(false, f16, KS, RG, RW) TM_GEMV4K_Z(true, bf16, KS, RG, RW)
+#define TM_GEMV4K_KS(KS, RG) \
+  TM_GEMV4K_RW(KS, RG, 4) TM_GEMV4K_RW(KS, RG, 8) TM_GEMV4K_RW(KS, RG, 16)
+TM_GEMV4K_KS(1, 8)
+TM_GEMV4K_KS(2, 4)
+TM_GEMV4K_KS(3, 4)
+TM_GEMV4K_KS(4, 4)
+TM_GEMV4K_KS(5, 3)
+TM_GEMV4K_KS(6, 2)
+TM_GEMV4K_KS(7, 2)
+TM_GEMV4K_KS(8, 2)
 
 // ----------------------------------------------------------------------------
 // Pure-read twin of wq_gemv4p (a measurement kernel, not part of any matmul):
