@@ -31,13 +31,12 @@ for M, K in ((8, 1024), (12, 2048), (40, 512)):
 for N in (1024, 7168, 8192, 11264, 12288, 14336, 16384):
     CASES += _each(4, 1, N, 4096)
 # persistent int4 GEMV for other K: KS segments of 2048 k (the last one
-# partial for K = 1536, 2176, 9216, 11008) and RG row groups; per KS one N per
-# rows-per-wave count (4, 8, 16), the last workgroup shifted back (N not a
-# multiple of the workgroup's rows)
-GEMV4K = {1: (1536, 8), 2: (2176, 4), 3: (6144, 4), 4: (8192, 4), 5: (9216, 3),
-          6: (11008, 2), 7: (14336, 2), 8: (16384, 2)}  # KS: (K, RG)
-for ks, (K, rg) in GEMV4K.items():
-    for N in (1024 * rg - 48, 2048 * rg - 32, 4096 * rg - 16):
+# partial for K = 1536, 2176, 9216, 11008); per KS one N per row-group shape
+# (RG, RW) = (1, 8), (1, 16), (2, 16), (4, 16) (the last for KS <= 4), the
+# last workgroup shifted back (N not a multiple of the workgroup's rows)
+GEMV4K = {1: 1536, 2: 2176, 3: 6144, 4: 8192, 5: 9216, 6: 11008, 7: 14336, 8: 16384}
+for ks, K in GEMV4K.items():
+    for N in (2048 - 16, 4096 - 16, 8192 - 16, 16384 - 16)[: 4 if ks <= 4 else 3]:
         CASES += _each(4, 1, N, K)
 # linear int4 GEMV: K = 4096 / 8192 past the persistent kernels' reach (N >
 # 16384 / 16384 on 256 CUs, e.g. a fused gate/up projection)

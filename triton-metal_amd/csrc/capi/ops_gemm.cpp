@@ -125,16 +125,17 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
     }
   }
   // persistent int4 GEMV for other K (K % 128 == 0, K <= 16384): KS segments
-  // of 2048 k x RG row groups of RW rows, the smallest RW that keeps the grid
-  // within the CUs
+  // of 2048 k x RG row groups of RW rows, the first shape (fewest rows per
+  // workgroup) that keeps the grid within the CUs
   if (fast && qbits == 4 && M == 1 && G == 128 && K != 4096 && K % 128 == 0 && K <= 16384) {
     const int ks = (K + 2047) / 2048;
-    const int rg = ks == 1 ? 8 : std::min(4, 16 / ks);
-    static const int kRWk[] = {4, 8, 16};
-    for (int rw : kRWk) {
+    static const int kShape[][2] = {{1, 8}, {1, 16}, {2, 16}, {4, 16}};  // (RG, RW)
+    for (const auto& sh : kShape) {
+      const int rg = sh[0], rw = sh[1];
+      if (ks * rg > 16 || (ks > 4 && rg > 2)) continue;
       const int rows = rg * rw, grid = (N + rows - 1) / rows;
       if (N >= rows && grid <= cus) {
-        snprintf(pl->name, sizeof pl->name, "wq_gemv4k_%s_z%c_s%d_r%d", act, zc, ks, rw);
+        snprintf(pl->name, sizeof pl->name, "wq_gemv4k_%s_z%c_s%d_g%d_r%d", act, zc, ks, rg, rw);
         return set(grid, 64 * ks * rg, 0, WQ_ARGS_STD);
       }
     }

@@ -213,32 +213,35 @@ TM_GEMV4P_RW(12)
 TM_GEMV4P_RW(14)
 TM_GEMV4P_RW(16)
 
-// Other K (K % 128 == 0, K <= 16384): wq_gemv4k_<act>_z<zs>_s<KS>_r<RW>, KS
-// segments of 2048 k (the last one partial when K < 2048 KS) x RG row groups,
-// RG = min(4, 16 / KS) (4, 4, 4, 4, 3, 2, 2, 2 for KS = 1 .. 8 with KS = 1
-// taking 8), K at run time.
+// Other K (K % 128 == 0, K <= 16384): wq_gemv4k_<act>_z<zs>_s<KS>_g<RG>_r<RW>,
+// KS segments of 2048 k (the last one partial when K < 2048 KS) x RG row
+// groups of RW rows, K at run time.  Row-group shapes (RG, RW): (1, 8),
+// (1, 16), (2, 16), (4, 16) where KS RG <= 16.  Few, long waves stream best
+// here (K = 14336, N = 4096, one box: 7 waves x 16 rows 8.97 us, 14 waves x
+// 8 rows 10.34, 14 x 4 in two workgroups per CU 13.87; K = 8192: 4 waves x 16
+// rows 6.88, 8 x 8 7.58, 16 x 4 8.11).
 #define TM_GEMV4K(BF, ACT, ZS, ZDT, KS, RG, RW)                                                 \
   extern "C" __global__ __launch_bounds__(64 * KS * RG) void                                    \
-      wq_gemv4k_##ACT##_z##ZS##_s##KS##_r##RW(const uint16_t* X, const uint8_t* W, uint16_t* Y, \
-                                             const uint16_t* S, const void* Z, int M, int N,   \
-                                             int K, const uint16_t* bias) {                    \
+      wq_gemv4k_##ACT##_z##ZS##_s##KS##_g##RG##_r##RW(                                         \
+          const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S, const void* Z,   \
+          int M, int N, int K, const uint16_t* bias) {                                          \
     wq_gemv4p_body<BF, ZDT, RW, KS, RG, false>(X, W, Y, S, Z, N, K, bias);                      \
   }
 #define TM_GEMV4K_Z(BF, ACT, KS, RG, RW)                               \
   TM_GEMV4K(BF, ACT, n, -1, KS, RG, RW)                                \
   TM_GEMV4K(BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), KS, RG, RW)     \
   TM_GEMV4K(BF, ACT, u, 3, KS, RG, RW)
-#define TM_GEMV4K_RW(KS, RG, RW) TM_GEMV4K_Z(false, f16, KS, RG, RW) TM_GEMV4K_Z(true, bf16, KS, RG, RW)
-#define TM_GEMV4K_KS(KS, RG) \
-  TM_GEMV4K_RW(KS, RG, 4) TM_GEMV4K_RW(KS, RG, 8) TM_GEMV4K_RW(KS, RG, 16)
-TM_GEMV4K_KS(1, 8)
-TM_GEMV4K_KS(2, 4)
-TM_GEMV4K_KS(3, 4)
-TM_GEMV4K_KS(4, 4)
-TM_GEMV4K_KS(5, 3)
-TM_GEMV4K_KS(6, 2)
-TM_GEMV4K_KS(7, 2)
-TM_GEMV4K_KS(8, 2)
+#define TM_GEMV4K_A(KS, RG, RW) TM_GEMV4K_Z(false, f16, KS, RG, RW) TM_GEMV4K_Z(true, bf16, KS, RG, RW)
+#define TM_GEMV4K_KS3(KS) TM_GEMV4K_A(KS, 1, 8) TM_GEMV4K_A(KS, 1, 16) TM_GEMV4K_A(KS, 2, 16)
+#define TM_GEMV4K_KS4(KS) TM_GEMV4K_KS3(KS) TM_GEMV4K_A(KS, 4, 16)
+TM_GEMV4K_KS4(1)
+TM_GEMV4K_KS4(2)
+TM_GEMV4K_KS4(3)
+TM_GEMV4K_KS4(4)
+TM_GEMV4K_KS3(5)
+TM_GEMV4K_KS3(6)
+TM_GEMV4K_KS3(7)
+TM_GEMV4K_KS3(8)
 
 // ----------------------------------------------------------------------------
 // Pure-read twin of wq_gemv4p (a measurement kernel, not part of any matmul):
