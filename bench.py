@@ -111,11 +111,18 @@ def dense(dev, M=512, N=512, K=512):
                 flops=2 * M * N * K, bound="mfma", dtype="fp16", config={"workload": f"dense_{M}x{N}x{K}", "M": M, "N": N, "K": K})
 
 
-def flash(dev, causal, B=4, H=32, S=4096, D=128):
+def flash(dev, causal, B=4, H=32, S=4096, D=128, const_data=False):
+    """C4.  const_data: every element of q, k, v the same value (0.5), the
+    same kernel and work with no bit toggling in the MFMA operands - the
+    measurement that shows the clock the random data costs."""
     import torch
     import triton_metal_amd as tm
     g = torch.Generator(device=dev).manual_seed(4)
-    q, k, v = (torch.randn(B, H, S, D, device=dev, generator=g).bfloat16() for _ in range(3))
+    if const_data:
+        q, k, v = (torch.full((B, H, S, D), 0.5, device=dev, dtype=torch.bfloat16)
+                   for _ in range(3))
+    else:
+        q, k, v = (torch.randn(B, H, S, D, device=dev, generator=g).bfloat16() for _ in range(3))
     o = torch.empty_like(q)
     lse = torch.empty(B, H, S, device=dev, dtype=torch.float32)
     launches = [tm.plan_flash_attention(q, k, v, o, lse, causal=causal)]
@@ -123,7 +130,8 @@ def flash(dev, causal, B=4, H=32, S=4096, D=128):
     nbytes = 2 * 4 * B * H * S * D + 4 * B * H * S
     return dict(launches=launches, keep=(q, k, v, o, lse), bytes=nbytes, flops=flops,
                 bound="mfma", dtype="bf16",
-                config={"workload": f"flash_fwd_{'causal' if causal else 'full'}", "B": B,
+                config={"workload": f"flash_fwd_{'causal' if causal else 'full'}"
+                        + ("_constdata" if const_data else ""), "B": B,
                         "H": H, "S": S, "D": D, "causal": causal,
                         "flops_convention": "4*B*H*S^2*D, halved when causal"})
 
@@ -311,6 +319,8 @@ def w4a16_wide_k(dev, M, K=14336, N=4096, G=128):
 EXTRA = {"hbm_copy": hbm_copy,
          "w4a16_m1_read_twin": lambda d: w4a16_read_twin(d),
          "w4a16_m1_read_twin_w": lambda d: w4a16_read_twin(d, weights_only=True),
+         "flash_causal_constdata": lambda d: flash(d, True, const_data=True),
+         "flash_full_constdata": lambda d: flash(d, False, const_data=True),
          "w4a16_m1_k14336": lambda d: w4a16_wide_k(d, 1),
          "w4a16_m16_k14336": lambda d: w4a16_wide_k(d, 16)}
 
