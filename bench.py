@@ -322,7 +322,9 @@ EXTRA = {"hbm_copy": hbm_copy,
          "flash_causal_constdata": lambda d: flash(d, True, const_data=True),
          "flash_full_constdata": lambda d: flash(d, False, const_data=True),
          "w4a16_m1_k14336": lambda d: w4a16_wide_k(d, 1),
-         "w4a16_m16_k14336": lambda d: w4a16_wide_k(d, 16)}
+         "w4a16_m16_k14336": lambda d: w4a16_wide_k(d, 16),
+         "w4a16_m8_k14336": lambda d: w4a16_wide_k(d, 8),
+         "w4a16_m4_k11008": lambda d: w4a16_wide_k(d, 4, K=11008)}
 
 
 def time_workload(w, steps, warmup, graph=True, budget_s=2.0, min_replays=100):

@@ -43,16 +43,22 @@ for ks, K in GEMV4K.items():
 CASES += _each(4, 1, 16400, 4096)
 CASES += _each(4, 1, 28672, 4096, acts=(torch.float16,))
 CASES += _each(4, 1, 16400, 8192)
+# long-K streaming kernel (2 <= M <= 16, 4096 < K <= 16384): tiles per
+# workgroup NT = 1 / 2, activation rows staged XR = 8 / 16, chunks per wave
+# NCH = 8 / 16 (K = 11008: the last round of chunks partly past K)
+for M, K, N in ((5, 6144, 1040), (8, 11008, 4096), (16, 8192, 2048), (12, 14336, 4096),
+                (3, 5120, 8176), (7, 16384, 8176), (9, 6144, 5120), (16, 11008, 8176)):
+    CASES += _each(4, M, N, K)
 # int4 GEMV at K = 8192, 2 <= M <= 8
 CASES += _each(4, 4, 64, 8192)
 # int8 GEMVs, M = 1, K = 4096: linear (fp16) and 8-wave (bf16)
 CASES += _each(8, 1, 64, 4096)
 # skinny (M <= 8, other K): int4 without and with vector scale loads, int8
-CASES += _each(4, 2, 64, 5120)
-CASES += _each(4, 2, 64, 12288)
+CASES += _each(4, 2, 64, 5120, G=256)
+CASES += _each(4, 2, 64, 20480)
 CASES += _each(8, 1, 64, 1024)
 # tiled (K past the streaming kernel's 4096, M > 8)
-CASES += _each(4, 9, 64, 4352)
+CASES += _each(4, 20, 64, 8192)
 CASES += _each(8, 9, 64, 4352)
 # general fp32 kernel
 CASES += [(4, 3, 40, 100, 32, torch.float32, None), (8, 3, 40, 100, 1, torch.float32, "s")]

@@ -156,6 +156,25 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
       return set(N / 16, 512, glds, WQ_ARGS_STD);
     }
   }
+  // long-K streaming kernel: 2 <= M <= 16, 4096 < K <= 16384 (K % 128 == 0),
+  // NT = 1 or 2 16-column tiles per workgroup (one workgroup per CU for the
+  // N of a down projection), K in 128-k chunks over at most 8 waves
+  if (fast && qbits == 4 && M >= 2 && M <= 16 && G == 128 && K > 4096 && K <= 16384 &&
+      K % 128 == 0 && sz4) {
+    const int nchunk = K / 128;
+    const int nch = nchunk <= 64 ? 8 : 16;
+    const int nwv = (nchunk + nch - 1) / nch;
+    const int tiles = N / 16;
+    const int nt = tiles <= cus ? 1 : 2;
+    const int xr = M <= 8 ? 8 : 16;
+    const size_t slot = (size_t)nt * 1024 + (size_t)xr * 256;
+    const size_t wb = 2 * slot + (size_t)512 * nt * (nch / 4);
+    const size_t slds = (size_t)nwv * (wb + 8 * 64 * sizeof(float));
+    if (slds <= max_lds) {
+      snprintf(pl->name, sizeof pl->name, "wq_streamk_%s_z%c_t%d_x%d_c%d", act, zc, nt, xr, nch);
+      return set((tiles + nt - 1) / nt, 64 * nwv, slds, WQ_ARGS_STD);
+    }
+  }
   // linear int8 GEMV: M = 1, K = 4096, fp16 (VALU dot products, 1 KB of one
   // row per load instruction)
   if (fast && qbits == 8 && M == 1 && K == 4096 && adt == TM_DT_F16) {
