@@ -135,12 +135,17 @@ def test_flash_every_head_xcd_pairing(dev, B, H, causal):
 # --- benchmark configuration C4 (sampled rows against the oracle) -----------------
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_config_c4(dev, causal):
+    """C4 at full size: every one of the 128 (batch, head) pairs on 24 rows
+    sampled across the sequence (the last row always), and three heads on 128
+    rows, against the fp64 softmax of the same bf16 inputs."""
     B, H, S, D = 4, 32, 4096, 128
     q, k, v = (_rand((B, H, S, D), s, torch.bfloat16, dev) for s in (21, 22, 23))
     o, lse = tm.attention(q, k, v, causal=causal, return_lse=True)
     rng = np.random.default_rng(0)
-    for b, h in [(0, 0), (3, 31), (2, 17)]:
-        rows = np.sort(rng.choice(S, 128, replace=False))
+    heads = [(b, h, 24) for b in range(B) for h in range(H)]
+    heads += [(0, 0, 128), (3, 31, 128), (2, 17, 128)]
+    for b, h, nrow in heads:
+        rows = np.sort(rng.choice(S, nrow, replace=False))
         rows[-1] = S - 1
         qs = q[b, h, rows].float().cpu().numpy()
         kk, vv = k[b, h].float().cpu().numpy(), v[b, h].float().cpu().numpy()

@@ -183,18 +183,18 @@ def test_kda_empty_sequence_passes_state_through(dev):
     assert o.shape == (1, 0, 2, 128) and torch.equal(st, s0)
 
 
-def test_kda_config_c5_sampled_heads(dev):
-    """Benchmark configuration C5 (B=1, H=16, T=8192): two heads against the
-    fp64 recurrence, every head finite."""
+def test_kda_config_c5_every_head(dev):
+    """Benchmark configuration C5 (B=1, H=16, T=8192): every head's output and
+    final state against the fp64 recurrence (the oracle steps all heads at
+    once, about 8 s on the host)."""
     B, T, H = 1, 8192, 16
     q, k, v, g, beta = kda_inputs(B, T, H, seed=0)
     o, st = _run(dev, q, k, v, g, beta)
     assert np.isfinite(o).all() and np.isfinite(st).all()
-    for h in (0, 13):
-        sl = slice(h, h + 1)
-        o_ref, st_ref = _ref(q[:, :, sl], k[:, :, sl], v[:, :, sl], g[:, :, sl], beta[:, :, sl])
-        _close(o[:, :, sl], o_ref, f"o head {h}")
-        _close(st[:, sl], st_ref, f"final state head {h}")
+    o_ref, st_ref = _ref(q, k, v, g, beta)
+    for h in range(H):
+        _close(o[:, :, h], o_ref[:, :, h], f"o head {h}")
+        _close(st[:, h], st_ref[:, h], f"final state head {h}")
 
 
 def test_kda_many_chunks_per_workgroup_partial_last_chunk(dev):
