@@ -195,18 +195,22 @@ int tm_matmul(const void* A, const void* B, void* C, int M, int N, int K, int ld
  * row-major with leading dimensions K, N, N; M, N, K are one uint32 each on
  * the device, the buffer(3..5) arguments of make_matmul_2d_kernel
  * (_msl_templates.py:588-679) and make_matmul_swizzled_kernel (682-781).
- * max_m / max_n: the host-known capacity the launch covers; sizes read on
+ * max_m / max_n: the host-known capacity the launch covers; M and N read on
  * the device are clamped to it (rows / columns beyond are not written), so a
- * captured launch serves any M <= max_m, N <= max_n.  in_dtype F32, F16 or
- * BF16; out_dtype in_dtype or F32; fp32 accumulation.  tm_matmul_2d walks
- * the output tiles on a 2-D grid; tm_matmul_swizzled in runs of group_size
- * tile rows (64-row tiles), column by column within a run. */
+ * captured launch serves any M <= max_m, N <= max_n.  a_elems / b_elems /
+ * c_elems: the element counts of A, B and C; sizes on the device whose M K,
+ * K N or M N exceed them make the launch do nothing (the reference trusts the
+ * buffers; here nothing past them is read or written).  in_dtype F32, F16 or
+ * BF16; out_dtype in_dtype or F32; fp32 accumulation.  tm_matmul_2d walks the
+ * output tiles on a 2-D grid; tm_matmul_swizzled in runs of group_size tile
+ * rows (64-row tiles), column by column within a run. */
 int tm_matmul_2d(const void* A, const void* B, void* C, const unsigned* M, const unsigned* N,
-                 const unsigned* K, int max_m, int max_n, int in_dtype, int out_dtype,
-                 void* stream);
+                 const unsigned* K, int max_m, int max_n, size_t a_elems, size_t b_elems,
+                 size_t c_elems, int in_dtype, int out_dtype, void* stream);
 int tm_matmul_swizzled(const void* A, const void* B, void* C, const unsigned* M,
                        const unsigned* N, const unsigned* K, int max_m, int max_n,
-                       int group_size, int in_dtype, int out_dtype, void* stream);
+                       size_t a_elems, size_t b_elems, size_t c_elems, int group_size,
+                       int in_dtype, int out_dtype, void* stream);
 /* tl.dot in general form: the strided dot template of the reference,
  * _lower_dot_via_prebuilt_template (triton_metal/codegen/_lowerer_templates.py:
  * 1116-1540), with the epilogue detection of _detect_dot_epilogue

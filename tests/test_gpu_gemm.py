@@ -106,6 +106,28 @@ def test_device_sizes_shapes(dev, dt, out, group):
                                atol=tol[0], rtol=tol[1])
 
 
+def test_device_sizes_past_the_buffers_do_nothing(dev):
+    """Sizes on the device that the buffers cannot hold (here K larger than A
+    and B allow, then M larger than C) make the launch write nothing; with
+    fitting sizes the same launch computes."""
+    M, N, K = 16, 16, 16
+    A = torch.randn(M * K, device=dev)
+    B = torch.randn(K * N, device=dev)
+    C = torch.full((M * N,), 7.0, device=dev)
+    dims = torch.tensor([M, N, 1000], dtype=torch.int32, device=dev)
+    tm.matmul_device_sizes(A, B, C, dims[0:1], dims[1:2], dims[2:3], max_m=M, max_n=N)
+    torch.cuda.synchronize()
+    assert torch.all(C == 7.0)
+    dims = torch.tensor([64, N, K], dtype=torch.int32, device=dev)
+    tm.matmul_device_sizes(A, B, C, dims[0:1], dims[1:2], dims[2:3], max_m=64, max_n=N)
+    torch.cuda.synchronize()
+    assert torch.all(C == 7.0)
+    dims = torch.tensor([M, N, K], dtype=torch.int32, device=dev)
+    tm.matmul_device_sizes(A, B, C, dims[0:1], dims[1:2], dims[2:3], max_m=M, max_n=N)
+    ref = oracle.matmul(A.double().cpu().numpy().reshape(M, K), B.double().cpu().numpy().reshape(K, N))
+    np.testing.assert_allclose(C.double().cpu().numpy().reshape(M, N), ref, atol=1e-4, rtol=1e-4)
+
+
 @pytest.mark.parametrize("name", ["linear_seed1111", "linear_seed2222"])
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16])
 def test_fused_linear_reference_kat(kats, dev, name, dt):

@@ -435,8 +435,8 @@ int tm_wq_dequant(const void* weight, const void* scales, const void* zeros, voi
 
 namespace {
 int matmul_dd(const char* op, const void* A, const void* B, void* C, const unsigned* Mp,
-              const unsigned* Np, const unsigned* Kp, int max_m, int max_n, int group_m,
-              int idt, int odt, void* stream) {
+              const unsigned* Np, const unsigned* Kp, int max_m, int max_n, size_t a_elems,
+              size_t b_elems, size_t c_elems, int group_m, int idt, int odt, void* stream) {
   if (max_m < 0 || max_n < 0 || group_m < 0)
     return fail(TM_ERR_INVALID_ARG, "%s: max_m=%d max_n=%d group=%d", op, max_m, max_n, group_m);
   if (max_m == 0 || max_n == 0) return 0;
@@ -454,25 +454,27 @@ int matmul_dd(const char* op, const void* A, const void* B, void* C, const unsig
            odt == idt ? "same" : "f32");
   const dim3 grid = group_m == 0 ? dim3((unsigned)ntc, (unsigned)ntr)
                                  : dim3((unsigned)(ntr * ntc));
-  return launch(kernel(name), grid, dim3(256), 0, stream, A, B, C, Mp, Np, Kp, max_m, max_n,
-                group_m);
+  const unsigned long long ae = a_elems, be = b_elems, ce = c_elems;
+  return launch(kernel(name), grid, dim3(256), 0, stream, A, B, C, Mp, Np, Kp, max_m, max_n, ae,
+                be, ce, group_m);
 }
 }  // namespace
 
 int tm_matmul_2d(const void* A, const void* B, void* C, const unsigned* M, const unsigned* N,
-                 const unsigned* K, int max_m, int max_n, int in_dtype, int out_dtype,
-                 void* stream) {
-  return matmul_dd("tm_matmul_2d", A, B, C, M, N, K, max_m, max_n, 0, in_dtype, out_dtype,
-                   stream);
+                 const unsigned* K, int max_m, int max_n, size_t a_elems, size_t b_elems,
+                 size_t c_elems, int in_dtype, int out_dtype, void* stream) {
+  return matmul_dd("tm_matmul_2d", A, B, C, M, N, K, max_m, max_n, a_elems, b_elems, c_elems, 0,
+                   in_dtype, out_dtype, stream);
 }
 
 int tm_matmul_swizzled(const void* A, const void* B, void* C, const unsigned* M,
                        const unsigned* N, const unsigned* K, int max_m, int max_n,
-                       int group_size, int in_dtype, int out_dtype, void* stream) {
+                       size_t a_elems, size_t b_elems, size_t c_elems, int group_size,
+                       int in_dtype, int out_dtype, void* stream) {
   if (group_size <= 0)
     return fail(TM_ERR_INVALID_ARG, "tm_matmul_swizzled: group_size=%d", group_size);
-  return matmul_dd("tm_matmul_swizzled", A, B, C, M, N, K, max_m, max_n, group_size, in_dtype,
-                   out_dtype, stream);
+  return matmul_dd("tm_matmul_swizzled", A, B, C, M, N, K, max_m, max_n, a_elems, b_elems,
+                   c_elems, group_size, in_dtype, out_dtype, stream);
 }
 
 int tm_matmul(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb,

@@ -376,7 +376,9 @@ TM_GEMM_S32_ALL(128)
 // read M, N, K from `device const uint*` buffers).  The grid covers a
 // host-known capacity (max_m x max_n); workgroups whose tile lies past the
 // sizes read on the device return at once, so one launch (or one captured
-// graph node) serves any M <= max_m, N <= max_n.
+// graph node) serves any M <= max_m, N <= max_n (M, N beyond are clamped to
+// it).  The buffers' element counts come with the launch: sizes on the device
+// whose M K, K N or M N exceed them make the launch do nothing.
 //
 // 64 x 64 output tile per 256-thread workgroup, K in steps of 16 through LDS
 // ([k][row] fp32, so each thread's 4 x 4 outputs take 8 LDS reads per k),
@@ -392,11 +394,17 @@ __device__ __forceinline__ void gemm_dd_body(const void* __restrict__ A,
                                              const unsigned* __restrict__ Mp,
                                              const unsigned* __restrict__ Np,
                                              const unsigned* __restrict__ Kp, int max_m,
-                                             int max_n, int group_m) {
+                                             int max_n, unsigned long long a_elems,
+                                             unsigned long long b_elems,
+                                             unsigned long long c_elems, int group_m) {
   __shared__ float As[16][64 + 4];
   __shared__ float Bs[16][64 + 4];
   const int M = (int)min(Mp[0], (unsigned)max_m), N = (int)min(Np[0], (unsigned)max_n);
   const int K = (int)min(Kp[0], 0x7fffffffu);
+  // sizes the buffers cannot hold produce nothing (no read or write past them)
+  if ((unsigned long long)M * K > a_elems || (unsigned long long)K * N > b_elems ||
+      (unsigned long long)M * N > c_elems)
+    return;
   const int ntr = (M + 63) / 64, ntc = (N + 63) / 64;
   int tr, tc;
   if (group_m <= 0) {
@@ -461,8 +469,10 @@ __device__ __forceinline__ void gemm_dd_body(const void* __restrict__ A,
 #define TM_GEMM_DD(IN, IDT, OUT, ODT)                                                           \
   extern "C" __global__ __launch_bounds__(256) void gemm_dd_##IN##_##OUT(                       \
       const void* A, const void* B, void* C, const unsigned* Mp, const unsigned* Np,            \
-      const unsigned* Kp, int max_m, int max_n, int group_m) {                                  \
-    gemm_dd_body<IDT, ODT>(A, B, C, Mp, Np, Kp, max_m, max_n, group_m);                        \
+      const unsigned* Kp, int max_m, int max_n, unsigned long long a_elems,                     \
+      unsigned long long b_elems, unsigned long long c_elems, int group_m) {                    \
+    gemm_dd_body<IDT, ODT>(A, B, C, Mp, Np, Kp, max_m, max_n, a_elems, b_elems, c_elems,       \
+                           group_m);                                                            \
   }
 TM_GEMM_DD(f32, TM_DT_F32, same, TM_DT_F32)
 TM_GEMM_DD(f16, TM_DT_F16, same, TM_DT_F16)

@@ -52,8 +52,8 @@ SIGNATURES = {
     "tm_wq_repack_awq": [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp],
     "tm_matmul": [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_linear": [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp],
-    "tm_matmul_2d": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp],
-    "tm_matmul_swizzled": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp],
+    "tm_matmul_2d": [vp, vp, vp, vp, vp, vp, i32, i32, sz, sz, sz, i32, i32, vp],
+    "tm_matmul_swizzled": [vp, vp, vp, vp, vp, vp, i32, i32, sz, sz, sz, i32, i32, i32, vp],
     "tm_dot": [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, C.POINTER(C.c_longlong), i32, i32,
                i32, i32, i32, vp],
     "tm_flash_attention": [vp, vp, vp, vp, vp, i32, i32, i32, i32, C.POINTER(C.c_longlong),

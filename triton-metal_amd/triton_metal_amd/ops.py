@@ -412,9 +412,10 @@ def plan_matmul_device_sizes(A, B, C, M_buf, N_buf, K_buf, max_m=None, max_n=Non
         _numel_at_least(A, m * k, "A")
         _numel_at_least(B, k * n, "B")
         _numel_at_least(C, min(m, max_m) * min(n, max_n), "C")
-    else:
-        _numel_at_least(C, max_m * max_n, "C")
-    args = (_ptr(A), _ptr(B), _ptr(C), _ptr(mb), _ptr(nb), _ptr(kb), int(max_m), int(max_n))
+    # the kernel checks the sizes it reads on the device against the buffers'
+    # element counts and does nothing when they do not fit
+    args = (_ptr(A), _ptr(B), _ptr(C), _ptr(mb), _ptr(nb), _ptr(kb), int(max_m), int(max_n),
+            A.numel(), B.numel(), C.numel())
     if group_size:
         f, args = _lib.lib().tm_matmul_swizzled, args + (int(group_size),)
     else:
@@ -430,12 +431,13 @@ def matmul_device_sizes(A, B, C, M_buf, N_buf, K_buf, max_m=None, max_n=None, gr
     order of make_matmul_2d_kernel / make_matmul_swizzled_kernel
     (_msl_templates.py:588-781; A, B, C, M_buf, N_buf, K_buf, row-major with
     leading dimensions K, N, N).  The sizes are one-element uint32 / int32
-    device tensors or ints.  max_m / max_n bound the launch (sizes read on the
-    device are clamped to them; C must then hold max_m * max_n elements);
-    left out, they are the sizes themselves, read with one synchronising copy.
-    group_size 0 walks the output tiles on a 2-D grid, > 0 in runs of that many
-    tile rows (the swizzled template's grouped order).  fp32 accumulation; C is
-    A's dtype or float32."""
+    device tensors or ints.  max_m / max_n bound the launch's grid (M and N
+    read on the device are clamped to them); left out, they are the sizes
+    themselves, read with one synchronising copy.  Sizes on the device whose
+    M K, K N or M N exceed A's, B's or C's elements make the launch do
+    nothing.  group_size 0 walks the output tiles on a 2-D grid, > 0 in runs of
+    that many tile rows (the swizzled template's grouped order).  fp32
+    accumulation; C is A's dtype or float32."""
     _run(plan_matmul_device_sizes(A, B, C, M_buf, N_buf, K_buf, max_m, max_n, group_size))
     return C
 
