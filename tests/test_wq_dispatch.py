@@ -62,7 +62,9 @@ def _built(stem):
 def wq_kernels(tmp_path_factory):
     tmp = tmp_path_factory.mktemp("co")
     names = set()
-    for stem in ("wq_gemm", "wq_gemvp", "wq_streamk"):
+    stems = ["wq_gemm", "wq_gemvp"] + sorted(
+        p.stem for p in (ROOT / "triton-metal_amd" / "csrc" / "kernels").glob("wq_streamk*.hip"))
+    for stem in stems:
         names |= {n for n, _, _ in _kernel_metadata(_built(stem), tmp)}
     # the dequantised tile and the GEMV's pure-read twin (a measurement kernel)
     return {n for n in names if n != "wq_dequant" and not n.startswith("wq_read_twin")}

@@ -43,23 +43,35 @@ for ks, K in GEMV4K.items():
 CASES += _each(4, 1, 16400, 4096)
 CASES += _each(4, 1, 28672, 4096, acts=(torch.float16,))
 CASES += _each(4, 1, 16400, 8192)
-# long-K streaming kernel (2 <= M <= 16, 4096 < K <= 16384): tiles per
-# workgroup NT = 1 / 2, activation rows staged XR = 8 / 16, chunks per wave
-# NCH = 8 / 16 (K = 11008: the last round of chunks partly past K)
-for M, K, N in ((5, 6144, 1040), (8, 11008, 4096), (16, 8192, 2048), (12, 14336, 4096),
-                (3, 5120, 8176), (7, 16384, 8176), (9, 6144, 5120), (16, 11008, 8176)):
-    CASES += _each(4, M, N, K)
+# long-K streaming kernel (M <= 64, K > 4096): tiles per workgroup NT = 1 / 2
+# (N / 16 <= 256 or not), activation rows staged XR = 8 / 16 in one pass (M <=
+# 8 / 16) or 16 over several (M > 16, NT = 1; int4 K <= 16384), chunks per
+# wave NCH (int4 8 / 16 / 32, int8 16 / 32); K = 11008, 16512: the last round
+# of chunks partly past K
+STREAMK = {
+    4: ((5, 6144, 1040), (3, 5120, 8176), (8, 11008, 4096), (7, 16384, 8176), (2, 20480, 1024),
+        (6, 28672, 8192), (16, 8192, 2048), (9, 6144, 5120), (12, 14336, 4096), (16, 11008, 8176),
+        (13, 24576, 2048), (10, 16512, 4112), (40, 6144, 1024), (24, 14336, 1040)),
+    8: ((4, 6144, 1040), (8, 5120, 4112), (3, 14336, 2048), (1, 11008, 4112), (16, 8192, 512),
+        (12, 4608, 4112), (9, 16384, 1024), (14, 9216, 4112), (33, 6144, 256), (64, 12288, 512)),
+}
+for qb, shapes in STREAMK.items():
+    for M, K, N in shapes:
+        CASES += _each(qb, M, N, K)
 # int4 GEMV at K = 8192, 2 <= M <= 8
 CASES += _each(4, 4, 64, 8192)
 # int8 GEMVs, M = 1, K = 4096: linear (fp16) and 8-wave (bf16)
 CASES += _each(8, 1, 64, 4096)
-# skinny (M <= 8, other K): int4 without and with vector scale loads, int8
+# skinny (M <= 8, other K or G): int4 without and with vector scale loads
+# (G = 256; K past the long-K kernel's 32768), int8
 CASES += _each(4, 2, 64, 5120, G=256)
-CASES += _each(4, 2, 64, 20480)
+CASES += _each(4, 2, 64, 36864)
 CASES += _each(8, 1, 64, 1024)
-# tiled (K past the streaming kernel's 4096, M > 8)
-CASES += _each(4, 20, 64, 8192)
-CASES += _each(8, 9, 64, 4352)
+# tiled (M > 64 with K past the streaming kernels' 4096; int4 M > 16 with K
+# past 16384)
+CASES += _each(4, 80, 64, 8192)
+CASES += _each(4, 20, 64, 20480, acts=(torch.bfloat16,))
+CASES += _each(8, 80, 64, 4352)
 # general fp32 kernel
 CASES += [(4, 3, 40, 100, 32, torch.float32, None), (8, 3, 40, 100, 1, torch.float32, "s")]
 

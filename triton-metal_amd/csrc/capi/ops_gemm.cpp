@@ -156,23 +156,29 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
       return set(N / 16, 512, glds, WQ_ARGS_STD);
     }
   }
-  // long-K streaming kernel: 2 <= M <= 16, 4096 < K <= 16384 (K % 128 == 0),
-  // NT = 1 or 2 16-column tiles per workgroup (one workgroup per CU for the
-  // N of a down projection), K in 128-k chunks over at most 8 waves
-  if (fast && qbits == 4 && M >= 2 && M <= 16 && G == 128 && K > 4096 && K <= 16384 &&
-      K % 128 == 0 && sz4) {
-    const int nchunk = K / 128;
-    const int nch = nchunk <= 64 ? 8 : 16;
+  // long-K streaming kernel: M <= 64, K > 4096 in chunks of 64 weight bytes
+  // per row (int4 128 k = one group, int8 64 k), NCH chunks per wave over at
+  // most 8 waves (int4 K <= 32768, int8 K <= 16384); NT = 1 or 2 16-column
+  // tiles per workgroup (one workgroup per CU for the N of a down projection;
+  // NT = 2 only where its LDS fits); M > 16 in passes of 16 rows (NT = 1;
+  // int4 K <= 16384, as the first pass's weights stay in registers)
+  if (fast && M <= 64 && K > 4096 && K % CK == 0 && K <= (qbits == 4 ? 32768 : 16384) && sz4 &&
+      (qbits == 8 || G == 128) && (M <= 16 || qbits == 8 || K <= 16384)) {
+    const int nchunk = K / CK;
+    const int nch = nchunk <= 64 && qbits == 4 ? 8 : nchunk <= 128 ? 16 : 32;
     const int nwv = (nchunk + nch - 1) / nch;
     const int tiles = N / 16;
-    const int nt = tiles <= cus ? 1 : 2;
+    const bool multi = M > 16;
     const int xr = M <= 8 ? 8 : 16;
-    const size_t slot = (size_t)nt * 1024 + (size_t)xr * 256;
-    const size_t wb = 2 * slot + (size_t)512 * nt * (nch / 4);
-    const size_t slds = (size_t)nwv * (wb + 8 * 64 * sizeof(float));
-    if (slds <= max_lds) {
-      snprintf(pl->name, sizeof pl->name, "wq_streamk_%s_z%c_t%d_x%d_c%d", act, zc, nt, xr, nch);
-      return set((tiles + nt - 1) / nt, 64 * nwv, slds, WQ_ARGS_STD);
+    for (int nt = tiles > cus && !multi ? 2 : 1; nt >= 1; --nt) {
+      const size_t slot = (size_t)nt * 1024 + (size_t)xr * 2 * CK;
+      const size_t scb = qbits == 4 ? (size_t)512 * nt * (nch / 4) : 1024;
+      const size_t slds = (size_t)nwv * (2 * slot + scb + 8 * 64 * sizeof(float));
+      if (slds <= max_lds) {
+        snprintf(pl->name, sizeof pl->name, "wq_streamk_q%d_%s_z%c_t%d_x%d%c_c%d", qbits, act, zc,
+                 nt, xr, multi ? 'm' : 's', nch);
+        return set((tiles + nt - 1) / nt, 64 * nwv, slds, WQ_ARGS_STD);
+      }
     }
   }
   // linear int8 GEMV: M = 1, K = 4096, fp16 (VALU dot products, 1 KB of one
