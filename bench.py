@@ -315,6 +315,15 @@ def w4a16_wide_k(dev, M, K=14336, N=4096, G=128):
     return w
 
 
+def w8a16_wide_k(dev, M, K=14336, N=4096):
+    """The W8A16 counterpart of w4a16_wide_k (per-channel scales, no zero-points)."""
+    import triton_metal_amd as tm
+    w = w8a16(dev, M, K=K, N=N)
+    w["config"]["workload"] = f"w8a16_m{M}_k{K}"
+    w["config"]["kernel"] = tm.wq_kernel_for(8, M, N, K)[0]
+    return w
+
+
 # opt-in workloads (--only NAME), not part of the default run
 EXTRA = {"hbm_copy": hbm_copy,
          "w4a16_m1_read_twin": lambda d: w4a16_read_twin(d),
@@ -324,7 +333,12 @@ EXTRA = {"hbm_copy": hbm_copy,
          "w4a16_m1_k14336": lambda d: w4a16_wide_k(d, 1),
          "w4a16_m16_k14336": lambda d: w4a16_wide_k(d, 16),
          "w4a16_m8_k14336": lambda d: w4a16_wide_k(d, 8),
-         "w4a16_m4_k11008": lambda d: w4a16_wide_k(d, 4, K=11008)}
+         "w4a16_m4_k11008": lambda d: w4a16_wide_k(d, 4, K=11008),
+         "w4a16_m32_k14336": lambda d: w4a16_wide_k(d, 32),
+         "w4a16_m64_k14336": lambda d: w4a16_wide_k(d, 64),
+         "w4a16_m8_k28672": lambda d: w4a16_wide_k(d, 8, K=28672, N=8192),
+         "w8a16_m1_k14336": lambda d: w8a16_wide_k(d, 1),
+         "w8a16_m16_k14336": lambda d: w8a16_wide_k(d, 16)}
 
 
 def time_workload(w, steps, warmup, graph=True, budget_s=2.0, min_replays=100):
