@@ -138,21 +138,45 @@ int tm_int8_linear(const void* input, const void* weight, const void* bias, void
 int tm_int4_linear(const void* input, const void* weight, const void* bias, void* output,
                    const void* scales, const void* zeros, int M, int N, int K, int group_size,
                    int act_dtype, int scale_dtype, int zero_dtype, void* stream);
-/* Kernel selection of the four entry points above, without launching: the
- * name of the gfx950 kernel a call with these sizes and dtypes would run, its
- * grid, block and dynamic LDS bytes, for a device with cu_count CUs and
- * max_lds bytes of dynamic LDS per workgroup (MI355X: 256, 163840).
- * align_flags: TM_WQ_ALIGN_* bits for the pointer alignments of the call.  A
- * diagnostic with no counterpart in the reference (which compiles one kernel
- * per template); it lets tests show which kernel family a shape reaches.
- * Touches no device. */
+/* The same four operations (qbits 4 or 8; bias NULL for the plain matmul;
+ * group_size ignored for int8) with a caller-provided device workspace:
+ * shapes whose kernel would leave the GPU underfilled or exceed a kernel's K
+ * (long-K down projections at M >= 17, int8 K > 16384, ...) then run split-K
+ * (fp32 slice sums in the workspace, then one reduction launch).  workspace:
+ * 16-byte aligned, at least tm_wq_workspace_bytes(...) bytes, used only by
+ * this call's launches on `stream` (overlapping calls must not share one);
+ * NULL / 0 behaves as tm_int4_matmul / tm_int8_matmul / the linear forms, which
+ * never split.  The Python operators (int4_matmul, ...) pass a torch-allocated
+ * workspace this way.  No counterpart in the reference, whose templates run
+ * one threadgroup per output tile over the whole of K. */
+int tm_wq_matmul_ws(int qbits, const void* input, const void* weight, const void* bias,
+                    void* output, const void* scales, const void* zeros, int M, int N, int K,
+                    int group_size, int act_dtype, int scale_dtype, int zero_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace bytes tm_wq_matmul_ws needs for this call on the current device
+ * (0: no split-K; then any workspace, or none, will do).  The pointers are
+ * only inspected for their alignment. */
+size_t tm_wq_workspace_bytes(int qbits, const void* input, const void* weight,
+                             const void* scales, const void* zeros, int M, int N, int K,
+                             int group_size, int act_dtype, int scale_dtype, int zero_dtype);
+/* Kernel selection of the entry points above, without launching: the name of
+ * the gfx950 kernel a call with these sizes and dtypes would run, its grid,
+ * block and dynamic LDS bytes, its k-slices (1: no split-K; the grid is then
+ * (grid, splits) and wq_splitk_reduce_<act> follows) and workspace bytes,
+ * for a device with cu_count CUs and max_lds bytes of dynamic LDS per
+ * workgroup (MI355X: 256, 163840), with or without a workspace.  align_flags:
+ * TM_WQ_ALIGN_* bits for the pointer alignments of the call.  A diagnostic with
+ * no counterpart in the reference (which compiles one kernel per template); it
+ * lets tests show which kernel family a shape reaches.  Touches no device.
+ * Any of the output pointers may be NULL. */
 #define TM_WQ_ALIGN_XW16 1u /* input and weight 16-byte aligned */
 #define TM_WQ_ALIGN_S16 2u  /* scales 16-byte aligned */
 #define TM_WQ_ALIGN_Z16 4u  /* zeros 16-byte aligned (or no zeros) */
 #define TM_WQ_ALIGN_SZ4 8u  /* scales and zeros 4-byte aligned */
 int tm_wq_plan(int qbits, int M, int N, int K, int group_size, int act_dtype, int scale_dtype,
-               int zero_dtype, unsigned align_flags, int cu_count, size_t max_lds, char* name,
-               size_t name_len, unsigned* grid, unsigned* block, unsigned* lds_bytes);
+               int zero_dtype, unsigned align_flags, int cu_count, size_t max_lds,
+               int with_workspace, char* name, size_t name_len, unsigned* grid, unsigned* block,
+               unsigned* lds_bytes, unsigned* splits, size_t* workspace_bytes);
 /* Dequantised weight tile out[n, k] = round_out((float(q) - z) * s), the
  * per-element arithmetic of _msl_templates.py:2671 (int8) / 2738-2739 (int4).
  * qbits 4 or 8; out_dtype F32/F16/BF16. */

@@ -10,6 +10,7 @@ import torch
 
 import oracle
 import triton_metal_amd as tm
+from triton_metal_amd import _lib
 
 pytestmark = pytest.mark.gpu
 ATOL, RTOL = 2e-2, 1e-2
@@ -511,13 +512,32 @@ def cu_count(dev):
     return torch.cuda.get_device_properties(dev).multi_processor_count
 
 
+def _plain_c_call(qbits, x, w, bias, out, s, z, M, N, K, G=128):
+    """The call through tm_int{4,8}_linear (bias NULL: the plain matmul), the C
+    entry points without a workspace."""
+    L = _lib.lib()
+    dts = {torch.float16: _lib.TM_DT_F16, torch.bfloat16: _lib.TM_DT_BF16,
+           torch.float32: _lib.TM_DT_F32, torch.uint8: _lib.TM_DT_U8, None: _lib.TM_DT_NONE}
+    p = lambda t: None if t is None else t.data_ptr()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    zdt = dts[None if z is None else z.dtype]
+    if qbits == 4:
+        rc = L.tm_int4_linear(p(x), p(w), p(bias), p(out), p(s), p(z), M, N, K, G, dts[x.dtype],
+                              dts[s.dtype], zdt, stream)
+    else:
+        rc = L.tm_int8_linear(p(x), p(w), p(bias), p(out), p(s), p(z), M, N, K, dts[x.dtype],
+                              dts[s.dtype], zdt, stream)
+    _lib.check(rc, "plain C call")
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("case", CASES, ids=case_id)
 def test_dispatch_case(dev, cu_count, case):
     """Each case against the oracle (a column sample when N is large), with the
     bias form on alternate cases; the kernel it reaches is named by tm_wq_plan
     for this device, and on a 256-CU part is the kernel the CPU coverage test
     counts."""
-    qbits, M, N, K, G, act, zeros = case
+    qbits, M, N, K, G, act, zeros, ws = case
     name = plan(case, cu_count)
     if cu_count == 256:
         assert name == plan(case)
@@ -536,7 +556,9 @@ def test_dispatch_case(dev, cu_count, case):
         zi = torch.randint(0, 16, (N, ng), generator=g)
         z = None if zeros is None else zi.to(torch.uint8 if zeros == "u8" else act)
         args = (packed.to(dev), out, s.to(dev), None if z is None else z.to(dev), M, N, K, G)
-        if use_bias:
+        if not ws:
+            _plain_c_call(4, x.to(dev), args[0], None if bias is None else bias.to(dev), *args[1:])
+        elif use_bias:
             tm.int4_linear(x.to(dev), args[0], bias.to(dev), *args[1:])
         else:
             tm.int4_matmul(x.to(dev), *args)
@@ -550,7 +572,9 @@ def test_dispatch_case(dev, cu_count, case):
         elif zeros == "u8":
             z = torch.randint(0, 5, (N,), generator=_gen(seed + 1)).to(torch.uint8)
         args = (w.to(dev), out, s.to(dev), None if z is None else z.to(dev), M, N, K)
-        if use_bias:
+        if not ws:
+            _plain_c_call(8, x.to(dev), args[0], None if bias is None else bias.to(dev), *args[1:])
+        elif use_bias:
             tm.int8_linear(x.to(dev), args[0], bias.to(dev), *args[1:])
         else:
             tm.int8_matmul(x.to(dev), *args)

@@ -14,6 +14,8 @@ from pathlib import Path
 import pytest
 import torch
 
+import triton_metal_amd as tm
+
 from wq_cases import CASES, case_id, plan
 
 ROOT = Path(__file__).resolve().parent.parent
@@ -62,12 +64,14 @@ def _built(stem):
 def wq_kernels(tmp_path_factory):
     tmp = tmp_path_factory.mktemp("co")
     names = set()
-    stems = ["wq_gemm", "wq_gemvp"] + sorted(
+    stems = ["wq_gemm", "wq_gemvp", "wq_splitk"] + sorted(
         p.stem for p in (ROOT / "triton-metal_amd" / "csrc" / "kernels").glob("wq_streamk*.hip"))
     for stem in stems:
         names |= {n for n, _, _ in _kernel_metadata(_built(stem), tmp)}
-    # the dequantised tile and the GEMV's pure-read twin (a measurement kernel)
-    return {n for n in names if n != "wq_dequant" and not n.startswith("wq_read_twin")}
+    # the dequantised tile, the GEMV's pure-read twin (a measurement kernel)
+    # and the split-K reduction (launched after every split-K kernel)
+    return {n for n in names if n != "wq_dequant" and not n.startswith("wq_read_twin")
+            and not n.startswith("wq_splitk_reduce")}
 
 
 def test_cases_cover_every_wq_kernel(wq_kernels):
@@ -86,10 +90,25 @@ def test_m1_k4096_branches(c):
     assert name.startswith("wq_gemv4p_" if c[2] <= 16384 else "wq_gemv4l_"), name
 
 
+def test_split_k_plans():
+    """Split-K only with a workspace: the plan's slices, grid rows and
+    workspace bytes (fp32 slice sums), and the plain C entry points' choice."""
+    d = tm.wq_kernel_for(4, 24, 1040, 20480, zero_dtype=torch.float16, details=True)
+    assert d["name"].endswith("_x16m_c16_k") and d["splits"] == 2
+    assert d["workspace_bytes"] == 2 * 24 * 1040 * 4
+    d0 = tm.wq_kernel_for(4, 24, 1024, 20480, zero_dtype=torch.float16, with_workspace=False,
+                          details=True)
+    assert d0["name"].startswith("wq_tiled_") and d0["splits"] == 1 and d0["workspace_bytes"] == 0
+    # shapes a single launch covers never split, with or without a workspace
+    for args in ((4, 16, 4096, 14336), (8, 16, 4096, 14336), (4, 1, 14336, 4096)):
+        d = tm.wq_kernel_for(*args, details=True)
+        assert d["splits"] == 1 and d["workspace_bytes"] == 0, (args, d)
+
+
 def test_plan_depends_on_cu_count():
     # 14336 rows need 256 workgroups of 56; with 128 CUs the persistent grid
     # would take a second round, so the plan moves to the linear GEMV
-    c = (4, 1, 14336, 4096, 128, torch.float16, "s")
+    c = (4, 1, 14336, 4096, 128, torch.float16, "s", True)
     assert plan(c, 256) == "wq_gemv4p_f16_zs_r14"
     assert plan(c, 128).startswith("wq_gemv4l_")
 

@@ -2,8 +2,10 @@
 tm_int8_matmul can select (ops_gemm.cpp wq_plan), for torch-allocated
 (aligned) buffers on a 256-CU MI355X.
 
-Each case is (qbits, M, N, K, G, act, zeros); zeros is None, "s" (the scale
-dtype) or "u8".  tests/test_wq_dispatch.py checks on the CPU that the cases
+Each case is (qbits, M, N, K, G, act, zeros, ws); zeros is None, "s" (the
+scale dtype) or "u8"; ws says whether the call supplies a workspace (the
+Python operators, tm_wq_matmul_ws: split-K plans allowed) or not (the plain C
+entry points).  tests/test_wq_dispatch.py checks on the CPU that the cases
 reach every instantiated W-only kernel; tests/test_gpu_wq.py runs every case
 on the GPU against the oracle.
 """
@@ -13,8 +15,8 @@ ACTS = (torch.float16, torch.bfloat16)
 ZEROS = (None, "s", "u8")
 
 
-def _each(qbits, M, N, K, G=128, acts=ACTS, zeros=ZEROS):
-    return [(qbits, M, N, K, G, a, z) for a in acts for z in zeros]
+def _each(qbits, M, N, K, G=128, acts=ACTS, zeros=ZEROS, ws=True):
+    return [(qbits, M, N, K, G, a, z, ws) for a in acts for z in zeros]
 
 
 CASES = []
@@ -58,32 +60,44 @@ STREAMK = {
 for qb, shapes in STREAMK.items():
     for M, K, N in shapes:
         CASES += _each(qb, M, N, K)
+# its split-K forms (with a workspace): K past the single-launch limits in
+# two slices, one tile per workgroup; int4 x8 / x16 (K > 32768), x16m
+# (M > 16, K > 16384); int8 x8 / x16 / x16m (K > 16384)
+for qb, M, K in ((4, 5, 40960), (4, 12, 36864), (4, 24, 20480), (8, 4, 20480), (8, 16, 24576),
+                 (8, 40, 32768)):
+    CASES += _each(qb, M, 1040, K)
+# the same kind of shape through the plain C entry points (no workspace, no
+# split): the tiled kernel
+CASES += _each(4, 24, 1024, 20480, acts=(torch.float16,), zeros=("s",), ws=False)
+CASES += _each(8, 16, 1024, 24576, acts=(torch.bfloat16,), zeros=(None,), ws=False)
 # int4 GEMV at K = 8192, 2 <= M <= 8
 CASES += _each(4, 4, 64, 8192)
 # int8 GEMVs, M = 1, K = 4096: linear (fp16) and 8-wave (bf16)
 CASES += _each(8, 1, 64, 4096)
 # skinny (M <= 8, other K or G): int4 without and with vector scale loads
-# (G = 256; K past the long-K kernel's 32768), int8
+# (G = 256; K past the long-K kernel's 32768, no workspace), int8
 CASES += _each(4, 2, 64, 5120, G=256)
-CASES += _each(4, 2, 64, 36864)
+CASES += _each(4, 2, 64, 36864, ws=False)
 CASES += _each(8, 1, 64, 1024)
 # tiled (M > 64 with K past the streaming kernels' 4096; int4 M > 16 with K
-# past 16384)
+# past 16384 and no workspace)
 CASES += _each(4, 80, 64, 8192)
-CASES += _each(4, 20, 64, 20480, acts=(torch.bfloat16,))
+CASES += _each(4, 20, 64, 20480, acts=(torch.bfloat16,), ws=False)
 CASES += _each(8, 80, 64, 4352)
 # general fp32 kernel
-CASES += [(4, 3, 40, 100, 32, torch.float32, None), (8, 3, 40, 100, 1, torch.float32, "s")]
+CASES += [(4, 3, 40, 100, 32, torch.float32, None, True),
+          (8, 3, 40, 100, 1, torch.float32, "s", True)]
 
 
 def case_id(c):
-    q, M, N, K, G, a, z = c
-    return f"q{q}-M{M}-N{N}-K{K}-G{G}-{str(a).split('.')[-1]}-z{z}"
+    q, M, N, K, G, a, z, ws = c
+    return f"q{q}-M{M}-N{N}-K{K}-G{G}-{str(a).split('.')[-1]}-z{z}" + ("" if ws else "-nows")
 
 
 def plan(c, cu_count=256):
     """Kernel name for a case (tm_wq_plan through wq_kernel_for)."""
     import triton_metal_amd as tm
-    q, M, N, K, G, a, z = c
+    q, M, N, K, G, a, z, ws = c
     zdt = None if z is None else (torch.uint8 if z == "u8" else a)
-    return tm.wq_kernel_for(q, M, N, K, G, act_dtype=a, zero_dtype=zdt, cu_count=cu_count)[0]
+    return tm.wq_kernel_for(q, M, N, K, G, act_dtype=a, zero_dtype=zdt, cu_count=cu_count,
+                            with_workspace=ws)[0]

@@ -42,15 +42,22 @@ Kernel& kernel(const std::string& name) {
 // ---- W-only kernel selection ------------------------------------------------
 // A pure function of the problem (sizes, dtypes, pointer alignment, the
 // device's CU count and LDS limit): the launch path and tm_wq_plan share it.
-enum { WQ_ARGS_STD = 0, WQ_ARGS_G = 1, WQ_ARGS_GENERAL = 2 };
+// Split-K plans (split_ok: the caller supplies a workspace) run the split-K
+// form of a kernel over `splits` k-slices, grid (grid, splits), writing fp32
+// [splits][M][N] into the workspace, then wq_splitk_reduce_<act>.
+enum { WQ_ARGS_STD = 0, WQ_ARGS_G = 1, WQ_ARGS_GENERAL = 2, WQ_ARGS_SPLIT = 3 };
 struct WqPlan {
   char name[64];
   unsigned grid, block, lds;
-  int form;  // argument list: WQ_ARGS_*
+  int form;       // argument list: WQ_ARGS_*
+  int splits;     // k-slices (1: no split)
+  size_t ws;      // workspace bytes (split-K plans)
 };
 
 void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, unsigned align,
-             int cus, size_t max_lds, WqPlan* pl) {
+             int cus, size_t max_lds, bool split_ok, WqPlan* pl) {
+  pl->splits = 1;
+  pl->ws = 0;
   auto set = [&](unsigned grid, unsigned block, size_t lds, int form) {
     pl->grid = grid;
     pl->block = block;
@@ -161,23 +168,34 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
   // most 8 waves (int4 K <= 32768, int8 K <= 16384); NT = 1 or 2 16-column
   // tiles per workgroup (one workgroup per CU for the N of a down projection;
   // NT = 2 only where its LDS fits); M > 16 in passes of 16 rows (NT = 1;
-  // int4 K <= 16384, as the first pass's weights stay in registers)
-  if (fast && M <= 64 && K > 4096 && K % CK == 0 && K <= (qbits == 4 ? 32768 : 16384) && sz4 &&
-      (qbits == 8 || G == 128) && (M <= 16 || qbits == 8 || K <= 16384)) {
-    const int nchunk = K / CK;
-    const int nch = nchunk <= 64 && qbits == 4 ? 8 : nchunk <= 128 ? 16 : 32;
+  // int4 K <= 16384, as the first pass's weights stay in registers).  Past
+  // those K, with a workspace: split-K over the fewest slices that fit.
+  if (fast && M <= 64 && K > 4096 && K % CK == 0 && sz4 && (qbits == 8 || G == 128)) {
+    const bool multi = M > 16;
+    const int kmax = qbits == 4 ? (multi ? 16384 : 32768) : 16384;
+    int S = K <= kmax ? 1 : 0;
+    if (!S && split_ok)
+      for (int s2 = 2; s2 <= 64 && !S; ++s2)
+        if (K % (s2 * CK) == 0 && K / s2 <= kmax) S = s2;
+    const int Ks = S ? K / S : K;
+    const int nchunk = Ks / CK;
+    // split-K forms: int4 multi-pass 16 chunks per wave, the others 32
+    const int nch = S > 1 ? (qbits == 4 && multi ? 16 : 32)
+                          : (nchunk <= 64 && qbits == 4 ? 8 : nchunk <= 128 ? 16 : 32);
     const int nwv = (nchunk + nch - 1) / nch;
     const int tiles = N / 16;
-    const bool multi = M > 16;
     const int xr = M <= 8 ? 8 : 16;
-    for (int nt = tiles > cus && !multi ? 2 : 1; nt >= 1; --nt) {
+    for (int nt = S == 1 && tiles > cus && !multi ? 2 : 1; S && nt >= 1; --nt) {
       const size_t slot = (size_t)nt * 1024 + (size_t)xr * 2 * CK;
       const size_t scb = qbits == 4 ? (size_t)512 * nt * (nch / 4) : 1024;
       const size_t slds = (size_t)nwv * (2 * slot + scb + 8 * 64 * sizeof(float));
       if (slds <= max_lds) {
-        snprintf(pl->name, sizeof pl->name, "wq_streamk_q%d_%s_z%c_t%d_x%d%c_c%d", qbits, act, zc,
-                 nt, xr, multi ? 'm' : 's', nch);
-        return set((tiles + nt - 1) / nt, 64 * nwv, slds, WQ_ARGS_STD);
+        snprintf(pl->name, sizeof pl->name, "wq_streamk_q%d_%s_z%c_t%d_x%d%c_c%d%s", qbits, act,
+                 zc, nt, xr, multi ? 'm' : 's', nch, S > 1 ? "_k" : "");
+        set((tiles + nt - 1) / nt, 64 * nwv, slds, S > 1 ? WQ_ARGS_SPLIT : WQ_ARGS_STD);
+        pl->splits = S;
+        pl->ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+        return;
       }
     }
   }
@@ -207,9 +225,18 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
   set((N + 3) / 4, 256, 0, WQ_ARGS_GENERAL);
 }
 
+unsigned wq_align(const void* X, const void* W, const void* S, const void* Z) {
+  unsigned align = 0;
+  if (aligned16(X) && aligned16(W)) align |= TM_WQ_ALIGN_XW16;
+  if (aligned16(S)) align |= TM_WQ_ALIGN_S16;
+  if (!Z || aligned16(Z)) align |= TM_WQ_ALIGN_Z16;
+  if (((uintptr_t)S & 3u) == 0 && (!Z || ((uintptr_t)Z & 3u) == 0)) align |= TM_WQ_ALIGN_SZ4;
+  return align;
+}
+
 int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, const void* Z,
               int M, int N, int K, int G, int adt, int sdt, int zdt, const void* bias,
-              void* stream) {
+              void* workspace, size_t workspace_bytes, void* stream) {
   const char* op = bias ? (qbits == 4 ? "tm_int4_linear" : "tm_int8_linear")
                         : (qbits == 4 ? "tm_int4_matmul" : "tm_int8_matmul");
   if (M < 0 || N < 0 || K < 0) return fail(TM_ERR_INVALID_ARG, "%s: negative size", op);
@@ -227,16 +254,28 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
   if (!api()) return TM_ERR_NO_RUNTIME;
   clear_error();
 
-  unsigned align = 0;
-  if (aligned16(X) && aligned16(W)) align |= TM_WQ_ALIGN_XW16;
-  if (aligned16(S)) align |= TM_WQ_ALIGN_S16;
-  if (!Z || aligned16(Z)) align |= TM_WQ_ALIGN_Z16;
-  if (((uintptr_t)S & 3u) == 0 && (!Z || ((uintptr_t)Z & 3u) == 0)) align |= TM_WQ_ALIGN_SZ4;
+  if (workspace && !aligned16(workspace))
+    return fail(TM_ERR_INVALID_ARG, "%s: workspace must be 16-byte aligned", op);
+  const unsigned align = wq_align(X, W, S, Z);
   WqPlan pl;
-  wq_plan(qbits, M, N, K, G, adt, sdt, zdt, align, cu_count(), (size_t)max_dynamic_lds(), &pl);
+  wq_plan(qbits, M, N, K, G, adt, sdt, zdt, align, cu_count(), (size_t)max_dynamic_lds(),
+          workspace != nullptr, &pl);
+  if (pl.splits > 1 && workspace_bytes < pl.ws)
+    return fail(TM_ERR_INVALID_ARG, "%s: workspace of %zu bytes, this call needs %zu", op,
+                workspace_bytes, pl.ws);
   Kernel& k = kernel(pl.name);
   const dim3 grid(pl.grid), block(pl.block);
   switch (pl.form) {
+    case WQ_ARGS_SPLIT: {
+      float* P = (float*)workspace;
+      int rc = launch(k, dim3(pl.grid, (unsigned)pl.splits), block, pl.lds, stream, X, W, P, S, Z,
+                      M, N, K / pl.splits, K);
+      if (rc) return rc;
+      const size_t quads = (size_t)M * N / 4;
+      return launch(kernel(adt == TM_DT_BF16 ? "wq_splitk_reduce_bf16" : "wq_splitk_reduce_f16"),
+                    dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream, (const float*)P,
+                    Y, bias, M, N, pl.splits);
+    }
     case WQ_ARGS_G:
       return launch(k, grid, block, pl.lds, stream, X, W, Y, S, Z, M, N, K, G, bias);
     case WQ_ARGS_GENERAL:
@@ -323,34 +362,59 @@ int tm_int8_matmul(const void* input, const void* weight, void* output, const vo
                    const void* zeros, int M, int N, int K, int act_dtype, int scale_dtype,
                    int zero_dtype, void* stream) {
   return wq_matmul(8, input, weight, output, scales, zeros, M, N, K, 1, act_dtype, scale_dtype,
-                   zero_dtype, nullptr, stream);
+                   zero_dtype, nullptr, nullptr, 0, stream);
 }
 
 int tm_int4_matmul(const void* input, const void* weight, void* output, const void* scales,
                    const void* zeros, int M, int N, int K, int group_size, int act_dtype,
                    int scale_dtype, int zero_dtype, void* stream) {
   return wq_matmul(4, input, weight, output, scales, zeros, M, N, K, group_size, act_dtype,
-                   scale_dtype, zero_dtype, nullptr, stream);
+                   scale_dtype, zero_dtype, nullptr, nullptr, 0, stream);
 }
 
 int tm_int8_linear(const void* input, const void* weight, const void* bias, void* output,
                    const void* scales, const void* zeros, int M, int N, int K, int act_dtype,
                    int scale_dtype, int zero_dtype, void* stream) {
   return wq_matmul(8, input, weight, output, scales, zeros, M, N, K, 1, act_dtype, scale_dtype,
-                   zero_dtype, bias, stream);
+                   zero_dtype, bias, nullptr, 0, stream);
 }
 
 int tm_int4_linear(const void* input, const void* weight, const void* bias, void* output,
                    const void* scales, const void* zeros, int M, int N, int K, int group_size,
                    int act_dtype, int scale_dtype, int zero_dtype, void* stream) {
   return wq_matmul(4, input, weight, output, scales, zeros, M, N, K, group_size, act_dtype,
-                   scale_dtype, zero_dtype, bias, stream);
+                   scale_dtype, zero_dtype, bias, nullptr, 0, stream);
+}
+
+int tm_wq_matmul_ws(int qbits, const void* input, const void* weight, const void* bias,
+                    void* output, const void* scales, const void* zeros, int M, int N, int K,
+                    int group_size, int act_dtype, int scale_dtype, int zero_dtype,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  if (qbits != 4 && qbits != 8)
+    return fail(TM_ERR_INVALID_ARG, "tm_wq_matmul_ws: qbits=%d (4 or 8)", qbits);
+  return wq_matmul(qbits, input, weight, output, scales, zeros, M, N, K,
+                   qbits == 4 ? group_size : 1, act_dtype, scale_dtype, zero_dtype, bias,
+                   workspace, workspace_bytes, stream);
+}
+
+size_t tm_wq_workspace_bytes(int qbits, const void* input, const void* weight,
+                             const void* scales, const void* zeros, int M, int N, int K,
+                             int group_size, int act_dtype, int scale_dtype, int zero_dtype) {
+  if ((qbits != 4 && qbits != 8) || M <= 0 || N <= 0 || K <= 0 || (qbits == 4 && group_size <= 0))
+    return 0;
+  if (!api()) return 0;
+  WqPlan pl;
+  wq_plan(qbits, M, N, K, qbits == 4 ? group_size : 1, act_dtype, scale_dtype, zero_dtype,
+          wq_align(input, weight, scales, zeros), cu_count(), (size_t)max_dynamic_lds(), true,
+          &pl);
+  return pl.ws;
 }
 
 
 int tm_wq_plan(int qbits, int M, int N, int K, int group_size, int act_dtype, int scale_dtype,
-               int zero_dtype, unsigned align_flags, int cu_count, size_t max_lds, char* name,
-               size_t name_len, unsigned* grid, unsigned* block, unsigned* lds_bytes) {
+               int zero_dtype, unsigned align_flags, int cu_count, size_t max_lds,
+               int with_workspace, char* name, size_t name_len, unsigned* grid, unsigned* block,
+               unsigned* lds_bytes, unsigned* splits, size_t* workspace_bytes) {
   if ((qbits != 4 && qbits != 8) || M <= 0 || N <= 0 || K <= 0 || cu_count <= 0 ||
       (qbits == 4 && group_size <= 0))
     return fail(TM_ERR_INVALID_ARG, "tm_wq_plan: qbits=%d M=%d N=%d K=%d G=%d cus=%d", qbits, M,
@@ -358,11 +422,13 @@ int tm_wq_plan(int qbits, int M, int N, int K, int group_size, int act_dtype, in
   clear_error();
   WqPlan pl;
   wq_plan(qbits, M, N, K, qbits == 4 ? group_size : 1, act_dtype, scale_dtype, zero_dtype,
-          align_flags, cu_count, max_lds, &pl);
+          align_flags, cu_count, max_lds, with_workspace != 0, &pl);
   if (name && name_len) snprintf(name, name_len, "%s", pl.name);
   if (grid) *grid = pl.grid;
   if (block) *block = pl.block;
   if (lds_bytes) *lds_bytes = pl.lds;
+  if (splits) *splits = (unsigned)pl.splits;
+  if (workspace_bytes) *workspace_bytes = pl.ws;
   return 0;
 }
 

@@ -28,6 +28,10 @@
 // int8: y = s (sum x q - z sum x) at the end.  MULTI (M > 16): passes of 16
 // activation rows; the first pass keeps the weight words in registers, the
 // later ones stream only X.
+// Split-K form (SPLIT): workgroup row blockIdx.y takes the k-slice
+// [blockIdx.y K, + K) of rows that are ldk long (X, weights and, int4, the
+// group scales / zero-points offset by it) and writes its fp32 sums, scaled
+// but without bias, to P[blockIdx.y][M][N]; wq_splitk_reduce adds the slices.
 #pragma once
 #include "common.h"
 #include "wq_common.h"
@@ -46,11 +50,11 @@ constexpr int streamk_ahead(int rs, int nch, int c0, int c1, bool first, int i, 
 }
 }  // namespace
 
-template <int QB, bool BF16, int ZDT, int NT, int XR, int NCH, bool MULTI>
+template <int QB, bool BF16, int ZDT, int NT, int XR, int NCH, bool MULTI, bool SPLIT>
 __device__ __forceinline__ void wq_streamk_body(const uint16_t* X, const uint8_t* W,
-                                                uint16_t* __restrict__ Y, const void* S,
-                                                const void* Z, int M, int N, int K,
-                                                const uint16_t* bias) {
+                                                uint16_t* __restrict__ Y, float* __restrict__ P,
+                                                const void* S, const void* Z, int M, int N, int K,
+                                                int ldk, const uint16_t* bias) {
   constexpr int SDT = BF16 ? TM_DT_BF16 : TM_DT_F16;
   constexpr int CK = QB == 4 ? 128 : 64;  // k per chunk: 64 weight bytes of a row
   constexpr int NJ = CK / 32;             // MFMA k-steps per chunk
@@ -72,7 +76,13 @@ __device__ __forceinline__ void wq_streamk_body(const uint16_t* X, const uint8_t
   const int n0 = blockIdx.x * (16 * NT);
   const int nchunk = K / CK;
   const int npass = MULTI ? (M + 15) >> 4 : 1;
-  const size_t rowbytes = QB == 4 ? (size_t)(K >> 1) : (size_t)K;
+  // split-K: this workgroup's k-slice (the whole row otherwise, ldk == K)
+  const int ks0 = SPLIT ? (int)blockIdx.y * K : 0;
+  X += ks0;
+  W += QB == 4 ? ks0 >> 1 : ks0;
+  const size_t rowbytes = QB == 4 ? (size_t)(ldk >> 1) : (size_t)ldk;
+  const size_t srow = (size_t)(ldk / CK);  // int4: groups per row of S / Z
+  const size_t g0 = (size_t)(ks0 / CK);
   const uint8_t* const wl = lds + wave * WB;
   const uint8_t* const scl = wl + RS * SLOT;
   const uint32_t wlo = __builtin_amdgcn_readfirstlane(lds_off(wl));
@@ -89,7 +99,7 @@ __device__ __forceinline__ void wq_streamk_body(const uint16_t* X, const uint8_t
     for (int qq = 0; qq < NQ; ++qq) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const size_t gi = (size_t)min(n0 + 16 * t + l16, N - 1) * nchunk + chunk_of(4 * qq + q);
+        const size_t gi = (size_t)min(n0 + 16 * t + l16, N - 1) * srow + g0 + chunk_of(4 * qq + q);
         const uint32_t dst = slo + 512 * (qq * NT + t);
         dma4((const uint16_t*)S + (gi & ~(size_t)1), dst);
         if constexpr (ZDT == 3) dma4((const uint8_t*)Z + (gi & ~(size_t)3), dst + 256);
@@ -126,7 +136,7 @@ __device__ __forceinline__ void wq_streamk_body(const uint16_t* X, const uint8_t
       const int rr = h * (64 / XPR) + lane / XPR;
       const int pc = (lane % XPR) ^ xsw(rr);
       const int m = min(16 * p + rr, M - 1);
-      dma16(X + (size_t)m * K + CK * c + 8 * pc, sb + NT * 1024 + 1024 * h);
+      dma16(X + (size_t)m * ldk + CK * c + 8 * pc, sb + NT * 1024 + 1024 * h);
     }
   };
   const std::integral_constant<bool, true> first_c;
@@ -213,7 +223,7 @@ __device__ __forceinline__ void wq_streamk_body(const uint16_t* X, const uint8_t
           // dword of lane (l16, i % 4) in block (i / 4, t): this chunk's group
           // of column 16 t + l16
           const uint8_t* sp2 = scl + 512 * ((i / 4) * NT + t) + 4 * (16 * (i % 4) + l16);
-          const size_t gi = (size_t)min(n0 + 16 * t + l16, N - 1) * nchunk + cc;
+          const size_t gi = (size_t)min(n0 + 16 * t + l16, N - 1) * srow + g0 + cc;
           float sc = raw_to_f32<SDT>((uint16_t)(*(const uint32_t*)sp2 >> (16 * (gi & 1))));
           sc = live ? sc : 0.0f;
           float zb = w4_offset<BF16>();
@@ -265,7 +275,10 @@ __device__ __forceinline__ void wq_streamk_body(const uint16_t* X, const uint8_t
         for (int w2 = 0; w2 < nwv; ++w2) v += red[(w2 * 8 + f) * 64 + lane];
         const int F = 8 * r + f, t = F >> 2, e = F & 3;
         const int row = 16 * p + 4 * q + e, col = n0 + 16 * t + l16;
-        if (row < M && col < N) store_out(Y, (size_t)row * N + col, v + bias_at(bias, col, BF16), BF16);
+        if (row < M && col < N) {
+          if constexpr (SPLIT) P[((size_t)blockIdx.y * M + row) * N + col] = v;
+          else store_out(Y, (size_t)row * N + col, v + bias_at(bias, col, BF16), BF16);
+        }
       }
     });
   };
@@ -274,13 +287,23 @@ __device__ __forceinline__ void wq_streamk_body(const uint16_t* X, const uint8_t
     for (int p = 1; p < npass; ++p) run_pass(later_c, p);
 }
 
-// wq_streamk_q<QB>_<act>_z<zs>_t<NT>_x<XR><s|m>_c<NCH>
+// wq_streamk_q<QB>_<act>_z<zs>_t<NT>_x<XR><s|m>_c<NCH>; split-K form with the
+// suffix _k: (X, W, P, S, Z, M, N, K of a slice, ldk), grid (tiles, slices)
 #define TM_STREAMK(QB, BF, ACT, ZS, ZDT, NT, XR, MS, MULTI, NCH)                                   \
   extern "C" __global__ __launch_bounds__(512) void                                                \
       wq_streamk_q##QB##_##ACT##_z##ZS##_t##NT##_x##XR##MS##_c##NCH(                              \
           const uint16_t* X, const uint8_t* W, uint16_t* Y, const void* S, const void* Z, int M,   \
           int N, int K, const uint16_t* bias) {                                                   \
-    wq_streamk_body<QB, BF, ZDT, NT, XR, NCH, MULTI>(X, W, Y, S, Z, M, N, K, bias);               \
+    wq_streamk_body<QB, BF, ZDT, NT, XR, NCH, MULTI, false>(X, W, Y, nullptr, S, Z, M, N, K, K,   \
+                                                            bias);                                \
+  }
+#define TM_STREAMK_SPLIT(QB, BF, ACT, ZS, ZDT, XR, MS, MULTI, NCH)                                 \
+  extern "C" __global__ __launch_bounds__(512) void                                                \
+      wq_streamk_q##QB##_##ACT##_z##ZS##_t1_x##XR##MS##_c##NCH##_k(                               \
+          const uint16_t* X, const uint8_t* W, float* P, const void* S, const void* Z, int M,      \
+          int N, int K, int ldk) {                                                                \
+    wq_streamk_body<QB, BF, ZDT, 1, XR, NCH, MULTI, true>(X, W, nullptr, P, S, Z, M, N, K, ldk,   \
+                                                          nullptr);                               \
   }
 #define TM_STREAMK_Z(QB, BF, ACT, NT, XR, MS, MULTI, NCH)                          \
   TM_STREAMK(QB, BF, ACT, n, -1, NT, XR, MS, MULTI, NCH)                           \
@@ -295,3 +318,16 @@ __device__ __forceinline__ void wq_streamk_body(const uint16_t* X, const uint8_t
   TM_STREAMK_A(QB, NT, 8, s, false, NCH) \
   TM_STREAMK_A(QB, NT, 16, s, false, NCH)
 #define TM_STREAMK_M(QB, NCH) TM_STREAMK_A(QB, 1, 16, m, true, NCH)
+// split-K forms (one 16-column tile per workgroup; the slices supply the
+// workgroups): single pass x8 / x16, multi-pass x16
+#define TM_STREAMK_SPLIT_Z(QB, BF, ACT, XR, MS, MULTI, NCH)                          \
+  TM_STREAMK_SPLIT(QB, BF, ACT, n, -1, XR, MS, MULTI, NCH)                           \
+  TM_STREAMK_SPLIT(QB, BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16), XR, MS, MULTI, NCH) \
+  TM_STREAMK_SPLIT(QB, BF, ACT, u, 3, XR, MS, MULTI, NCH)
+#define TM_STREAMK_SPLIT_A(QB, XR, MS, MULTI, NCH)        \
+  TM_STREAMK_SPLIT_Z(QB, false, f16, XR, MS, MULTI, NCH)  \
+  TM_STREAMK_SPLIT_Z(QB, true, bf16, XR, MS, MULTI, NCH)
+#define TM_STREAMK_KS(QB, NCH)                   \
+  TM_STREAMK_SPLIT_A(QB, 8, s, false, NCH)       \
+  TM_STREAMK_SPLIT_A(QB, 16, s, false, NCH)
+#define TM_STREAMK_KM(QB, NCH) TM_STREAMK_SPLIT_A(QB, 16, m, true, NCH)

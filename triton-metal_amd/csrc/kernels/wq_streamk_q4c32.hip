@@ -5,3 +5,5 @@
 
 TM_STREAMK_S(4, 1, 32)
 TM_STREAMK_S(4, 2, 32)
+// split-K, M <= 16: K above 32768 in slices of at most 32768
+TM_STREAMK_KS(4, 32)

@@ -46,8 +46,12 @@ SIGNATURES = {
     "tm_int8_linear": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp],
     "tm_int4_linear": [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_wq_dequant": [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp],
-    "tm_wq_plan": [i32, i32, i32, i32, i32, i32, i32, i32, u32, i32, sz, C.c_char_p, sz,
-                   C.POINTER(u32), C.POINTER(u32), C.POINTER(u32)],
+    "tm_wq_matmul_ws": [i32, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, vp, sz,
+                        vp],
+    "tm_wq_workspace_bytes": [i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32],
+    "tm_wq_plan": [i32, i32, i32, i32, i32, i32, i32, i32, u32, i32, sz, i32, C.c_char_p, sz,
+                   C.POINTER(u32), C.POINTER(u32), C.POINTER(u32), C.POINTER(u32),
+                   C.POINTER(sz)],
     "tm_wq_repack_gptq": [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp],
     "tm_wq_repack_awq": [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp],
     "tm_matmul": [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp],
@@ -77,6 +81,7 @@ _RESTYPES = {
     "tm_builtin_module_name": C.c_char_p,
     "tm_kda_workspace_size": sz,
     "tm_decode_attention_workspace_size": sz,
+    "tm_wq_workspace_bytes": sz,
 }
 
 _lock = threading.Lock()

@@ -148,9 +148,8 @@ def plan_int8_matmul(input, weight, output, scales, zeros, M, N, K, stream=None)
     _numel_at_least(scales, N, "scales")
     if zeros is not None:
         _numel_at_least(zeros, N, "zeros")
-    args = (_ptr(input), _ptr(weight), _ptr(output), _ptr(scales), _ptr(zeros), M, N, K, adt,
-            _dt(scales, "scales"), _zdt(zeros))
-    return Launch(_lib.lib().tm_int8_matmul, args, "int8_matmul", dev, stream)
+    return _wq_launch(8, input, weight, None, output, scales, zeros, M, N, K, 1, adt,
+                      _dt(scales, "scales"), _zdt(zeros), "int8_matmul", dev, stream)
 
 
 def int8_matmul(input, weight, output, scales, zeros, M, N, K):
@@ -184,28 +183,50 @@ def plan_int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size=1
     _numel_at_least(scales, N * ng, "scales")
     if zeros is not None:
         _numel_at_least(zeros, N * ng, "zeros")
-    args = (_ptr(input), _ptr(weight), _ptr(output), _ptr(scales), _ptr(zeros), M, N, K,
-            group_size, adt, _dt(scales, "scales"), _zdt(zeros))
-    return Launch(_lib.lib().tm_int4_matmul, args, "int4_matmul", dev, stream)
+    return _wq_launch(4, input, weight, None, output, scales, zeros, M, N, K, group_size, adt,
+                      _dt(scales, "scales"), _zdt(zeros), "int4_matmul", dev, stream)
+
+
+def _wq_launch(qbits, input, weight, bias, output, scales, zeros, M, N, K, group_size, adt, sdt,
+               zdt, what, dev, stream):
+    """Bind a validated weight-only call to tm_wq_matmul_ws with the device
+    workspace its plan needs (split-K shapes; none otherwise), allocated here
+    from torch's caching allocator and kept alive with the launch."""
+    L = _lib.lib()
+    ws_bytes = L.tm_wq_workspace_bytes(qbits, _ptr(input), _ptr(weight), _ptr(scales),
+                                       _ptr(zeros), M, N, K, group_size, adt, sdt, zdt)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+    args = (qbits, _ptr(input), _ptr(weight), _ptr(bias), _ptr(output), _ptr(scales),
+            _ptr(zeros), M, N, K, group_size, adt, sdt, zdt, _ptr(ws), ws_bytes)
+    launch = Launch(L.tm_wq_matmul_ws, args, what, dev, stream)
+    launch._keep = ws
+    return launch
 
 
 def wq_kernel_for(qbits, M, N, K, group_size=128, act_dtype=torch.float16, scale_dtype=None,
                   zero_dtype=None, align=_lib.TM_WQ_ALIGN_ALL, cu_count=256,
-                  max_lds=160 * 1024):
+                  max_lds=160 * 1024, with_workspace=True, details=False):
     """Name, grid, block and dynamic LDS bytes of the kernel that an int4 /
     int8 matmul of these sizes and dtypes runs (tm_wq_plan; no device is
     touched).  ``zero_dtype`` is a torch dtype or None (no zero-points);
     ``align`` the TM_WQ_ALIGN_* bits of the call's pointers; the defaults
-    describe torch allocations on one MI355X."""
+    describe torch allocations on one MI355X and the Python operators, which
+    pass a workspace (``with_workspace=False``: the plain C entry points).
+    ``details=True`` returns a dict that adds the split-K slices and the
+    workspace bytes."""
     dts = {None: TM_DT_NONE, torch.uint8: _lib.TM_DT_U8, **_FLOAT_DT}
     adt = dts[act_dtype]
     sdt = dts[scale_dtype if scale_dtype is not None else act_dtype]
     name = C.create_string_buffer(64)
-    grid, block, lds = C.c_uint(), C.c_uint(), C.c_uint()
+    grid, block, lds, splits = C.c_uint(), C.c_uint(), C.c_uint(), C.c_uint()
+    ws = C.c_size_t()
     rc = _lib.lib().tm_wq_plan(qbits, M, N, K, group_size, adt, sdt, dts[zero_dtype], align,
-                               cu_count, max_lds, name, 64, C.byref(grid), C.byref(block),
-                               C.byref(lds))
+                               cu_count, max_lds, int(with_workspace), name, 64, C.byref(grid),
+                               C.byref(block), C.byref(lds), C.byref(splits), C.byref(ws))
     _lib.check(rc, "wq_kernel_for")
+    if details:
+        return dict(name=name.value.decode(), grid=grid.value, block=block.value, lds=lds.value,
+                    splits=splits.value, workspace_bytes=ws.value)
     return name.value.decode(), grid.value, block.value, lds.value
 
 
@@ -220,8 +241,9 @@ def int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size=128):
     return output
 
 
-def _linear_bias(base, bias, input, N, entry, what, stream):
-    """Rebind a validated weight-only matmul launch to its fused-bias entry."""
+def _linear_bias(base, bias, input, N, what, stream):
+    """Rebind a validated weight-only matmul launch with a bias (its fused
+    nn.Linear form; the bias is argument 3 of tm_wq_matmul_ws)."""
     if bias is not None:
         _device_of(input, bias)
         _need_contig(bias, "bias")
@@ -229,13 +251,15 @@ def _linear_bias(base, bias, input, N, entry, what, stream):
             raise TypeError("bias dtype must equal input dtype")
         _numel_at_least(bias, N, "bias")
     a = base._args
-    return Launch(entry, (a[0], a[1], _ptr(bias)) + tuple(a[2:]), what, base.dev, stream)
+    launch = Launch(base._f, a[:3] + (_ptr(bias),) + tuple(a[4:]), what, base.dev, stream)
+    launch._keep = base._keep
+    return launch
 
 
 def plan_int8_linear(input, weight, bias, output, scales, zeros, M, N, K, stream=None) -> Launch:
     """Validate and bind an int8_linear call (see int8_linear)."""
     base = plan_int8_matmul(input, weight, output, scales, zeros, M, N, K, stream)
-    return _linear_bias(base, bias, input, N, _lib.lib().tm_int8_linear, "int8_linear", stream)
+    return _linear_bias(base, bias, input, N, "int8_linear", stream)
 
 
 def int8_linear(input, weight, bias, output, scales, zeros, M, N, K):
@@ -252,7 +276,7 @@ def plan_int4_linear(input, weight, bias, output, scales, zeros, M, N, K, group_
                      stream=None) -> Launch:
     """Validate and bind an int4_linear call (see int4_linear)."""
     base = plan_int4_matmul(input, weight, output, scales, zeros, M, N, K, group_size, stream)
-    return _linear_bias(base, bias, input, N, _lib.lib().tm_int4_linear, "int4_linear", stream)
+    return _linear_bias(base, bias, input, N, "int4_linear", stream)
 
 
 def int4_linear(input, weight, bias, output, scales, zeros, M, N, K, group_size=128):
