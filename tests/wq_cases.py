@@ -23,6 +23,11 @@ CASES = []
 # wide kernels (fp16 activations, M > 64): int4 every zero form, int8 none
 CASES += _each(4, 80, 256, 1024, acts=(torch.float16,))
 CASES += _each(8, 80, 256, 512, acts=(torch.float16,), zeros=(None,))
+# their split-K forms (with a workspace): few tiles (16 slices), and int4 K
+# past 4096 (K = 14336 at N = 4096: 4 slices)
+CASES += _each(4, 96, 1024, 8192, acts=(torch.float16,))
+CASES += _each(8, 96, 1024, 4096, acts=(torch.float16,), zeros=(None,))
+CASES += _each(4, 128, 4096, 14336, acts=(torch.float16,), zeros=("s",))
 # two-tile int4 GEMV, 2 <= M <= 6, K = 4096
 CASES += _each(4, 3, 64, 4096)
 # streaming kernels: x8s (M <= 8), x16s (M <= 16), x16m (M <= 64 / 128)

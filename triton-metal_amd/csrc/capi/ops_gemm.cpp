@@ -72,18 +72,38 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
                     (qbits == 8 || G % 128 == 0) && N % 16 == 0 && K > 0 && a16;
   const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
   const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
-  // wide kernel: fp16 activations, M > 64, 64 x 128 output blocks
+  // wide kernel: fp16 activations, M > 64, 64 x 128 output blocks.  With a
+  // workspace, split-K over S k-slices when its tiles would fill less than
+  // half the CUs, or when int4 K exceeds the 4096 whose scales fit in LDS
   if (fast && adt == TM_DT_F16 && M > 64 && N % 128 == 0 && s16 && z16 &&
-      ((qbits == 4 && G == 128 && K % 512 == 0 && K <= 4096) ||
+      ((qbits == 4 && G == 128 && K % 512 == 0) ||
        (qbits == 8 && zdt == TM_DT_NONE && K % 128 == 0))) {
     const int ns = qbits == 4 ? 3 : 4, ck = qbits == 4 ? 64 : 32;
-    size_t wl = (size_t)ns * 4 * (64 * 2 * ck + 4096);  // ring stages
-    if (qbits == 4)  // scales and zero-points of the 128 columns
-      wl += (size_t)2 * K + (zdt == TM_DT_NONE ? 0 : zdt == TM_DT_U8 ? (size_t)K : (size_t)2 * K);
-    if (wl <= max_lds) {
-      snprintf(pl->name, sizeof pl->name, "wq_wide_q%d_f16_z%c", qbits, zc);
-      const int mtl = (M + 63) / 64, ntl = N / 128;
-      return set(8 * mtl * ((ntl + 7) / 8), 512, wl, WQ_ARGS_STD);
+    const int unit = qbits == 4 ? 512 : 128;  // slice granularity
+    const int mtl = (M + 63) / 64, ntl = N / 128;
+    const long tiles = (long)mtl * ntl;
+    int S = 1;
+    if (split_ok && (tiles < cus / 2 || (qbits == 4 && K > 4096))) {
+      S = 0;
+      const long want = std::max<long>((cus + tiles - 1) / tiles, qbits == 4 ? (K + 4095) / 4096 : 1);
+      for (int s2 = (int)std::min<long>(want, 16); s2 <= 16 && !S; ++s2)
+        if (K % (s2 * unit) == 0 && (qbits == 8 || K / s2 <= 4096)) S = s2;
+      if (!S && !(qbits == 4 && K > 4096)) S = 1;
+    }
+    const int Ks = S ? K / S : K;
+    if (S && (qbits == 8 || Ks <= 4096)) {
+      size_t wl = (size_t)ns * 4 * (64 * 2 * ck + 4096);  // ring stages
+      if (qbits == 4)  // scales and zero-points of the 128 columns
+        wl += (size_t)2 * Ks +
+              (zdt == TM_DT_NONE ? 0 : zdt == TM_DT_U8 ? (size_t)Ks : (size_t)2 * Ks);
+      if (wl <= max_lds) {
+        snprintf(pl->name, sizeof pl->name, "wq_wide_q%d_f16_z%c%s", qbits, zc,
+                 S > 1 ? "_k" : "");
+        set(8 * mtl * ((ntl + 7) / 8), 512, wl, S > 1 ? WQ_ARGS_SPLIT : WQ_ARGS_STD);
+        pl->splits = S;
+        pl->ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+        return;
+      }
     }
   }
   // two-tile int4 GEMV: 2 <= M <= 6 at K = 4096 (from M = 7 on the streaming

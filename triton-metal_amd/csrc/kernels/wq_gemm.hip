@@ -1302,12 +1302,17 @@ TM_DEV u4_t w4_exact(uint32_t w, float z, float s) {
 }
 }  // namespace
 
-template <int QB, int ZDT>
+// Split-K form (SPLIT): workgroup row blockIdx.y takes the k-slice
+// [blockIdx.y K, + K) of rows ldk long and writes its fp32 sums (scaled, no
+// bias) to P[blockIdx.y][M][N]; the int4 scale / zero-point rows of the slice
+// are gathered row by row (ldk / 128 groups apart).
+template <int QB, int ZDT, bool SPLIT = false>
 __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
                                              const uint8_t* __restrict__ W,
                                              uint16_t* __restrict__ Y, const uint16_t* S,
                                              const void* Z, int M, int N, int K,
-                                             const uint16_t* bias) {
+                                             const uint16_t* bias, int ldk = 0,
+                                             float* __restrict__ P = nullptr) {
   constexpr int CK = QB == 4 ? 64 : 32;  // k per chunk and K-quarter
   constexpr int KS = CK / 16;            // MFMA k-steps per chunk
   constexpr int NS = QB == 4 ? 3 : 4;    // ring stages
@@ -1332,8 +1337,13 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
   if (nb >= ntl) return;
   const int m0 = mb * 64, n0 = nb * 128;
   const int NC = K / (4 * CK);  // stages of 4 CK k
-  const size_t wrow = QB == 4 ? (size_t)(K >> 1) : (size_t)K;
-  const int ng = K >> 7;  // int4 groups per row
+  if constexpr (!SPLIT) ldk = K;
+  const int ks0 = SPLIT ? (int)blockIdx.y * K : 0;
+  X += ks0;
+  W += QB == 4 ? ks0 >> 1 : ks0;
+  const size_t wrow = QB == 4 ? (size_t)(ldk >> 1) : (size_t)ldk;
+  const int ng = K >> 7;  // int4 groups per row of the slice
+  const size_t ngr = (size_t)(ldk >> 7), g0 = (size_t)(ks0 >> 7);  // groups per row of S / Z
   const uint32_t lbase = __builtin_amdgcn_readfirstlane(lds_off(lds));
   const uint32_t sbase = lbase + NS * ST;  // int4 scales, then zero-points
   constexpr int ZRB = ZDT == 3 ? 1 : 2;    // zero-point bytes
@@ -1343,12 +1353,28 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
   // a multiple of 512 only)
   if constexpr (QB == 4) {
     const int sb = 128 * ng * 2, zb = 128 * ng * ZRB;
-    for (int o = 1024 * wave; o < sb; o += 8192)
-      if (o + 16 * lane < sb) dma16((const uint8_t*)(S + (size_t)n0 * ng) + o + 16 * lane, sbase + o);
-    if constexpr (ZDT >= 0)
-      for (int o = 1024 * wave; o < zb; o += 8192)
-        if (o + 16 * lane < zb)
-          dma16((const uint8_t*)Z + (size_t)n0 * ng * ZRB + o + 16 * lane, sbase + sb + o);
+    if constexpr (!SPLIT) {
+      for (int o = 1024 * wave; o < sb; o += 8192)
+        if (o + 16 * lane < sb) dma16((const uint8_t*)(S + (size_t)n0 * ng) + o + 16 * lane, sbase + o);
+      if constexpr (ZDT >= 0)
+        for (int o = 1024 * wave; o < zb; o += 8192)
+          if (o + 16 * lane < zb)
+            dma16((const uint8_t*)Z + (size_t)n0 * ng * ZRB + o + 16 * lane, sbase + sb + o);
+    } else {
+      // dword d of the [row][group] block: row d / (ng * ZB / 4) (K % 512 == 0
+      // keeps every row a whole number of dwords)
+      const int sdw = ng / 2, zdw = ng * ZRB / 4;
+      for (int o = 64 * wave; o < 128 * sdw; o += 512) {
+        const int d = o + lane, r = d / sdw, j = d - r * sdw;
+        if (d < 128 * sdw) dma4(S + (size_t)(n0 + r) * ngr + g0 + 2 * j, sbase + 4 * o);
+      }
+      if constexpr (ZDT >= 0)
+        for (int o = 64 * wave; o < 128 * zdw; o += 512) {
+          const int d = o + lane, r = d / zdw, j = d - r * zdw;
+          if (d < 128 * zdw)
+            dma4((const uint8_t*)Z + ((size_t)(n0 + r) * ngr + g0) * ZRB + 4 * j, sbase + sb + 4 * o);
+        }
+    }
   }
 
   // ---- copies of one stage (chunk c of every K-quarter: 4 CK consecutive k).
@@ -1360,7 +1386,7 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
 #pragma unroll
   for (int i = 0; i < DX; ++i) {
     const int rr = XLR * (DX * wave + i) + lane / (XRB / 16), sl = lane % (XRB / 16);
-    xsrc[i] = (const uint8_t*)(X + (size_t)min(m0 + rr, M - 1) * K) + 16 * (sl ^ (rr & 15));
+    xsrc[i] = (const uint8_t*)(X + (size_t)min(m0 + rr, M - 1) * ldk) + 16 * (sl ^ (rr & 15));
     xdst[i] = 1024 * (DX * wave + i);
   }
   const uint8_t* wsrc[2];
@@ -1546,11 +1572,14 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
   const int col = n0 + 64 * wn + 32 * t + r32;
   float sc = 1.0f;
   if constexpr (QB == 8) sc = f16_bits_to_f32(S[col]);
-  const float bv = bias_at(bias, col, false);
+  const float bv = SPLIT ? 0.0f : bias_at(bias, col, false);
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int row = m0 + 32 * mt + 8 * (e >> 2) + 4 * h + (e & 3);
-    if (row < M) Y[(size_t)row * N + col] = f32_to_f16_bits(y[e] * sc + bv);
+    if (row < M) {
+      if constexpr (SPLIT) P[((size_t)blockIdx.y * M + row) * N + col] = y[e] * sc;
+      else Y[(size_t)row * N + col] = f32_to_f16_bits(y[e] * sc + bv);
+    }
   }
 }
 
@@ -1663,6 +1692,17 @@ TM_WIDE(4, n, -1)
 TM_WIDE(4, s, TM_DT_F16)
 TM_WIDE(4, u, 3)
 TM_WIDE(8, n, -1)
+// split-K forms: (X, W, P, S, Z, M, N, K of a slice, ldk), grid (tiles, slices)
+#define TM_WIDE_K(QB, ZS, ZDT)                                                                  \
+  extern "C" __global__ __launch_bounds__(512) void wq_wide_q##QB##_f16_z##ZS##_k(              \
+      const uint16_t* X, const uint8_t* W, float* P, const uint16_t* S, const void* Z, int M,   \
+      int N, int K, int ldk) {                                                                  \
+    wq_wide_body<QB, ZDT, true>(X, W, nullptr, S, Z, M, N, K, nullptr, ldk, P);                 \
+  }
+TM_WIDE_K(4, n, -1)
+TM_WIDE_K(4, s, TM_DT_F16)
+TM_WIDE_K(4, u, 3)
+TM_WIDE_K(8, n, -1)
 
 // Streaming kernels: wq_stream_q<QB>_<act>_z<zs>_x<XR><s|m> (s: single pass,
 // M <= XR; m: multi-pass, M <= 128).  Scales are of the activation dtype.
