@@ -311,7 +311,10 @@ def w4a16_wide_k(dev, M, K=14336, N=4096, G=128):
     import triton_metal_amd as tm
     w = w4a16(dev, M, K=K, N=N, G=G)
     w["config"]["workload"] = f"w4a16_m{M}_k{K}"
-    w["config"]["kernel"] = tm.wq_kernel_for(4, M, N, K, G, zero_dtype=torch.float16)[0]
+    d = tm.wq_kernel_for(4, M, N, K, G, zero_dtype=torch.float16, details=True)
+    w["config"]["kernel"] = d["name"]
+    if d["splits"] > 1:
+        w["config"]["k_slices"] = d["splits"]
     return w
 
 
@@ -320,7 +323,10 @@ def w8a16_wide_k(dev, M, K=14336, N=4096):
     import triton_metal_amd as tm
     w = w8a16(dev, M, K=K, N=N)
     w["config"]["workload"] = f"w8a16_m{M}_k{K}"
-    w["config"]["kernel"] = tm.wq_kernel_for(8, M, N, K)[0]
+    d = tm.wq_kernel_for(8, M, N, K, details=True)
+    w["config"]["kernel"] = d["name"]
+    if d["splits"] > 1:
+        w["config"]["k_slices"] = d["splits"]
     return w
 
 
@@ -338,7 +344,12 @@ EXTRA = {"hbm_copy": hbm_copy,
          "w4a16_m64_k14336": lambda d: w4a16_wide_k(d, 64),
          "w4a16_m8_k28672": lambda d: w4a16_wide_k(d, 8, K=28672, N=8192),
          "w8a16_m1_k14336": lambda d: w8a16_wide_k(d, 1),
-         "w8a16_m16_k14336": lambda d: w8a16_wide_k(d, 16)}
+         "w8a16_m16_k14336": lambda d: w8a16_wide_k(d, 16),
+         # split-K plans (the Python operators pass a workspace)
+         "w4a16_m128_k14336": lambda d: w4a16_wide_k(d, 128),
+         "w8a16_m128_k14336": lambda d: w8a16_wide_k(d, 128),
+         "w4a16_m32_k28672": lambda d: w4a16_wide_k(d, 32, K=28672, N=8192),
+         "w8a16_m16_k28672": lambda d: w8a16_wide_k(d, 16, K=28672, N=8192)}
 
 
 def time_workload(w, steps, warmup, graph=True, budget_s=2.0, min_replays=100):
