@@ -20,13 +20,13 @@ def _each(qbits, M, N, K, G=128, acts=ACTS, zeros=ZEROS, ws=True):
 
 
 CASES = []
-# wide kernels (fp16 activations, M > 64): int4 every zero form, int8 none
+# wide kernels (M > 64): int4 (fp16) every zero form, int8 (fp16, bf16) none
 CASES += _each(4, 80, 256, 1024, acts=(torch.float16,))
-CASES += _each(8, 80, 256, 512, acts=(torch.float16,), zeros=(None,))
+CASES += _each(8, 80, 256, 512, zeros=(None,))
 # their split-K forms (with a workspace): few tiles (16 slices), and int4 K
 # past 4096 (K = 14336 at N = 4096: 4 slices)
 CASES += _each(4, 96, 1024, 8192, acts=(torch.float16,))
-CASES += _each(8, 96, 1024, 4096, acts=(torch.float16,), zeros=(None,))
+CASES += _each(8, 96, 1024, 4096, zeros=(None,))
 CASES += _each(4, 128, 4096, 14336, acts=(torch.float16,), zeros=("s",))
 # two-tile int4 GEMV, 2 <= M <= 6, K = 4096
 CASES += _each(4, 3, 64, 4096)

@@ -72,11 +72,12 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
                     (qbits == 8 || G % 128 == 0) && N % 16 == 0 && K > 0 && a16;
   const char* act = adt == TM_DT_BF16 ? "bf16" : "f16";
   const char zc = zdt == TM_DT_NONE ? 'n' : (zdt == TM_DT_U8 ? 'u' : 's');
-  // wide kernel: fp16 activations, M > 64, 64 x 128 output blocks.  With a
-  // workspace, split-K over S k-slices when its tiles would fill less than
-  // half the CUs, or when int4 K exceeds the 4096 whose scales fit in LDS
-  if (fast && adt == TM_DT_F16 && M > 64 && N % 128 == 0 && s16 && z16 &&
-      ((qbits == 4 && G == 128 && K % 512 == 0) ||
+  // wide kernel: M > 64, 64 x 128 output blocks (int4: fp16 activations;
+  // int8: fp16 or bf16).  With a workspace, split-K over S k-slices when its
+  // tiles would fill less than half the CUs, or when int4 K exceeds the 4096
+  // whose scales fit in LDS
+  if (fast && M > 64 && N % 128 == 0 && s16 && z16 &&
+      ((qbits == 4 && adt == TM_DT_F16 && G == 128 && K % 512 == 0) ||
        (qbits == 8 && zdt == TM_DT_NONE && K % 128 == 0))) {
     const int ns = qbits == 4 ? 3 : 4, ck = qbits == 4 ? 64 : 32;
     const int unit = qbits == 4 ? 512 : 128;  // slice granularity
@@ -97,7 +98,7 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
         wl += (size_t)2 * Ks +
               (zdt == TM_DT_NONE ? 0 : zdt == TM_DT_U8 ? (size_t)Ks : (size_t)2 * Ks);
       if (wl <= max_lds) {
-        snprintf(pl->name, sizeof pl->name, "wq_wide_q%d_f16_z%c%s", qbits, zc,
+        snprintf(pl->name, sizeof pl->name, "wq_wide_q%d_%s_z%c%s", qbits, act, zc,
                  S > 1 ? "_k" : "");
         set(8 * mtl * ((ntl + 7) / 8), 512, wl, S > 1 ? WQ_ARGS_SPLIT : WQ_ARGS_STD);
         pl->splits = S;

@@ -1306,13 +1306,17 @@ TM_DEV u4_t w4_exact(uint32_t w, float z, float s) {
 // [blockIdx.y K, + K) of rows ldk long and writes its fp32 sums (scaled, no
 // bias) to P[blockIdx.y][M][N]; the int4 scale / zero-point rows of the slice
 // are gathered row by row (ldk / 128 groups apart).
-template <int QB, int ZDT, bool SPLIT = false>
+// BF16: bf16 activations, int8 only (q is exact in bf16 and the per-channel
+// scale multiplies the fp32 sums; an int4 operand dequantised to bf16 would
+// round every weight to 8 bits).
+template <int QB, int ZDT, bool SPLIT = false, bool BF16 = false>
 __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
                                              const uint8_t* __restrict__ W,
                                              uint16_t* __restrict__ Y, const uint16_t* S,
                                              const void* Z, int M, int N, int K,
                                              const uint16_t* bias, int ldk = 0,
                                              float* __restrict__ P = nullptr) {
+  static_assert(!BF16 || QB == 8, "bf16 wide kernel: int8 only");
   constexpr int CK = QB == 4 ? 64 : 32;  // k per chunk and K-quarter
   constexpr int KS = CK / 16;            // MFMA k-steps per chunk
   constexpr int NS = QB == 4 ? 3 : 4;    // ring stages
@@ -1538,13 +1542,13 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
       } else {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-          b[t] = s == 0 ? w8_operand<false>(braw[t].x, braw[t].y)
-                        : w8_operand<false>(braw[t].z, braw[t].w);
+          b[t] = s == 0 ? w8_operand<BF16>(braw[t].x, braw[t].y)
+                        : w8_operand<BF16>(braw[t].z, braw[t].w);
       }
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) acc[mt][t] = mfma32<false>(a[mt], b[t], acc[mt][t]);
+        for (int t = 0; t < 2; ++t) acc[mt][t] = mfma32<BF16>(a[mt], b[t], acc[mt][t]);
     }
   }
 
@@ -1571,14 +1575,14 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
   }
   const int col = n0 + 64 * wn + 32 * t + r32;
   float sc = 1.0f;
-  if constexpr (QB == 8) sc = f16_bits_to_f32(S[col]);
-  const float bv = SPLIT ? 0.0f : bias_at(bias, col, false);
+  if constexpr (QB == 8) sc = BF16 ? bf16_bits_to_f32(S[col]) : f16_bits_to_f32(S[col]);
+  const float bv = SPLIT ? 0.0f : bias_at(bias, col, BF16);
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int row = m0 + 32 * mt + 8 * (e >> 2) + 4 * h + (e & 3);
     if (row < M) {
       if constexpr (SPLIT) P[((size_t)blockIdx.y * M + row) * N + col] = y[e] * sc;
-      else Y[(size_t)row * N + col] = f32_to_f16_bits(y[e] * sc + bv);
+      else store_out(Y, (size_t)row * N + col, y[e] * sc + bv, BF16);
     }
   }
 }
@@ -1682,27 +1686,26 @@ TM_WQ_Z(tiled, 8, false, f16, , )
 TM_WQ_Z(tiled, 8, true, bf16, , )
 
 // Wide kernels (fp16 activations): wq_wide_q4_f16_z{n,s,u}, wq_wide_q8_f16_zn
-#define TM_WIDE(QB, ZS, ZDT)                                                                  \
-  extern "C" __global__ __launch_bounds__(512) void wq_wide_q##QB##_f16_z##ZS(               \
+#define TM_WIDE(QB, BF, ACT, ZS, ZDT)                                                        \
+  extern "C" __global__ __launch_bounds__(512) void wq_wide_q##QB##_##ACT##_z##ZS(             \
       const uint16_t* X, const uint8_t* W, uint16_t* Y, const uint16_t* S, const void* Z,    \
       int M, int N, int K, const uint16_t* bias) {                                            \
-    wq_wide_body<QB, ZDT>(X, W, Y, S, Z, M, N, K, bias);                                      \
+    wq_wide_body<QB, ZDT, false, BF>(X, W, Y, S, Z, M, N, K, bias);                           \
   }
-TM_WIDE(4, n, -1)
-TM_WIDE(4, s, TM_DT_F16)
-TM_WIDE(4, u, 3)
-TM_WIDE(8, n, -1)
 // split-K forms: (X, W, P, S, Z, M, N, K of a slice, ldk), grid (tiles, slices)
-#define TM_WIDE_K(QB, ZS, ZDT)                                                                  \
-  extern "C" __global__ __launch_bounds__(512) void wq_wide_q##QB##_f16_z##ZS##_k(              \
+#define TM_WIDE_K(QB, BF, ACT, ZS, ZDT)                                                         \
+  extern "C" __global__ __launch_bounds__(512) void wq_wide_q##QB##_##ACT##_z##ZS##_k(          \
       const uint16_t* X, const uint8_t* W, float* P, const uint16_t* S, const void* Z, int M,   \
       int N, int K, int ldk) {                                                                  \
-    wq_wide_body<QB, ZDT, true>(X, W, nullptr, S, Z, M, N, K, nullptr, ldk, P);                 \
+    wq_wide_body<QB, ZDT, true, BF>(X, W, nullptr, S, Z, M, N, K, nullptr, ldk, P);             \
   }
-TM_WIDE_K(4, n, -1)
-TM_WIDE_K(4, s, TM_DT_F16)
-TM_WIDE_K(4, u, 3)
-TM_WIDE_K(8, n, -1)
+// fp16: int4 every zero-point form, int8 without zero-points; bf16: int8
+#define TM_WIDE_ALL(M_)                                       \
+  M_(4, false, f16, n, -1) M_(4, false, f16, s, TM_DT_F16)    \
+  M_(4, false, f16, u, 3) M_(8, false, f16, n, -1)            \
+  M_(8, true, bf16, n, -1)
+TM_WIDE_ALL(TM_WIDE)
+TM_WIDE_ALL(TM_WIDE_K)
 
 // Streaming kernels: wq_stream_q<QB>_<act>_z<zs>_x<XR><s|m> (s: single pass,
 // M <= XR; m: multi-pass, M <= 128).  Scales are of the activation dtype.
