@@ -583,3 +583,79 @@ def test_dispatch_case(dev, cu_count, case):
     if use_bias:
         ref = ref + np32(bias)[cols][None, :].astype(np.float64)
     check_close(out.cpu()[:, cols], ref)
+
+
+# --- split-K: the workspace contract and graph replays -----------------------------
+SPLIT_SHAPES = {"streamk": (24, 1040, 20480), "wide": (128, 1024, 14336)}
+
+
+def _split_problem(dev, shape, seed):
+    M, N, K = shape
+    x, _, packed, s, z = make_int4_problem(M, N, K, 128, seed=seed)
+    return [t.to(dev) for t in (x, packed, s, z)]
+
+
+@pytest.mark.parametrize("kind", list(SPLIT_SHAPES))
+def test_split_k_workspace_contract(dev, kind):
+    """tm_wq_matmul_ws: a split-K plan refuses a workspace smaller than
+    tm_wq_workspace_bytes (nothing launched), runs with exactly that many
+    bytes, and without a workspace takes the single-launch plan; the three
+    results agree with the oracle, and the split and unsplit sums to within
+    the output rounding."""
+    M, N, K = SPLIT_SHAPES[kind]
+    x, packed, s, z = _split_problem(dev, SPLIT_SHAPES[kind], seed=61)
+    L = _lib.lib()
+    args = (_lib.TM_DT_F16, _lib.TM_DT_F16, _lib.TM_DT_F16)
+    need = L.tm_wq_workspace_bytes(4, x.data_ptr(), packed.data_ptr(), s.data_ptr(), z.data_ptr(),
+                                   M, N, K, 128, *args)
+    assert need == tm.wq_kernel_for(4, M, N, K, zero_dtype=torch.float16,
+                                    details=True)["workspace_bytes"] > 0
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = torch.full((M, N), 7.0, dtype=torch.float16, device=dev)
+    small = torch.empty(need - 16, dtype=torch.uint8, device=dev)
+    rc = L.tm_wq_matmul_ws(4, x.data_ptr(), packed.data_ptr(), None, out.data_ptr(), s.data_ptr(),
+                           z.data_ptr(), M, N, K, 128, *args, small.data_ptr(), need - 16, stream)
+    torch.cuda.synchronize()
+    assert rc == _lib.TM_ERR_INVALID_ARG and "workspace" in _lib.last_error()
+    assert bool((out == 7.0).all()), "nothing may run when the workspace is refused"
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    rc = L.tm_wq_matmul_ws(4, x.data_ptr(), packed.data_ptr(), None, out.data_ptr(), s.data_ptr(),
+                           z.data_ptr(), M, N, K, 128, *args, ws.data_ptr(), need, stream)
+    assert rc == 0
+    plain = torch.empty_like(out)
+    _plain_c_call(4, x, packed, None, plain, s, z, M, N, K)
+    ref = oracle.int4_matmul(np32(x.cpu()), packed.cpu().numpy(), np32(s.cpu()), np32(z.cpu()),
+                             M, N, K, 128)
+    check_close(out.cpu(), ref)
+    check_close(plain.cpu(), ref)
+    diff = (out.float() - plain.float()).abs().max().item()
+    assert diff <= 2 ** -10 * plain.float().abs().max().item() + 1e-3, diff
+
+
+@pytest.mark.parametrize("kind", list(SPLIT_SHAPES))
+def test_split_k_graph_replays_track_new_inputs(dev, kind):
+    """A split-K call (two launches and the workspace the plan holds) captured
+    in a HIP graph and replayed three times with new inputs copied in and eager
+    work in between: every replay equals the eager call bit for bit."""
+    M, N, K = SPLIT_SHAPES[kind]
+    x, packed, s, z = _split_problem(dev, SPLIT_SHAPES[kind], seed=71)
+    out = torch.empty(M, N, dtype=torch.float16, device=dev)
+    plan = tm.plan_int4_matmul(x, packed, out, s, z, M, N, K, 128)
+    assert plan._keep is not None  # the split plan's workspace
+    plan()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    with torch.cuda.graph(graph, stream=cap):
+        plan(torch.cuda.current_stream().cuda_stream)
+    for seed in (72, 73, 74):
+        new = _split_problem(dev, SPLIT_SHAPES[kind], seed=seed)
+        for dst, src in zip((x, packed, s, z), new):
+            dst.copy_(src)
+        eager = torch.empty_like(out)
+        tm.int4_matmul(*new[:2], eager, *new[2:], M, N, K, 128)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {seed}"
+    del graph

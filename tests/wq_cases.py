@@ -20,9 +20,11 @@ def _each(qbits, M, N, K, G=128, acts=ACTS, zeros=ZEROS, ws=True):
 
 
 CASES = []
-# wide kernels (M > 64): int4 (fp16) every zero form, int8 (fp16, bf16) none
-CASES += _each(4, 80, 256, 1024, acts=(torch.float16,))
-CASES += _each(8, 80, 256, 512, zeros=(None,))
+# wide kernels (M > 64): int4 (fp16) every zero form, int8 (fp16, bf16) none;
+# their one-launch forms through the plain C entry points (with a workspace
+# these few tiles would split K)
+CASES += _each(4, 80, 256, 1024, acts=(torch.float16,), ws=False)
+CASES += _each(8, 80, 256, 512, zeros=(None,), ws=False)
 # their split-K forms (with a workspace): few tiles (16 slices), and int4 K
 # past 4096 (K = 14336 at N = 4096: 4 slices)
 CASES += _each(4, 96, 1024, 8192, acts=(torch.float16,))

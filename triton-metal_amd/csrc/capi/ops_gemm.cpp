@@ -86,9 +86,15 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
     int S = 1;
     if (split_ok && (tiles < cus / 2 || (qbits == 4 && K > 4096))) {
       S = 0;
-      const long want = std::max<long>((cus + tiles - 1) / tiles, qbits == 4 ? (K + 4095) / 4096 : 1);
-      for (int s2 = (int)std::min<long>(want, 16); s2 <= 16 && !S; ++s2)
-        if (K % (s2 * unit) == 0 && (qbits == 8 || K / s2 <= 4096)) S = s2;
+      // the largest valid slice count up to the one that fills the CUs, else
+      // the smallest above it (int4: at least K / 4096 slices)
+      const int smin = qbits == 4 ? (K + 4095) / 4096 : 1;
+      const int want = (int)std::min<long>(std::max<long>((cus + tiles - 1) / tiles, smin), 16);
+      auto ok = [&](int s2) { return K % (s2 * unit) == 0 && (qbits == 8 || K / s2 <= 4096); };
+      for (int s2 = want; s2 >= std::max(smin, 2) && !S; --s2)
+        if (ok(s2)) S = s2;
+      for (int s2 = want + 1; s2 <= 16 && !S; ++s2)
+        if (ok(s2)) S = s2;
       if (!S && !(qbits == 4 && K > 4096)) S = 1;
     }
     const int Ks = S ? K / S : K;
