@@ -336,6 +336,9 @@ EXTRA = {"hbm_copy": hbm_copy,
          "w4a16_m1_read_twin_w": lambda d: w4a16_read_twin(d, weights_only=True),
          "flash_causal_constdata": lambda d: flash(d, True, const_data=True),
          "flash_full_constdata": lambda d: flash(d, False, const_data=True),
+         # 256 x 256 tiles with fewer workgroups than CUs (40 and 32 tiles)
+         "dense_2560x4096x4096": lambda d: dense(d, 2560, 4096, 4096),
+         "dense_2048x4096x4096": lambda d: dense(d, 2048, 4096, 4096),
          "w4a16_m1_k14336": lambda d: w4a16_wide_k(d, 1),
          "w4a16_m16_k14336": lambda d: w4a16_wide_k(d, 16),
          "w4a16_m8_k14336": lambda d: w4a16_wide_k(d, 8),

@@ -241,12 +241,12 @@ def test_matmul_small_tiles_padded_leading_dims(dev, ldc_pad):
     assert (got[:, N:] == 0).all()  # the padding columns of C are untouched
 
 
-# --- 256 x 256 tiles (M, N multiples of 256 with at least 192 tiles, K % 64 == 0) ----
+# --- 256 x 256 tiles (M, N multiples of 256 with at least 32 tiles, K % 64 == 0) -----
 def _sample(n, k, seed):
     return np.sort(np.random.default_rng(seed).choice(n, k, replace=False))
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 3072, 128), (3072, 4096, 192)])
+@pytest.mark.parametrize("M,N,K", [(4096, 3072, 128), (3072, 4096, 192), (2048, 1024, 320)])
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("out32", [False, True])
 def test_matmul_large_tiles(dev, M, N, K, dt, out32):

@@ -336,11 +336,14 @@ int dense(const void* A, const void* B, void* C, const void* bias, int M, int N,
   bool mfma = is_half(idt) && (odt == idt || odt == TM_DT_F32) && K % 8 == 0 && lda % 8 == 0 &&
               ldb % 8 == 0 && aligned16(A) && aligned16(B) && (bt || N % 8 == 0);
   if (mfma) {
-    // 256 x 256 tiles (gemm_big.hip) for large aligned problems: at least 192
-    // tiles, so that most CUs get one; the 32-bit copy offsets of a tile
-    // (up to 256 rows of A / B^T, 64 rows of B) must fit
+    // 256 x 256 tiles (gemm_big.hip) for aligned problems from 32 tiles on:
+    // one such workgroup per CU beats four 128 x 128 ones over the same
+    // outputs even when most CUs stay idle (one box, fp16, K = 4096: 2048 x
+    // 3072 78 against 125 us, 2560 x 4096 84 against 241; at 16 tiles the
+    // smaller tiles win, 140 against 147 us); the 32-bit copy offsets of a
+    // tile (up to 256 rows of A / B^T, 64 rows of B) must fit
     const long t256 = (M % 256 == 0 && N % 256 == 0) ? (long)(M / 256) * (N / 256) : 0;
-    if (t256 >= 192 && K % 64 == 0 && 256LL * lda * 2 < (1LL << 32) &&
+    if (t256 >= 32 && K % 64 == 0 && 256LL * lda * 2 < (1LL << 32) &&
         (bt ? 256LL : 64LL) * ldb * 2 < (1LL << 32)) {
       char name[96];
       snprintf(name, sizeof name, "gemm_t256_%s_%s_%s%s", bt ? "nt" : "nn",

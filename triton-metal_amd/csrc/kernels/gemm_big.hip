@@ -17,9 +17,11 @@
 // MFMAs, with one barrier per step.
 // LDS layouts (16-byte pieces, XOR-swizzled so the operand reads spread over
 // the banks):
-//   A, and B of nt:  [256 rows][64 k], row = 8 pieces, piece p of row r at
-//                    p ^ (r & 7); operands by ds_read_b128 (row l % 32,
-//                    k = 8 (l / 32) + e);
+//   A, and B of nt:  [256 rows][64 k], row = 8 pieces (128 bytes, so the
+//                    64 banks hold two rows), piece p of row r at
+//                    p ^ ((r >> 1) & 7): the 16 rows of one 16-lane read phase
+//                    land in 16 different 16-byte bank groups; operands by
+//                    ds_read_b128 (row l % 32, k = 8 (l / 32) + e);
 //   B of nn:         [64 k][256 n], row = 32 pieces, piece p of row k at
 //                    p ^ 4 (k & 3); operands by two ds_read_b64_tr_b16 (lane
 //                    l: column l % 32, rows k = 8 (l / 32) + e), the order of
@@ -32,6 +34,9 @@ constexpr int GB_BM = 256, GB_BN = 256, GB_BK = 64;
 
 typedef short gb_s4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) gb_s4_t gb_lds_s4_t;
+
+// XOR swizzle of the 128-byte rows of the A (and nt B) tiles
+TM_DEV int gb_sw(int r) { return (r >> 1) & 7; }
 
 TM_DEV u2_t gb_tr16(const uint16_t* p) {
   gb_s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((gb_lds_s4_t*)(p));
@@ -68,9 +73,9 @@ __device__ __forceinline__ void gemm_big_body(const uint16_t* __restrict__ A,
   for (int i = 0; i < 4; ++i) {
     const int blk = 4 * wave + i;
     const int r = 8 * blk + (lane >> 3), ph = lane & 7;  // row-major [256][64] tile
-    aoff[i] = 2u * (uint32_t)(r * lda + 8 * (ph ^ (r & 7)));
+    aoff[i] = 2u * (uint32_t)(r * lda + 8 * (ph ^ gb_sw(r)));
     if constexpr (BT) {
-      boff[i] = 2u * (uint32_t)(r * ldb + 8 * (ph ^ (r & 7)));
+      boff[i] = 2u * (uint32_t)(r * ldb + 8 * (ph ^ gb_sw(r)));
     } else {
       const int kr = 2 * blk + (lane >> 5), pc = lane & 31;  // [64][256] tile
       boff[i] = 2u * (uint32_t)(kr * ldb + 8 * (pc ^ (4 * (kr & 3))));
@@ -103,13 +108,13 @@ __device__ __forceinline__ void gemm_big_body(const uint16_t* __restrict__ A,
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       const int r = 128 * wm + 32 * rt + l32, p = 2 * kk + h32;
-      ao[rt] = *(const u4_t*)(as + r * GB_BK + 8 * (p ^ (r & 7)));
+      ao[rt] = *(const u4_t*)(as + r * GB_BK + 8 * (p ^ gb_sw(r)));
     }
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       if constexpr (BT) {
         const int r = 64 * wn + 32 * ct + l32, p = 2 * kk + h32;
-        bo[ct] = *(const u4_t*)(bs + r * GB_BK + 8 * (p ^ (r & 7)));
+        bo[ct] = *(const u4_t*)(bs + r * GB_BK + 8 * (p ^ gb_sw(r)));
       } else {
         const int c = 64 * wn + 32 * ct + tr_c, pc = c >> 3, co = c & 7;
         const int k0 = 16 * kk + tr_k, k1 = k0 + 4;
