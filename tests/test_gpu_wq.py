@@ -633,6 +633,27 @@ def test_split_k_workspace_contract(dev, kind):
 
 
 @pytest.mark.parametrize("kind", list(SPLIT_SHAPES))
+def test_split_k_output_view_off_8_byte_alignment(dev, kind):
+    """The split-K reduction writes an output view that starts 2 bytes into
+    its buffer (so its 4-output groups are not 8-byte aligned), with a bias:
+    bit for bit the aligned call's result, and the element before the view is
+    untouched."""
+    M, N, K = SPLIT_SHAPES[kind]
+    x, packed, s, z = _split_problem(dev, SPLIT_SHAPES[kind], seed=67)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(68)) * 0.1).half().to(dev)
+    assert tm.wq_kernel_for(4, M, N, K, zero_dtype=torch.float16, details=True)["splits"] > 1
+    ref = torch.empty(M, N, dtype=torch.float16, device=dev)
+    tm.int4_linear(x, packed, bias, ref, s, z, M, N, K, 128)
+    buf = torch.full((M * N + 1,), 3.0, dtype=torch.float16, device=dev)
+    out = buf[1:].view(M, N)
+    assert out.data_ptr() % 8 == 2
+    tm.int4_linear(x, packed, bias, out, s, z, M, N, K, 128)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert buf[0].item() == 3.0
+
+
+@pytest.mark.parametrize("kind", list(SPLIT_SHAPES))
 def test_split_k_graph_replays_track_new_inputs(dev, kind):
     """A split-K call (two launches and the workspace the plan holds) captured
     in a HIP graph and replayed three times with new inputs copied in and eager

@@ -3,7 +3,8 @@
 //   Y[m, n] = round(sum_s P[s][m][n] + bias[n])
 // in the activation dtype, the bias added to the fp32 sum before the output
 // rounding as in the single-launch kernels.  Four consecutive outputs per
-// thread (N % 4 == 0); grid = ceil(M N / 1024) workgroups of 256.
+// thread (N % 4 == 0), one 8-byte store where the output allows it;
+// grid = ceil(M N / 1024) workgroups of 256.
 #include "common.h"
 #include "wq_common.h"
 
@@ -21,6 +22,11 @@ __device__ __forceinline__ void wq_splitk_reduce_body(const float* __restrict__ 
   if (bias) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) v[c] += bias_at(bias, n + c, BF16);
+  }
+  if (((uintptr_t)(Y + i) & 7u) != 0) {  // an output view not 8-byte aligned
+#pragma unroll
+    for (int c = 0; c < 4; ++c) store_out(Y, i + c, v[c], BF16);
+    return;
   }
   u2_t w;
   if constexpr (BF16) {
