@@ -262,6 +262,19 @@ int tm_dot(const void* A, const void* B, void* C, const void* Z, const void* W, 
  * input, weight, C, [bias], M, N, K). */
 int tm_linear(const void* input, const void* weight, const void* bias, void* output, int M,
               int N, int K, int in_dtype, int out_dtype, void* stream);
+/* The kernel a tm_matmul (trans_b = 0: B [K, N]) or tm_linear (trans_b = 1:
+ * weight [N, K], has_bias) call of these sizes, leading dimensions, dtypes and
+ * pointer alignment runs, with its grid and block: the selection those entry
+ * points make, as a pure function (no device is touched).  No counterpart in
+ * the reference, whose callers pick a template; for tests and callers that
+ * want to know the path.  FP8 inputs (the general dot) give
+ * TM_ERR_UNSUPPORTED.  tm_linear's leading dimensions are K, K, N. */
+#define TM_GEMM_ALIGN_AB16 1u /* A and B 16-byte aligned */
+#define TM_GEMM_ALIGN_C16 2u  /* C 16-byte aligned */
+#define TM_GEMM_ALIGN_ALL 3u
+int tm_gemm_plan(int M, int N, int K, int lda, int ldb, int ldc, int trans_b, int has_bias,
+                 int in_dtype, int out_dtype, unsigned align_flags, char* name, size_t name_len,
+                 unsigned* grid, unsigned* block);
 
 /* ---- flash attention forward -------------------------------------------------
  * O = softmax(scale * Q K^T [+ causal mask]) V per (batch, head), fp32 softmax

@@ -305,3 +305,28 @@ def test_fp32_general_path(dev):
     tm.matmul(A.to(dev), B.to(dev), C, M, N, K)
     np.testing.assert_allclose(C.cpu().numpy(), oracle.matmul(A.numpy(), B.numpy()),
                                atol=1e-5, rtol=1e-5)
+
+
+# --- every dense kernel the selection can make (tests/gemm_cases.py) ------------
+from gemm_cases import CASES as DENSE_CASES, case_id as dense_case_id, plan as dense_plan  # noqa: E402
+
+
+@pytest.mark.parametrize("case", DENSE_CASES, ids=[dense_case_id(c) for c in DENSE_CASES])
+def test_dispatch_case(dev, case):
+    form, M, N, K, dt, out, bias = case
+    print(f"[dense] {dense_case_id(case)} -> {dense_plan(case)}", flush=True)
+    seed = M + 3 * N + 7 * K
+    A = _rand((M, K), seed, dt)
+    B = _rand((N, K) if form == "nt" else (K, N), seed + 1, dt)
+    b = _rand((N,), seed + 2, dt) if bias else None
+    C = torch.full((M, N), 3.0, dtype=out, device=dev)
+    if form == "nt":
+        tm.fused_linear(A.to(dev), B.to(dev), C, None if b is None else b.to(dev), M, N, K)
+        ref = oracle.linear(A.float().numpy(), B.float().numpy(),
+                            None if b is None else b.float().numpy())
+    else:
+        tm.matmul(A.to(dev), B.to(dev), C, M, N, K)
+        ref = oracle.matmul(A.float().numpy(), B.float().numpy())
+    torch.cuda.synchronize()
+    atol, rtol = (1e-3, 1e-4) if out == torch.float32 else (ATOL, RTOL)
+    np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=atol, rtol=rtol)

@@ -313,6 +313,69 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
   }
 }
 
+// ---- dense kernel selection ---------------------------------------------------
+// A pure function of the call (sizes, leading dimensions, dtypes, whether B is
+// the transposed nn.Linear weight and a bias is given, pointer alignment): the
+// launch path and tm_gemm_plan share it.  FP8 inputs are not planned here (they
+// run the general dot).
+struct GemmPlan {
+  char name[96];
+  unsigned grid, block;
+  bool general;  // gemm_general's argument list
+};
+
+void gemm_plan(int M, int N, int K, int lda, int ldb, int ldc, bool bt, bool bias, int idt,
+               int odt, bool ab16, bool c16, GemmPlan* pl) {
+  pl->general = false;
+  const char* dt = idt == TM_DT_BF16 ? "bf16" : "f16";
+  const char* od = odt == TM_DT_F32 ? "f32" : "same";
+  const char* bs = (bt && bias) ? "_bias" : "";
+  const bool mfma = is_half(idt) && (odt == idt || odt == TM_DT_F32) && K % 8 == 0 &&
+                    lda % 8 == 0 && ldb % 8 == 0 && ab16 && (bt || N % 8 == 0);
+  if (mfma) {
+    // 256 x 256 tiles (gemm_big.hip) for aligned problems from 32 tiles on:
+    // one such workgroup per CU beats four 128 x 128 ones over the same
+    // outputs even when most CUs stay idle (one box, fp16, K = 4096: 2048 x
+    // 3072 78 against 125 us, 2560 x 4096 84 against 241; at 16 tiles the
+    // smaller tiles win, 140 against 147 us); the 32-bit copy offsets of a
+    // tile (up to 256 rows of A / B^T, 64 rows of B) must fit
+    const long t256 = (M % 256 == 0 && N % 256 == 0) ? (long)(M / 256) * (N / 256) : 0;
+    if (t256 >= 32 && K % 64 == 0 && 256LL * lda * 2 < (1LL << 32) &&
+        (bt ? 256LL : 64LL) * ldb * 2 < (1LL << 32)) {
+      snprintf(pl->name, sizeof pl->name, "gemm_t256_%s_%s_%s%s", bt ? "nt" : "nn", dt, od, bs);
+      pl->grid = (unsigned)t256;
+      pl->block = 512;
+      return;
+    }
+    const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+    // small aligned problems with K = 256 or 512 (C1): 32 x 32 tiles, K split
+    // over the workgroup's 4 waves, 16-byte copies and 8 / 16-byte stores
+    if (t128 < 256 && M % 32 == 0 && N % 32 == 0 && (K == 256 || K == 512) && c16 &&
+        ldc % 4 == 0) {
+      snprintf(pl->name, sizeof pl->name, "gemm_s32k%d_%s_%s_%s%s", K / 4, bt ? "nt" : "nn", dt,
+               od, bs);
+      pl->grid = (unsigned)((M / 32) * (N / 32));
+      pl->block = 256;
+      return;
+    }
+    const char* tile;
+    const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    int bm;
+    if (t128 >= 256) { tile = "t128"; bm = 128; }
+    else if (t64 >= 192) { tile = "t64"; bm = 64; }
+    else if (K <= 512) { tile = "t32k"; bm = 32; }  // one load stage
+    else { tile = "t32"; bm = 32; }
+    snprintf(pl->name, sizeof pl->name, "gemm_%s_%s_%s_%s%s", tile, bt ? "nt" : "nn", dt, od, bs);
+    pl->grid = (unsigned)(((M + bm - 1) / bm) * ((N + bm - 1) / bm));
+    pl->block = 256;
+    return;
+  }
+  snprintf(pl->name, sizeof pl->name, "gemm_general");
+  pl->grid = (unsigned)(((size_t)M * N + 255) / 256);
+  pl->block = 256;
+  pl->general = true;
+}
+
 int dense(const void* A, const void* B, void* C, const void* bias, int M, int N, int K, int lda,
           int ldb, int ldc, bool bt, int idt, int odt, void* stream) {
   const char* op = bt ? "tm_linear" : "tm_matmul";
@@ -333,55 +396,14 @@ int dense(const void* A, const void* B, void* C, const void* bias, int M, int N,
     return fail(TM_ERR_INVALID_ARG, "%s: leading dimension too small", op);
   if (!api()) return TM_ERR_NO_RUNTIME;
   clear_error();
-  bool mfma = is_half(idt) && (odt == idt || odt == TM_DT_F32) && K % 8 == 0 && lda % 8 == 0 &&
-              ldb % 8 == 0 && aligned16(A) && aligned16(B) && (bt || N % 8 == 0);
-  if (mfma) {
-    // 256 x 256 tiles (gemm_big.hip) for aligned problems from 32 tiles on:
-    // one such workgroup per CU beats four 128 x 128 ones over the same
-    // outputs even when most CUs stay idle (one box, fp16, K = 4096: 2048 x
-    // 3072 78 against 125 us, 2560 x 4096 84 against 241; at 16 tiles the
-    // smaller tiles win, 140 against 147 us); the 32-bit copy offsets of a
-    // tile (up to 256 rows of A / B^T, 64 rows of B) must fit
-    const long t256 = (M % 256 == 0 && N % 256 == 0) ? (long)(M / 256) * (N / 256) : 0;
-    if (t256 >= 32 && K % 64 == 0 && 256LL * lda * 2 < (1LL << 32) &&
-        (bt ? 256LL : 64LL) * ldb * 2 < (1LL << 32)) {
-      char name[96];
-      snprintf(name, sizeof name, "gemm_t256_%s_%s_%s%s", bt ? "nt" : "nn",
-               idt == TM_DT_BF16 ? "bf16" : "f16", odt == TM_DT_F32 ? "f32" : "same",
-               (bt && bias) ? "_bias" : "");
-      return launch(kernel(name), dim3((unsigned)t256), dim3(512), 0, stream, A, B, C, bias, M,
-                    N, K, lda, ldb, ldc);
-    }
-    long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
-    // small aligned problems with K = 256 or 512 (C1): 32 x 32 tiles, K split
-    // over the workgroup's 4 waves, 16-byte copies and 8 / 16-byte stores
-    if (t128 < 256 && M % 32 == 0 && N % 32 == 0 && (K == 256 || K == 512) && aligned16(C) &&
-        ldc % 4 == 0) {
-      char name[96];
-      snprintf(name, sizeof name, "gemm_s32k%d_%s_%s_%s%s", K / 4, bt ? "nt" : "nn",
-               idt == TM_DT_BF16 ? "bf16" : "f16", odt == TM_DT_F32 ? "f32" : "same",
-               (bt && bias) ? "_bias" : "");
-      return launch(kernel(name), dim3((unsigned)((M / 32) * (N / 32))), dim3(256), 0, stream, A,
-                    B, C, bias, M, N, K, lda, ldb, ldc);
-    }
-    const char* tile;
-    long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
-    int bm;
-    if (t128 >= 256) { tile = "t128"; bm = 128; }
-    else if (t64 >= 192) { tile = "t64"; bm = 64; }
-    else if (K <= 512) { tile = "t32k"; bm = 32; }  // one load stage
-    else { tile = "t32"; bm = 32; }
-    char name[96];
-    snprintf(name, sizeof name, "gemm_%s_%s_%s_%s%s", tile, bt ? "nt" : "nn",
-             idt == TM_DT_BF16 ? "bf16" : "f16", odt == TM_DT_F32 ? "f32" : "same",
-             (bt && bias) ? "_bias" : "");
-    int grid = ((M + bm - 1) / bm) * ((N + bm - 1) / bm);
-    return launch(kernel(name), dim3(grid), dim3(256), 0, stream, A, B, C, bias, M, N, K, lda,
-                  ldb, ldc);
-  }
-  size_t total = (size_t)M * N;
-  return launch(kernel("gemm_general"), dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                stream, A, B, C, bias, M, N, K, lda, ldb, ldc, bt ? 1 : 0, idt, odt);
+  GemmPlan pl;
+  gemm_plan(M, N, K, lda, ldb, ldc, bt, bias != nullptr, idt, odt, aligned16(A) && aligned16(B),
+            aligned16(C), &pl);
+  if (pl.general)
+    return launch(kernel(pl.name), dim3(pl.grid), dim3(pl.block), 0, stream, A, B, C, bias, M, N,
+                  K, lda, ldb, ldc, bt ? 1 : 0, idt, odt);
+  return launch(kernel(pl.name), dim3(pl.grid), dim3(pl.block), 0, stream, A, B, C, bias, M, N,
+                K, lda, ldb, ldc);
 }
 
 }  // namespace
@@ -459,6 +481,28 @@ int tm_wq_plan(int qbits, int M, int N, int K, int group_size, int act_dtype, in
   if (lds_bytes) *lds_bytes = pl.lds;
   if (splits) *splits = (unsigned)pl.splits;
   if (workspace_bytes) *workspace_bytes = pl.ws;
+  return 0;
+}
+
+int tm_gemm_plan(int M, int N, int K, int lda, int ldb, int ldc, int trans_b, int has_bias,
+                 int in_dtype, int out_dtype, unsigned align_flags, char* name, size_t name_len,
+                 unsigned* grid, unsigned* block) {
+  const bool bt = trans_b != 0;
+  if (M <= 0 || N <= 0 || K <= 0 || lda < K || ldc < N || (bt ? ldb < K : ldb < N))
+    return fail(TM_ERR_INVALID_ARG, "tm_gemm_plan: M=%d N=%d K=%d lda=%d ldb=%d ldc=%d", M, N, K,
+                lda, ldb, ldc);
+  if (!is_float(in_dtype) || !is_float(out_dtype))
+    return fail(in_dtype >= TM_DT_FP8_E4M3 && in_dtype <= TM_DT_FP8_E5M2B16 ? TM_ERR_UNSUPPORTED
+                                                                            : TM_ERR_INVALID_ARG,
+                "tm_gemm_plan: dtypes %d -> %d (FP8 inputs run the general dot)", in_dtype,
+                out_dtype);
+  clear_error();
+  GemmPlan pl;
+  gemm_plan(M, N, K, lda, ldb, ldc, bt, bt && has_bias != 0, in_dtype, out_dtype,
+            (align_flags & TM_GEMM_ALIGN_AB16) != 0, (align_flags & TM_GEMM_ALIGN_C16) != 0, &pl);
+  if (name && name_len) snprintf(name, name_len, "%s", pl.name);
+  if (grid) *grid = pl.grid;
+  if (block) *block = pl.block;
   return 0;
 }
 

@@ -23,6 +23,7 @@ TM_ERR_INVALID_ARG, TM_ERR_UNSUPPORTED, TM_ERR_NO_RUNTIME, TM_ERR_NOT_FOUND, TM_
     -1, -2, -3, -4, -5)
 TM_WQ_ALIGN_XW16, TM_WQ_ALIGN_S16, TM_WQ_ALIGN_Z16, TM_WQ_ALIGN_SZ4 = 1, 2, 4, 8
 TM_WQ_ALIGN_ALL = 15
+TM_GEMM_ALIGN_AB16, TM_GEMM_ALIGN_C16, TM_GEMM_ALIGN_ALL = 1, 2, 3
 
 vp, i32, u32, sz = C.c_void_p, C.c_int, C.c_uint, C.c_size_t
 
@@ -56,6 +57,8 @@ SIGNATURES = {
     "tm_wq_repack_awq": [vp, vp, vp, i32, i32, i32, vp, vp, vp, vp],
     "tm_matmul": [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp],
     "tm_linear": [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp],
+    "tm_gemm_plan": [i32, i32, i32, i32, i32, i32, i32, i32, i32, i32, u32, C.c_char_p, sz,
+                     C.POINTER(u32), C.POINTER(u32)],
     "tm_matmul_2d": [vp, vp, vp, vp, vp, vp, i32, i32, sz, sz, sz, i32, i32, vp],
     "tm_matmul_swizzled": [vp, vp, vp, vp, vp, vp, i32, i32, sz, sz, sz, i32, i32, i32, vp],
     "tm_dot": [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, C.POINTER(C.c_longlong), i32, i32,

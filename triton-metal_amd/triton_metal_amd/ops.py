@@ -381,6 +381,27 @@ def plan_matmul(A, B, C, M, N, K, stream=None) -> Launch:
     return Launch(_lib.lib().tm_matmul, args, "matmul_kernel", dev, stream)
 
 
+def gemm_kernel_for(M, N, K, lda=None, ldb=None, ldc=None, trans_b=False, bias=False,
+                    in_dtype=torch.float16, out_dtype=None, align=_lib.TM_GEMM_ALIGN_ALL):
+    """Name, grid and block of the kernel a dense matmul (``trans_b=False``:
+    B [K, N], as ``matmul``) or linear (``trans_b=True``: weight [N, K], as
+    ``fused_linear``, with or without ``bias``) of these sizes runs
+    (tm_gemm_plan; no device is touched).  Leading dimensions default to the
+    contiguous ones; ``align`` holds the TM_GEMM_ALIGN_* bits of the call's
+    pointers (torch allocations: all)."""
+    lda = K if lda is None else lda
+    ldb = (K if trans_b else N) if ldb is None else ldb
+    ldc = N if ldc is None else ldc
+    out_dtype = in_dtype if out_dtype is None else out_dtype
+    name = C.create_string_buffer(96)
+    grid, block = C.c_uint(), C.c_uint()
+    rc = _lib.lib().tm_gemm_plan(M, N, K, lda, ldb, ldc, int(trans_b), int(bias),
+                                 _FLOAT_DT[in_dtype], _FLOAT_DT[out_dtype], align, name, 96,
+                                 C.byref(grid), C.byref(block))
+    _lib.check(rc, "gemm_kernel_for")
+    return name.value.decode(), grid.value, block.value
+
+
 def matmul(A, B, C, M, N, K):
     """C[M,N] = A[M,K] @ B[K,N] (row-major, contiguous), fp32 accumulation.
 
