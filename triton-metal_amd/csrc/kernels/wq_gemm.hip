@@ -1589,8 +1589,11 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
 
 // ----------------------------------------------------------------------------
 // General kernel: any M, N, K (int4: K even), any dtypes.  One wave per
-// column n; lanes stride over k; fp32 arithmetic exactly as the reference
-// template: w = (float(q) - z) * s; acc += x * w.
+// column n; fp32 arithmetic exactly as the reference template:
+// w = (float(q) - z) * s; acc += x * w.  The lanes take 8 consecutive k at a
+// time (one 4-byte int4 / 8-byte int8 load where K % 8 == 0 and the row start
+// allows it), and each weight, once dequantised, serves a block of up to 8
+// activation rows, so a row of weights is read ceil(M / 8) times, not M.
 // ----------------------------------------------------------------------------
 __device__ __forceinline__ void st_any(void* p, size_t i, int dt, float v) {
   switch (dt) {
@@ -1600,33 +1603,134 @@ __device__ __forceinline__ void st_any(void* p, size_t i, int dt, float v) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void wq_general(
-    const void* __restrict__ X, const uint8_t* __restrict__ W, void* __restrict__ Y,
-    const void* __restrict__ S, const void* __restrict__ Z, int M, int N, int K, int G, int qbits,
-    int xdt, int sdt, int zdt, const void* __restrict__ bias) {
+template <int XDT, int MB>
+__device__ __forceinline__ void wq_general_body(const void* __restrict__ X,
+                                                const uint8_t* __restrict__ W,
+                                                void* __restrict__ Y, const void* __restrict__ S,
+                                                const void* __restrict__ Z, int M, int N, int K,
+                                                int G, int qbits, int sdt, int zdt,
+                                                const void* __restrict__ bias) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int ngroups = (qbits == 4) ? (K + G - 1) / G : 1;
-  for (int m = 0; m < M; ++m) {
-    float acc = 0.0f;
-    for (int k = lane; k < K; k += 64) {
-      float qv;
-      size_t si;
-      if (qbits == 4) {
-        uint8_t byte = W[(size_t)n * (K / 2) + k / 2];
-        qv = (float)((k & 1) ? ((byte >> 4) & 0xF) : (byte & 0xF));
-        si = (size_t)n * ngroups + k / G;
-      } else {
-        qv = (float)(int8_t)W[(size_t)n * K + k];
-        si = (size_t)n;
+  const uint8_t* wr = W + (size_t)n * (qbits == 4 ? (size_t)(K / 2) : (size_t)K);
+  const bool wvec = K % 8 == 0 && ((uintptr_t)wr & (qbits == 4 ? 3u : 7u)) == 0;
+  // 8 activations of a row as one 16-byte load (16-bit) or two (fp32)
+  const bool xvec = K % 8 == 0 && ((uintptr_t)X & 15u) == 0;
+  const bool group8 = qbits == 8 || G % 8 == 0;  // 8 consecutive k share a scale
+  for (int m0 = 0; m0 < M; m0 += MB) {
+    float acc[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[i] = 0.0f;
+    // one row: several steps' loads in flight at once
+    constexpr int KU = MB == 1 ? 4 : 1;
+#pragma unroll KU
+    for (int k0 = 8 * lane; k0 < K; k0 += 512) {
+      // loads first: weights, scale / zero-point, the block's activations
+      uint32_t wlo = 0, whi = 0;
+      if (wvec) {
+        if (qbits == 4) {
+          wlo = *(const uint32_t*)(wr + k0 / 2);
+        } else {
+          const uint2 v = *(const uint2*)(wr + k0);
+          wlo = v.x;
+          whi = v.y;
+        }
       }
-      float w = (qv - ld_scalar(Z, si, zdt)) * ld_scalar(S, si, sdt);
-      acc += ld_scalar(X, (size_t)m * K + k, xdt) * w;
+      float sc = 0.0f, zp = 0.0f;
+      if (group8) {
+        const size_t si = qbits == 4 ? (size_t)n * ngroups + k0 / G : (size_t)n;
+        sc = ld_scalar(S, si, sdt);
+        zp = ld_scalar(Z, si, zdt);
+      }
+      float xv[MB][8];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[i][e] = 0.0f;
+        if (m0 + i >= M) continue;
+        const size_t xo = (size_t)(m0 + i) * K + k0;
+        if (xvec) {
+          if constexpr (XDT == TM_DT_F32) {
+            const f4_t lo = *(const f4_t*)((const float*)X + xo);
+            const f4_t hi = *(const f4_t*)((const float*)X + xo + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              xv[i][e] = lo[e];
+              xv[i][4 + e] = hi[e];
+            }
+          } else {
+            const u4_t v = *(const u4_t*)((const uint16_t*)X + xo);
+            const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const uint32_t hbits = (wd[e / 2] >> (16 * (e & 1))) & 0xFFFFu;
+              xv[i][e] = XDT == TM_DT_F16 ? f16_bits_to_f32((uint16_t)hbits)
+                                          : bf16_bits_to_f32((uint16_t)hbits);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (k0 + e < K) xv[i][e] = ld_typed<XDT>(X, xo + e);
+        }
+      }
+      float w[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int k = k0 + e;
+        w[e] = 0.0f;
+        if (k < K) {
+          float qv;
+          if (qbits == 4) {
+            const uint32_t b = wvec ? wlo >> (4 * e) : (uint32_t)wr[k / 2] >> (4 * (k & 1));
+            qv = (float)(b & 0xF);
+          } else {
+            const uint32_t b = wvec ? (e < 4 ? wlo : whi) >> (8 * (e & 3)) : (uint32_t)wr[k];
+            qv = (float)(int8_t)(b & 0xFF);
+          }
+          if (!group8) {
+            const size_t si = (size_t)n * ngroups + k / G;
+            sc = ld_scalar(S, si, sdt);
+            zp = ld_scalar(Z, si, zdt);
+          }
+          w[e] = (qv - zp) * sc;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[i] += xv[i][e] * w[e];
     }
-    acc = wave_sum(acc);
-    if (lane == 0) st_any(Y, (size_t)m * N + n, xdt, acc + (bias ? ld_scalar(bias, n, xdt) : 0.0f));
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      if (m0 + i < M) {
+        const float sum = wave_sum(acc[i]);
+        if (lane == 0)
+          st_any(Y, (size_t)(m0 + i) * N + n, XDT,
+                 sum + (bias ? ld_typed<XDT>(bias, n) : 0.0f));
+      }
+    }
   }
+}
+
+extern "C" __global__ __launch_bounds__(256) void wq_general(
+    const void* __restrict__ X, const uint8_t* __restrict__ W, void* __restrict__ Y,
+    const void* __restrict__ S, const void* __restrict__ Z, int M, int N, int K, int G, int qbits,
+    int xdt, int sdt, int zdt, const void* __restrict__ bias) {
+  // a pass serves 8 activation rows (1 when there is one)
+#define TM_WQ_GENERAL_MB(XDT)                                                         \
+  if (M == 1) wq_general_body<XDT, 1>(X, W, Y, S, Z, M, N, K, G, qbits, sdt, zdt, bias); \
+  else wq_general_body<XDT, 8>(X, W, Y, S, Z, M, N, K, G, qbits, sdt, zdt, bias);
+  if (xdt == TM_DT_F32) {
+    TM_WQ_GENERAL_MB(TM_DT_F32)
+  } else if (xdt == TM_DT_F16) {
+    TM_WQ_GENERAL_MB(TM_DT_F16)
+  } else {
+    TM_WQ_GENERAL_MB(TM_DT_BF16)
+  }
+#undef TM_WQ_GENERAL_MB
 }
 
 // ----------------------------------------------------------------------------
