@@ -30,9 +30,15 @@ for fam, (M, N, K) in FAMILIES.items():
             CASES.append(("nn", M, N, K, dt, out, False))
             for bias in (False, True):
                 CASES.append(("nt", M, N, K, dt, out, bias))
-# the general kernel: fp32 inputs, and 16-bit inputs with K % 8 != 0
-CASES += [("nn", 37, 53, 29, F32, F32, False), ("nt", 37, 53, 29, F32, F32, True),
-          ("nn", 37, 53, 29, F16, F16, False), ("nt", 40, 48, 20, BF16, F32, True)]
+# fp32 inputs (the fp32-MFMA 64-tile kernel), every output dtype, sizes that
+# are not multiples of its tiles
+F32_SHAPE = (150, 130, 70)
+for out in (F32, F16, BF16):
+    CASES.append(("nn", *F32_SHAPE, F32, out, False))
+    for bias in (False, True):
+        CASES.append(("nt", *F32_SHAPE, F32, out, bias))
+# the general kernel: 16-bit inputs with K % 8 != 0
+CASES += [("nn", 37, 53, 29, F16, F16, False), ("nt", 40, 48, 20, BF16, F32, True)]
 
 
 def case_id(c):

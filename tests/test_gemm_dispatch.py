@@ -17,7 +17,7 @@ from test_wq_dispatch import _built, _kernel_metadata
 def gemm_kernels(tmp_path_factory):
     tmp = tmp_path_factory.mktemp("co")
     names = set()
-    for stem in ("gemm", "gemm_big"):
+    for stem in ("gemm", "gemm_big", "gemm_f32"):
         names |= {n for n, _, _ in _kernel_metadata(_built(stem), tmp)}
     return {n for n in names if n.startswith("gemm_") and not n.startswith("gemm_dd_")}
 
@@ -34,6 +34,8 @@ def test_case_reaches_its_family(case):
     from gemm_cases import FAMILIES
     form, M, N, K, dt, out, bias = case
     fam = next((f for f, s in FAMILIES.items() if s == (M, N, K)), "general")
+    if dt == torch.float32:
+        fam = "f32t64"
     name = plan(case)
     assert name.startswith(f"gemm_{fam}_" if fam != "general" else "gemm_general"), name
 
@@ -42,6 +44,8 @@ def test_plan_follows_alignment_and_leading_dimensions():
     # unaligned A / B, or a leading dimension that is not a multiple of 8,
     # leave the MFMA kernels; an unaligned C leaves the 32-tile K-split kernel
     assert tm.gemm_kernel_for(512, 512, 512, align=_lib.TM_GEMM_ALIGN_C16)[0] == "gemm_general"
+    # fp32 inputs take the fp32-MFMA kernel whatever the alignment
+    assert tm.gemm_kernel_for(5, 7, 3, in_dtype=torch.float32, align=0)[0] == "gemm_f32t64_nn_f32"
     assert tm.gemm_kernel_for(512, 512, 512, lda=516)[0] == "gemm_general"
     assert tm.gemm_kernel_for(512, 512, 512)[0] == "gemm_s32k128_nn_f16_same"
     assert tm.gemm_kernel_for(512, 512, 512, align=_lib.TM_GEMM_ALIGN_AB16)[0].startswith(

@@ -317,7 +317,8 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
 // A pure function of the call (sizes, leading dimensions, dtypes, whether B is
 // the transposed nn.Linear weight and a bias is given, pointer alignment): the
 // launch path and tm_gemm_plan share it.  FP8 inputs are not planned here (they
-// run the general dot).
+// run the general dot); fp32 inputs take gemm_f32t64, 16-bit inputs the MFMA
+// tile kernels where sizes and alignment allow, else gemm_general.
 struct GemmPlan {
   char name[96];
   unsigned grid, block;
@@ -327,6 +328,16 @@ struct GemmPlan {
 void gemm_plan(int M, int N, int K, int lda, int ldb, int ldc, bool bt, bool bias, int idt,
                int odt, bool ab16, bool c16, GemmPlan* pl) {
   pl->general = false;
+  if (idt == TM_DT_F32) {
+    // fp32 inputs (the reference's default dtype): 64 x 64 tiles on the fp32
+    // MFMA (gemm_f32.hip), any leading dimensions and alignment
+    snprintf(pl->name, sizeof pl->name, "gemm_f32t64_%s_%s%s", bt ? "nt" : "nn",
+             odt == TM_DT_F32 ? "f32" : odt == TM_DT_F16 ? "f16" : "bf16",
+             (bt && bias) ? "_bias" : "");
+    pl->grid = (unsigned)(((M + 63) / 64) * ((N + 63) / 64));
+    pl->block = 256;
+    return;
+  }
   const char* dt = idt == TM_DT_BF16 ? "bf16" : "f16";
   const char* od = odt == TM_DT_F32 ? "f32" : "same";
   const char* bs = (bt && bias) ? "_bias" : "";
