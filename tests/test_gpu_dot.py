@@ -77,6 +77,18 @@ def test_dot_layouts(dev, dt, layout, M, N, K):
     _check(c, oracle.dot(_np(a), _np(b)), dt)
 
 
+@pytest.mark.parametrize("layout", ["row", "trans_a", "trans_b", "strided"])
+@pytest.mark.parametrize("M,N,K", [(64, 64, 32), (100, 72, 136), (7, 130, 50), (300, 260, 520)])
+@pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
+def test_dot_fp32_layouts(dev, layout, M, N, K, out):
+    """fp32 inputs without an epilogue: k- and n-contiguous rows (row, trans_b)
+    run the fp32-MFMA dense kernel, the other layouts the per-row kernel."""
+    da, db, a, b = _views(M, N, K, torch.float32, layout, seed=M + 2 * N + K)
+    c = torch.empty(M, N, dtype=out, device=dev)
+    tm.dot(da, db, c)
+    _check(c, oracle.dot(_np(a), _np(b)), out, np.abs(_np(a)), np.abs(_np(b)))
+
+
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
 def test_dot_column_major_output(dev, dt):
     """The reference's "trans" case: C written through column-major strides."""

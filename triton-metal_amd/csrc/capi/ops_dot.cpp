@@ -119,6 +119,18 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
     }
   }
   if (!rows_kernel && batch > 65535) rows_kernel = true;
+  // fp32 without an epilogue, one batch, k- and n-contiguous rows (B as [K, N]
+  // or [N, K]): the fp32-MFMA dense kernel
+  const auto fits = [](long long v) { return v >= 0 && v <= 0x7fffffffLL; };
+  if (in_dtype == TM_DT_F32 && epilogue == TM_EPI_NONE && batch == 1 && K > 0 && st[2] == 1 &&
+      st[8] == 1 && (st[5] == 1 || st[4] == 1) && fits(st[1]) && fits(st[4]) && fits(st[5]) &&
+      fits(st[7])) {
+    const bool bt = st[5] != 1;  // B [N, K]: row n at stride sb_n, k contiguous
+    const long long ldb = bt ? st[5] : st[4];
+    if (st[1] >= K && st[7] >= N && ldb >= (bt ? K : N))
+      return dense_f32((const float*)A, (const float*)B, C, M, N, K, (int)st[1], (int)ldb,
+                       (int)st[7], bt, out_dtype, stream);
+  }
   if (rows_kernel) {
     static Kernel kr("dot_rows");
     return launch(kr, dim3((unsigned)((long long)batch * M)), dim3(256), 0, stream, p);

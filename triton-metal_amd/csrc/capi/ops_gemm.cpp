@@ -419,6 +419,15 @@ int dense(const void* A, const void* B, void* C, const void* bias, int M, int N,
 
 }  // namespace
 
+int tmhip::dense_f32(const float* A, const float* B, void* C, int M, int N, int K, int lda,
+                     int ldb, int ldc, bool bt, int out_dtype, void* stream) {
+  GemmPlan pl;
+  gemm_plan(M, N, K, lda, ldb, ldc, bt, false, TM_DT_F32, out_dtype, aligned16(A) && aligned16(B),
+            aligned16(C), &pl);
+  return launch(kernel(pl.name), dim3(pl.grid), dim3(pl.block), 0, stream, A, B, C,
+                (const float*)nullptr, M, N, K, lda, ldb, ldc);
+}
+
 extern "C" {
 
 int tm_int8_matmul(const void* input, const void* weight, void* output, const void* scales,

@@ -101,6 +101,10 @@ int launch(Kernel& k, dim3 grid, dim3 block, unsigned shared, void* stream, Args
 int dot_impl(const char* op, const void* A, const void* B, void* C, const void* Z, const void* W,
              int batch, int M, int N, int K, int L, const long long* strides, int epilogue,
              int in_dtype, int out_dtype, int z_dtype, int w_dtype, void* stream);
+// The fp32-MFMA dense kernel (ops_gemm.cpp), shared with tm_dot's fp32 path:
+// C[M, N] = A[M, K] @ B (B [K, N], or [N, K] with bt), rows ldx apart.
+int dense_f32(const float* A, const float* B, void* C, int M, int N, int K, int lda, int ldb,
+              int ldc, bool bt, int out_dtype, void* stream);
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline bool is_half(int dt) { return dt == TM_DT_F16 || dt == TM_DT_BF16; }
