@@ -13,7 +13,7 @@ using namespace tmhip;
 
 namespace {
 
-// Kernel argument block; must match struct FlashParams in flash_fwd.hip.
+// Kernel argument block; must match struct FlashParams in kernels/flash_params.h.
 struct FlashParams {
   const void* q;
   const void* k;
@@ -89,6 +89,19 @@ extern "C" int tm_flash_attention(const void* q, const void* k, const void* v, v
     const long long grid = (causal ? (nqb + 1) / 2 : nqb) * (long long)batch * heads;
     if (grid > 0x7fffffffLL) return fail(TM_ERR_UNSUPPORTED, "tm_flash_attention: grid");
     return launch(flash_kernel(name), dim3((unsigned)grid), dim3(256), 0, stream, p);
+  }
+  // fp32 (the reference template's dtype): the fp32-MFMA kernel for head dims
+  // 32 / 64 / 128 with 16-byte aligned rows
+  bool st4 = true;
+  for (int i = 0; i < 12; ++i) st4 &= (st[i] % 4) == 0;
+  if (dtype == TM_DT_F32 && (head_dim == 32 || head_dim == 64 || head_dim == 128) && st4 &&
+      aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o)) {
+    char name[64];
+    snprintf(name, sizeof name, "flash_fwd_f32_d%d_%s", head_dim, causal ? "causal" : "full");
+    const long long grid = (long long)((seq_len + 63) / 64) * batch * heads;
+    if (grid > 0x7fffffffLL) return fail(TM_ERR_UNSUPPORTED, "tm_flash_attention: grid");
+    const unsigned lds = 2u * 2u * 32u * (unsigned)(head_dim + 4) * 4u;
+    return launch(flash_kernel(name), dim3((unsigned)grid), dim3(256), lds, stream, p);
   }
   const char* gname = head_dim <= 32 ? "flash_fwd_general_d32"
                       : head_dim <= 64 ? "flash_fwd_general_d64" : "flash_fwd_general_d128";
