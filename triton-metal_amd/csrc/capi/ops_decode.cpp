@@ -1,6 +1,7 @@
 // Typed entry point for decode-time attention (one query token per head over
-// a contiguous or paged KV cache): decode_attn_d<D>_<dt> (+ decode_attn_combine
-// when the sequence is split into slices) or decode_attn_general.
+// a contiguous or paged KV cache): decode_attn_d<D>_<dt> (16-bit caches) or
+// decode_attn_f32_d<D> (fp32), + decode_attn_combine when the sequence is
+// split into slices, or decode_attn_general.
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -122,9 +123,15 @@ static int decode_attention(const char* op, bool noalloc, const void* q, const v
   p.q_dt = q_dtype; p.kv_dt = kv_dtype; p.o_dt = o_dtype;
 
   const bool rows16 = p.sB % 8 == 0 && p.sH % 8 == 0 && p.sS % 8 == 0;
-  bool mfma = is16(kv_dtype) && (head_dim == 64 || head_dim == 128) && rows16 &&
-              aligned16(k_cache) && aligned16(v_cache) && seq_len > 0 &&
-              (q_dtype == kv_dtype ? aligned16(q) : true);
+  // fp32 caches with fp32 queries (the reference templates' dtype): the fp32
+  // MFMA kernel, same slices, partials and combine
+  const bool f32 = kv_dtype == TM_DT_F32 && q_dtype == TM_DT_F32 &&
+                   (head_dim == 64 || head_dim == 128) && p.sB % 4 == 0 && p.sH % 4 == 0 &&
+                   p.sS % 4 == 0 && aligned16(k_cache) && aligned16(v_cache) && aligned16(q) &&
+                   seq_len > 0;
+  bool mfma = f32 || (is16(kv_dtype) && (head_dim == 64 || head_dim == 128) && rows16 &&
+                      aligned16(k_cache) && aligned16(v_cache) && seq_len > 0 &&
+                      (q_dtype == kv_dtype ? aligned16(q) : true));
   if (mfma) {
     int ns = 1, sl = 0;
     plan_split(batch, q_heads, kv_heads, seq_len, p.page_size, paged, &ns, &sl);
@@ -160,8 +167,13 @@ static int decode_attention(const char* op, bool noalloc, const void* q, const v
            {new Kernel("decode_attn_d64_bf16"), new Kernel("decode_attn_d64_bf16_x")}},
           {{new Kernel("decode_attn_d128_f16"), new Kernel("decode_attn_d128_f16_x")},
            {new Kernel("decode_attn_d128_bf16"), new Kernel("decode_attn_d128_bf16_x")}}};
-      Kernel& kk = *kd[head_dim == 128][kv_dtype == TM_DT_BF16][q_dtype != kv_dtype];
-      const unsigned lds = 3u * 2u * 32u * (unsigned)head_dim * 2u;
+      static Kernel kf128("decode_attn_f32_d128"), kf64("decode_attn_f32_d64");
+      Kernel& kk = f32 ? (head_dim == 128 ? kf128 : kf64)
+                       : *kd[head_dim == 128][kv_dtype == TM_DT_BF16][q_dtype != kv_dtype];
+      // 16-bit: a 3-slot ring of 32-position K and V tiles; fp32: a 2-slot
+      // ring of 16-position tiles with rows padded by 4 floats
+      const unsigned lds = f32 ? 2u * 2u * 16u * (unsigned)(head_dim + 4) * 4u
+                               : 3u * 2u * 32u * (unsigned)head_dim * 2u;
       int rc = launch(kk, dim3(ns, kv_heads * hbn, batch), dim3(64), lds, stream, p);
       if (rc || ns == 1) return rc;
       static Kernel comb("decode_attn_combine");

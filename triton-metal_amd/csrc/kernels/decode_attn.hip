@@ -321,6 +321,165 @@ TM_DECODE(64, f16, false)
 TM_DECODE(64, bf16, true)
 
 // ----------------------------------------------------------------------------
+// fp32 caches and queries (the dtype of the reference's decode templates other
+// than make_fp16_kv_attention_kernel): fp32 MFMA v_mfma_f32_16x16x4_f32.
+// grid = (nsplit, Hkv * ceil(group / 16), B), block = 64, the same slices,
+// partials and combine as the 16-bit kernel.  Per 16-position tile:
+//   S^T = K Q^T   A = K rows from LDS (lane l: position l % 16, d 4 s + l / 16),
+//                 B = Q^T in registers (query head l % 16): lane l receives
+//                 positions 4 (l / 16) + e of its head;
+//   O^T += V^T P^T  the MFMA's 4-wide k index bound to positions 4 (l / 16) +
+//                 kk at step kk, so P^T is the lane's own score.
+// Tiles go global -> registers -> a 2-slot LDS ring ([16][D + 4] floats), the
+// next tile's loads in flight while the current one multiplies.
+// ----------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ void decode_f32_body(const DecodeParams& p) {
+  constexpr int DS = D + 4;           // LDS row stride (floats)
+  constexpr int TILE = 16 * DS;       // floats of one K (or V) tile
+  constexpr int PPT = 16 * D / 4 / 64;  // float4 pieces per lane and tile
+  constexpr int KS = D / 4;           // k-steps of S^T
+  constexpr int DT = D / 16;          // 16-row d tiles of O^T
+  extern __shared__ __align__(16) uint8_t lds[];
+  float* ring = (float*)lds;          // [2 slots][K tile, V tile]
+  const int lane = threadIdx.x, l16 = lane & 15, g = lane >> 4;
+  const int group = p.Hq / p.Hkv, hbn = (group + 15) / 16;
+  const int split = blockIdx.x, b = blockIdx.z;
+  const int kvh = blockIdx.y / hbn, hb = blockIdx.y - kvh * hbn;
+  const int len = seq_len_of(p, b);
+  const int p0 = split * p.split_len, p1 = min(len, p0 + p.split_len);
+  const int hq = kvh * group + 16 * hb + l16;  // this lane's query head
+  const bool hvalid = 16 * hb + l16 < group;
+  const float* kc = (const float*)p.k;
+  const float* vc = (const float*)p.v;
+
+  // Q^T operand: qreg[s] = q[b, hq, 4 s + g]
+  float qreg[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    qreg[s] = hvalid ? ((const float*)p.q)[((long long)b * p.Hq + hq) * D + 4 * s + g] : 0.0f;
+
+  const long long hoff = (long long)kvh * p.sH;
+  const int* pt = p.page_table ? p.page_table + (long long)b * p.max_pages : nullptr;
+  const int ntile = p1 > p0 ? (p1 - p0 + 15) / 16 : 0;
+  // paged: lane i holds the physical page of the slice's i-th page (the slice
+  // starts on a page boundary and spans at most 64 pages)
+  const int fp = pt ? p0 / p.page_size : 0;
+  int mypage = 0;
+  if (pt && ntile > 0) {
+    const int np = (p1 - 1) / p.page_size - fp + 1;
+    if (lane < np) mypage = pt[fp + lane];
+  }
+  auto row_off = [&](int pos) -> long long {  // element offset of cache position pos
+    if (pt) {
+      const int rel = pos - p0;
+      const int pi = p.page_shift >= 0 ? rel >> p.page_shift : rel / p.page_size;
+      const int slot = p.page_shift >= 0 ? rel & (p.page_size - 1) : rel - pi * p.page_size;
+      const int page = __builtin_amdgcn_ds_bpermute(4 * pi, mypage);
+      return (long long)page * p.sB + hoff + (long long)slot * p.sS;
+    }
+    return (long long)b * p.sB + hoff + (long long)pos * p.sS;
+  };
+  // lane's pieces: row (lane + 64 i) / (D / 4), float4 column (lane + 64 i) % (D / 4)
+  f4_t rk[PPT], rv[PPT];
+  auto load = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int e = lane + 64 * i, r = e / (D / 4), c4 = e - r * (D / 4);
+      const long long off = row_off(min(p0 + 16 * t + r, len - 1)) + 4 * c4;
+      rk[i] = *(const f4_t*)(kc + off);
+      rv[i] = *(const f4_t*)(vc + off);
+    }
+  };
+  auto stash = [&](int slot) {
+    float* ks = ring + slot * 2 * TILE;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int e = lane + 64 * i, r = e / (D / 4), c4 = e - r * (D / 4);
+      *(f4_t*)(ks + r * DS + 4 * c4) = rk[i];
+      *(f4_t*)(ks + TILE + r * DS + 4 * c4) = rv[i];
+    }
+  };
+
+  f4_t oacc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) oacc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  if (ntile > 0) {
+    load(0);
+    stash(0);
+  }
+  for (int t = 0; t < ntile; ++t) {
+    const bool more = t + 1 < ntile;
+    if (more) load(t + 1);
+    const float* ks = ring + (t & 1) * 2 * TILE;
+    const float* vs = ks + TILE;
+    f4_t st = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(ks[l16 * DS + 4 * s + g], qreg[s], st, 0, 0, 0);
+    const int pbase = p0 + 16 * t + 4 * g;
+    float sc[4], mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sc[e] = pbase + e < p1 ? st[e] * p.sl2 : -INFINITY;
+      mx = fmaxf(mx, sc[e]);
+    }
+    mx = max_swap<32>(max_swap<16>(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+    const float mu = m_new == -INFINITY ? 0.0f : m_new;
+    m_run = m_new;
+    float pv[4], ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pv[e] = __builtin_amdgcn_exp2f(sc[e] - mu);
+      ps += pv[e];
+    }
+    l_run = l_run * alpha + ps;  // this lane's positions; the lane groups meet at the end
+#pragma unroll
+    for (int d = 0; d < DT; ++d) oacc[d] *= alpha;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const float* vrow = vs + (4 * g + kk) * DS + l16;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+        oacc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * d], pv[kk], oacc[d], 0, 0, 0);
+    }
+    if (more) stash((t + 1) & 1);
+  }
+  l_run = fold_swap<16>(l_run, l_run);
+  l_run = fold_swap<32>(l_run, l_run);
+  if (!hvalid) return;
+  // lane holds O^T[16 d + 4 g + e][head l16]
+  if (p.nsplit == 1) {
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+    const long long ob = ((long long)b * p.Hq + hq) * D;
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) st_any(p.o, ob + 16 * d + 4 * g + e, p.o_dt, oacc[d][e] * inv);
+    if (p.lse && g == 0)
+      p.lse[(long long)b * p.Hq + hq] = l_run > 0.0f ? (m_run + __log2f(l_run)) * kLn2f : -INFINITY;
+  } else {
+    float* w = p.ws + (((long long)b * p.Hq + hq) * p.nsplit + split) * (D + 4);
+#pragma unroll
+    for (int d = 0; d < DT; ++d) *(f4_t*)(w + 16 * d + 4 * g) = oacc[d];
+    if (g == 0) {
+      w[D] = m_run;
+      w[D + 1] = l_run;
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(64) void decode_attn_f32_d128(DecodeParams p) {
+  decode_f32_body<128>(p);
+}
+extern "C" __global__ __launch_bounds__(64) void decode_attn_f32_d64(DecodeParams p) {
+  decode_f32_body<64>(p);
+}
+
+// ----------------------------------------------------------------------------
 // Combine the slices: grid = B * Hq, block = 64 (D <= 256, 4 per lane).  The
 // lanes take the slices' maxima in parallel; the weighted sum runs 8 slices
 // per step so that their loads are in flight together.
