@@ -131,6 +131,21 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
       return dense_f32((const float*)A, (const float*)B, C, M, N, K, (int)st[1], (int)ldb,
                        (int)st[7], bt, out_dtype, stream);
   }
+  // 16-bit, no epilogue, one batch, k- and n-contiguous rows, output in the
+  // input dtype or fp32: the dense selection's MFMA tile kernels, when it has
+  // one for these sizes and alignments
+  if (is_half(in_dtype) && (out_dtype == in_dtype || out_dtype == TM_DT_F32) &&
+      epilogue == TM_EPI_NONE && batch == 1 && K > 0 && st[2] == 1 && st[8] == 1 &&
+      (st[5] == 1 || st[4] == 1) && fits(st[1]) && fits(st[4]) && fits(st[5]) && fits(st[7])) {
+    const bool bt = st[5] != 1;
+    const long long ldb = bt ? st[5] : st[4];
+    if (st[1] >= K && st[7] >= N && ldb >= (bt ? K : N)) {
+      bool used = false;
+      const int rc = dense_mfma(A, B, C, M, N, K, (int)st[1], (int)ldb, (int)st[7], bt, in_dtype,
+                                out_dtype, stream, &used);
+      if (used || rc) return rc;
+    }
+  }
   if (rows_kernel) {
     static Kernel kr("dot_rows");
     return launch(kr, dim3((unsigned)((long long)batch * M)), dim3(256), 0, stream, p);

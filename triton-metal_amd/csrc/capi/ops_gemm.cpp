@@ -428,6 +428,20 @@ int tmhip::dense_f32(const float* A, const float* B, void* C, int M, int N, int 
                 (const float*)nullptr, M, N, K, lda, ldb, ldc);
 }
 
+int tmhip::dense_mfma(const void* A, const void* B, void* C, int M, int N, int K, int lda,
+                      int ldb, int ldc, bool bt, int in_dtype, int out_dtype, void* stream,
+                      bool* used) {
+  *used = false;
+  if (!is_half(in_dtype)) return 0;
+  GemmPlan pl;
+  gemm_plan(M, N, K, lda, ldb, ldc, bt, false, in_dtype, out_dtype, aligned16(A) && aligned16(B),
+            aligned16(C), &pl);
+  if (pl.general) return 0;
+  *used = true;
+  return launch(kernel(pl.name), dim3(pl.grid), dim3(pl.block), 0, stream, A, B, C,
+                (const void*)nullptr, M, N, K, lda, ldb, ldc);
+}
+
 extern "C" {
 
 int tm_int8_matmul(const void* input, const void* weight, void* output, const void* scales,

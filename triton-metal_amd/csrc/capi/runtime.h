@@ -105,6 +105,11 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
 // C[M, N] = A[M, K] @ B (B [K, N], or [N, K] with bt), rows ldx apart.
 int dense_f32(const float* A, const float* B, void* C, int M, int N, int K, int lda, int ldb,
               int ldc, bool bt, int out_dtype, void* stream);
+// The 16-bit MFMA dense kernels (ops_gemm.cpp), shared with tm_dot: launches
+// and sets *used when the dense selection picks an MFMA tile kernel for this
+// call, else launches nothing and clears *used.
+int dense_mfma(const void* A, const void* B, void* C, int M, int N, int K, int lda, int ldb,
+               int ldc, bool bt, int in_dtype, int out_dtype, void* stream, bool* used);
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 inline bool is_half(int dt) { return dt == TM_DT_F16 || dt == TM_DT_BF16; }
