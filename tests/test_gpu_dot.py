@@ -82,25 +82,26 @@ def test_dot_layouts(dev, dt, layout, M, N, K):
 @pytest.mark.parametrize("out", [torch.float32, torch.bfloat16])
 def test_dot_fp32_layouts(dev, layout, M, N, K, out):
     """fp32 inputs without an epilogue: k- and n-contiguous rows (row, trans_b)
-    run the fp32-MFMA dense kernel, the other layouts the per-row kernel."""
+    run the fp32-MFMA dense kernel, the other layouts the strided fp32-MFMA
+    tile kernel."""
     da, db, a, b = _views(M, N, K, torch.float32, layout, seed=M + 2 * N + K)
     c = torch.empty(M, N, dtype=out, device=dev)
     tm.dot(da, db, c)
     _check(c, oracle.dot(_np(a), _np(b)), out, np.abs(_np(a)), np.abs(_np(b)))
 
 
-@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 def test_dot_column_major_output(dev, dt):
     """The reference's "trans" case: C written through column-major strides."""
     M, N, K = 96, 80, 64
     da, db, a, b = _views(M, N, K, dt, "row", seed=5)
     cbuf = torch.zeros(N, M, dtype=dt, device=dev)
     tm.dot(da, db, cbuf.t())
-    _check(cbuf.t(), oracle.dot(_np(a), _np(b)), dt)
+    _check(cbuf.t(), oracle.dot(_np(a), _np(b)), dt, np.abs(_np(a)), np.abs(_np(b)))
 
 
 @pytest.mark.parametrize("layout", ["row", "trans_a", "trans_b", "strided"])
-@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 def test_dot_batched_3d(dev, layout, dt):
     B, M, N, K = 3, 70, 40, 96
     da, db, a, b = _views(M, N, K, dt, layout, seed=17, batch=B)
@@ -125,14 +126,16 @@ def test_dot_add_epilogues(dev, epilogue, dt, batch):
 
 
 @pytest.mark.parametrize("epilogue", ["add-matrix", "add-rows"])
-def test_dot_bias_read_in_place(dev, epilogue):
+@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
+def test_dot_bias_read_in_place(dev, epilogue, dt):
     """Z is the output buffer itself, as in the reference's test kernels."""
     M, N, K = 130, 70, 64
-    da, db, a, b = _views(M, N, K, torch.float16, "row", seed=31)
-    z = _rand((M, N), 37, torch.float16)
+    da, db, a, b = _views(M, N, K, dt, "row", seed=31)
+    z = _rand((M, N), 37, dt)
     c = z.to(dev)
     tm.dot(da, db, c, epilogue, z=c)
-    _check(c, oracle.dot(_np(a), _np(b), epilogue, Z=_np(z)), torch.float16)
+    _check(c, oracle.dot(_np(a), _np(b), epilogue, Z=_np(z)), dt, np.abs(_np(a)),
+           np.abs(_np(b)))
 
 
 def test_dot_add_cols_in_place_rejected_for_many_rows(dev):

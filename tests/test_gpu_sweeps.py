@@ -223,6 +223,72 @@ def test_dense_random_shapes(dev, case):
     np.testing.assert_allclose(C_.float().cpu().numpy(), ref, atol=atol, rtol=rtol)
 
 
+# --- tl.dot in general form ---------------------------------------------------
+def _dot_cases(n=40, seed=9090):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        dt = [F16, BF16, F32, F32][int(rng.integers(4))]
+        odt = dt if rng.random() < 0.5 else F32
+        epi = ["none", "none", "add-matrix", "add-rows", "add-cols"][int(rng.integers(5))]
+        batch = None if rng.random() < 0.5 else int(rng.integers(1, 5))
+        la = ["row", "col", "strided"][int(rng.integers(3))]
+        lb = ["row", "col", "strided"][int(rng.integers(3))]
+        if rng.random() < 0.3:
+            M, N, K = (64 * int(v) for v in rng.integers(1, 6, size=3))
+        else:
+            M, N, K = (int(v) for v in rng.integers(1, 400, size=3))
+        out.append((dt, odt, epi, batch, la, lb, M, N, K))
+    return out
+
+
+def _operand(rows, cols, bs, dt, layout, g, dev):
+    """A [.., rows, cols] view on the device in the given layout and its CPU
+    values: row-major, column-major (a transposed copy) or every second
+    element of a wider row."""
+    x = torch.randn(*bs, rows, cols, generator=g).to(dt)
+    if layout == "row":
+        return x.to(dev), x
+    if layout == "col":
+        return x.transpose(-1, -2).contiguous().to(dev).transpose(-1, -2), x
+    buf = torch.zeros(*bs, rows, 2 * cols + 1, dtype=dt)
+    buf[..., : 2 * cols : 2] = x
+    return buf.to(dev)[..., : 2 * cols : 2], x
+
+
+DOT_CASES = _dot_cases()
+
+
+@pytest.mark.parametrize("case", DOT_CASES,
+                         ids=[f"{str(c[0]).split('.')[-1]}-{str(c[1]).split('.')[-1]}-{c[2]}"
+                              f"-b{c[3]}-{c[4]}-{c[5]}-{c[6]}x{c[7]}x{c[8]}" for c in DOT_CASES])
+def test_dot_random_layouts(dev, case):
+    """tm.dot with mixed operand layouts, batches and add-* epilogues against
+    oracle.dot; fp32 outputs within 1e-4 |ref| + 2^-16 (|A| @ |B|) (fp32
+    accumulation of exact products), 16-bit outputs atol 2e-2 / rtol 1e-2."""
+    dt, odt, epi, batch, la, lb, M, N, K = case
+    g = torch.Generator().manual_seed(M * 977 + N * 31 + K)
+    bs = () if batch is None else (batch,)
+    a, a_cpu = _operand(M, K, bs, dt, la, g, dev)
+    b, b_cpu = _operand(K, N, bs, dt, lb, g, dev)
+    z = z_cpu = None
+    if epi != "none":
+        z_cpu = torch.randn(*bs, M, N, generator=g).to(dt)
+        z = z_cpu.to(dev)
+    c = torch.empty(*bs, M, N, dtype=odt, device=dev)
+    tm.dot(a, b, c, epi, z=z)
+    torch.cuda.synchronize()
+    an, bn = a_cpu.double().numpy(), b_cpu.double().numpy()
+    ref = oracle.dot(an, bn, epi, Z=None if z_cpu is None else z_cpu.double().numpy())
+    got = c.double().cpu().numpy()
+    if odt == F32:
+        bound = 1e-4 * np.abs(ref) + 2.0 ** -16 * (np.abs(an) @ np.abs(bn))
+        err = np.abs(got - ref)
+        assert (err <= bound + 1e-30).all(), f"max err {err.max():.3e}"
+    else:
+        np.testing.assert_allclose(got, ref, atol=2e-2, rtol=1e-2)
+
+
 # --- flash attention ----------------------------------------------------------
 def _fa_cases(n=28, seed=777):
     rng = np.random.default_rng(seed)

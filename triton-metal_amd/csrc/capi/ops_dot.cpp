@@ -1,6 +1,7 @@
 // Typed entry point for tl.dot in general form (strided / transposed
-// operands, a batch dimension, FP8 inputs, epilogues): dot_tile_{f16,bf16}
-// (MFMA) or dot_rows (fp32, every epilogue).  Also the FP8 path of tm_matmul.
+// operands, a batch dimension, FP8 inputs, epilogues): dot_tile_{f16,bf16,f32}
+// (MFMA, the none / add-* epilogues) or dot_rows (softmax, chain-dot).  Also
+// the FP8 path of tm_matmul.
 #include <cstring>
 
 #include "runtime.h"
@@ -33,14 +34,16 @@ bool is_fp8(int dt) { return dt >= TM_DT_FP8_E4M3 && dt <= TM_DT_FP8_E5M2B16; }
 int elem_size(int dt) { return dt == TM_DT_F32 ? 4 : is_fp8(dt) ? 1 : 2; }
 bool is_input(int dt) { return is_float(dt) || is_fp8(dt); }
 
-// Fetch mode of a [rows, K] operand with strides (s_b, s_r, s_k): 16-byte
-// (FP8: 8-byte) pieces along k or along the rows when that dimension is
-// contiguous and every piece starts aligned, else element by element.
+// Fetch mode of a [rows, K] operand with strides (s_b, s_r, s_k): pieces of
+// 8 elements (fp32: 4; 16 bytes, FP8 8 bytes) along k or along the rows when
+// that dimension is contiguous and every piece starts aligned, else element
+// by element.
 int fetch_mode(const void* X, long long s_b, long long s_r, long long s_k, int batch, int esz) {
-  const uintptr_t align = 8u * (uintptr_t)esz;
-  const bool base_ok = ((uintptr_t)X % align) == 0 && (batch <= 1 || s_b % 8 == 0);
-  if (base_ok && s_k == 1 && s_r % 8 == 0) return MODE_KC;
-  if (base_ok && s_r == 1 && s_k % 8 == 0) return MODE_RC;
+  const int piece = esz == 4 ? 4 : 8;
+  const uintptr_t align = (uintptr_t)piece * (uintptr_t)esz;
+  const bool base_ok = ((uintptr_t)X % align) == 0 && (batch <= 1 || s_b % piece == 0);
+  if (base_ok && s_k == 1 && s_r % piece == 0) return MODE_KC;
+  if (base_ok && s_r == 1 && s_k % piece == 0) return MODE_RC;
   return MODE_SCALAR;
 }
 
@@ -99,7 +102,7 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
   // one thread, which is only race-free when Z is C element for element (same
   // base, dtype and strides); add-rows reads its row's element in the row's
   // own workgroup (dot_rows) before any store; add-cols across rows would race.
-  bool rows_kernel = epilogue == TM_EPI_SOFTMAX || chain || in_dtype == TM_DT_F32 || K == 0;
+  bool rows_kernel = epilogue == TM_EPI_SOFTMAX || chain || K == 0;
   if (add) {
     uintptr_t zl, zh, cl, ch;
     extent(Z, elem_size(z_dtype), batch, M, N, st[9], st[10], st[11], &zl, &zh);
@@ -153,11 +156,11 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
   const int esz = elem_size(in_dtype);
   p.a_mode = fetch_mode(A, p.sa_b, p.sa_m, p.sa_k, batch, esz);
   p.b_mode = fetch_mode(B, p.sb_b, p.sb_n, p.sb_k, batch, esz);
-  static Kernel kf("dot_tile_f16"), kb("dot_tile_bf16");
+  static Kernel kf("dot_tile_f16"), kb("dot_tile_bf16"), k32("dot_tile_f32");
   const long long tiles = (long long)((M + 63) / 64) * ((N + 63) / 64);
   if (tiles > 0x7fffffffLL) return fail(TM_ERR_UNSUPPORTED, "%s: too many tiles", op);
-  return launch(in_dtype == TM_DT_BF16 ? kb : kf, dim3((unsigned)tiles, (unsigned)batch),
-                dim3(256), 0, stream, p);
+  Kernel& kt = in_dtype == TM_DT_F32 ? k32 : in_dtype == TM_DT_BF16 ? kb : kf;
+  return launch(kt, dim3((unsigned)tiles, (unsigned)batch), dim3(256), 0, stream, p);
 }
 
 }  // namespace tmhip

@@ -24,10 +24,13 @@
 // LDS: every FP8 value of the five formats is exactly an fp16 value, so the
 // fp16 MFMA forms the same products the reference forms in fp32.
 //
+// dot_tile_f32: the same tiling for fp32 inputs on the fp32 MFMA (the
+// reference computes fp32 dots in fp32), K in steps of 16.
+//
 // dot_rows: one workgroup per (batch, row), fp32 FMA, any dtype and strides,
 // every epilogue.  The softmax and chain-dot epilogues need the whole row of
 // the product, which the workgroup keeps in LDS (N <= 8192); it also serves
-// fp32 inputs, which the reference computes in fp32.
+// K = 0 and a bias read in place across rows.
 #include "common.h"
 
 enum { EPI_NONE = 0, EPI_ADD_MATRIX = 1, EPI_ADD_ROWS = 2, EPI_ADD_COLS = 3, EPI_SOFTMAX = 4,
@@ -250,6 +253,137 @@ extern "C" __global__ __launch_bounds__(256) void dot_tile_f16(DotParams p) {
 }
 extern "C" __global__ __launch_bounds__(256) void dot_tile_bf16(DotParams p) {
   dot_tile_body<true>(p);
+}
+
+// ----------------------------------------------------------------------------
+// dot_tile_f32: fp32 inputs with the none / add-* epilogues on the fp32 MFMA
+// (v_mfma_f32_16x16x4_f32: fp32 products, 4 added per step into the fp32
+// accumulator).  Grid (tiles_m * tiles_n, batch), block 256: a 64 x 64 output
+// tile, 2 x 2 waves of 32 x 32, each 2 x 2 MFMA tiles of 16 x 16
+// (A[l % 16][l / 16], B[l / 16][l % 16], D[4 (l / 16) + e][l % 16]).  K in
+// steps of 16 through two LDS buffers, both operands k-major there
+// ([16 k][64 + 16 pad] floats: a 16-lane operand read is 16 consecutive
+// floats, the four k rows of one read 16 banks apart).  Fetch modes of an
+// operand [64 rows][16 k]: KC  row tid / 4, 4 k from 4 (tid % 4), one
+// 16-byte load; RC  k tid / 16, 4 rows from 4 (tid % 16), one 16-byte load
+// stored as one 16-byte LDS write; SCALAR  the KC mapping element by element.
+// Rows and k past the operand read as zero.
+// ----------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void dot_tile_f32(DotParams p) {
+  constexpr int TB = 64, TK = 16, TS = TB + 16;
+  __shared__ __align__(16) float As[2][TK * TS], Bs[2][TK * TS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_n = (p.N + TB - 1) / TB;
+  const int m0 = (blockIdx.x / tiles_n) * TB, n0 = (blockIdx.x % tiles_n) * TB;
+  const int b = blockIdx.y;
+  const float* Ab = (const float*)p.A + (long long)b * p.sa_b;
+  const float* Bb = (const float*)p.B + (long long)b * p.sb_b;
+
+  auto fetch = [&](const float* X, int mode, int rows, int r0, long long s_r, long long s_k,
+                   int k0) -> f4_t {
+    f4_t v = f4_t{0.f, 0.f, 0.f, 0.f};
+    if (mode == MODE_RC) {  // s_r == 1
+      const int kk = k0 + (tid >> 4), rc = r0 + 4 * (tid & 15);
+      if (kk < p.K) {
+        const float* q = X + rc + (long long)kk * s_k;
+        if (rc + 3 < rows) {
+          v = *(const f4_t*)q;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (rc + j < rows) v[j] = q[j];
+        }
+      }
+      return v;
+    }
+    const int r = r0 + (tid >> 2), kc = k0 + 4 * (tid & 3);
+    if (r < rows) {
+      const float* q = X + (long long)r * s_r + (long long)kc * s_k;
+      if (mode == MODE_KC && kc + 3 < p.K) {
+        v = *(const f4_t*)q;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kc + j < p.K) v[j] = q[(long long)j * s_k];
+      }
+    }
+    return v;
+  };
+  auto put = [&](float* Xs, int mode, f4_t v) {
+    if (mode == MODE_RC) {
+      *(f4_t*)&Xs[(tid >> 4) * TS + 4 * (tid & 15)] = v;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Xs[(4 * (tid & 3) + j) * TS + (tid >> 2)] = v[j];
+    }
+  };
+
+  f4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+  const int nk = (p.K + TK - 1) / TK;
+  f4_t fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, 0);
+  f4_t fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, 0);
+  put(As[0], p.a_mode, fa);
+  put(Bs[0], p.b_mode, fb);
+  __syncthreads();
+  const int q = lane >> 4, r16 = lane & 15;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) {
+      fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, (kt + 1) * TK);
+      fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, (kt + 1) * TK);
+    }
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < TK / 4; ++kk) {
+      const int kr = (4 * kk + q) * TS;
+      float a[2], bv[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        a[t] = as[kr + 32 * wm + 16 * t + r16];
+        bv[t] = bs[kr + 32 * wn + 16 * t + r16];
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) {
+      put(As[buf ^ 1], p.a_mode, fa);
+      put(Bs[buf ^ 1], p.b_mode, fb);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 32 wm + 16 i + 4 q + e, column 32 wn + 16 j + r16
+  const long long zb = (long long)b * p.sz_b;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + 32 * wn + 16 * j + r16;
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = m0 + 32 * wm + 16 * i + 4 * q + e;
+        if (row >= p.M) continue;
+        float v = acc[i][j][e];
+        if (p.epi == EPI_ADD_MATRIX)
+          v += load_elem(p.Z, zb + (long long)row * p.sz_m + (long long)col * p.sz_n, p.z_dt);
+        else if (p.epi == EPI_ADD_ROWS)
+          v += load_elem(p.Z, zb + (long long)row * p.sz_m, p.z_dt);
+        else if (p.epi == EPI_ADD_COLS)
+          v += load_elem(p.Z, zb + (long long)col * p.sz_n, p.z_dt);
+        store_elem(p.C, (long long)b * p.sc_b + (long long)row * p.sc_m + (long long)col * p.sc_n,
+                   p.out_dt, v);
+      }
+    }
 }
 
 // ----------------------------------------------------------------------------
