@@ -156,10 +156,23 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
   const int esz = elem_size(in_dtype);
   p.a_mode = fetch_mode(A, p.sa_b, p.sa_m, p.sa_k, batch, esz);
   p.b_mode = fetch_mode(B, p.sb_b, p.sb_n, p.sb_k, batch, esz);
-  static Kernel kf("dot_tile_f16"), kb("dot_tile_bf16"), k32("dot_tile_f32");
-  const long long tiles = (long long)((M + 63) / 64) * ((N + 63) / 64);
+  // [f16, bf16, fp8, f32]: both operands in 16-byte pieces (KC / RC) ->
+  // dot_tile (16-bit and FP8: 128 x 128 tiles once they give every CU a
+  // workgroup, else 64 x 64), else the element-load form dot_tile_s
+  static Kernel* k64[4] = {new Kernel("dot_tile_f16"), new Kernel("dot_tile_bf16"),
+                           new Kernel("dot_tile_fp8"), new Kernel("dot_tile_f32")};
+  static Kernel* k128[3] = {new Kernel("dot_tile128_f16"), new Kernel("dot_tile128_bf16"),
+                            new Kernel("dot_tile128_fp8")};
+  static Kernel* ks[4] = {new Kernel("dot_tile_s_f16"), new Kernel("dot_tile_s_bf16"),
+                          new Kernel("dot_tile_s_fp8"), new Kernel("dot_tile_s_f32")};
+  const int kind = in_dtype == TM_DT_F32 ? 3 : is_fp8(in_dtype) ? 2 : in_dtype == TM_DT_BF16 ? 1 : 0;
+  const bool vec = p.a_mode != MODE_SCALAR && p.b_mode != MODE_SCALAR;
+  const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
+  const bool big = vec && kind != 3 && t128 * batch >= 256;
+  const int edge = big ? 128 : 64;
+  const long long tiles = (long long)((M + edge - 1) / edge) * ((N + edge - 1) / edge);
   if (tiles > 0x7fffffffLL) return fail(TM_ERR_UNSUPPORTED, "%s: too many tiles", op);
-  Kernel& kt = in_dtype == TM_DT_F32 ? k32 : in_dtype == TM_DT_BF16 ? kb : kf;
+  Kernel& kt = big ? *k128[kind] : vec ? *k64[kind] : *ks[kind];
   return launch(kt, dim3((unsigned)tiles, (unsigned)batch), dim3(256), 0, stream, p);
 }
 

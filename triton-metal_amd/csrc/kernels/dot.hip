@@ -14,8 +14,9 @@
 // converters do (FP8 output is fp32 there, _msl_templates.py:475-476).
 //
 // dot_tile: MFMA kernel for 16-bit and FP8 inputs with the none / add-*
-// epilogues.  64 x 64 output tile per 256-thread workgroup (2 x 2 waves of
-// 32 x 32, v_mfma_f32_16x16x32), K in steps of 32 through two LDS buffers,
+// epilogues.  64 x 64 output tile (dot_tile128: 128 x 128, for problems with
+// enough tiles to fill the chip) per 256-thread workgroup (2 x 2 waves,
+// v_mfma_f32_16x16x32), K in steps of 32 through two LDS buffers,
 // operands stored k-contiguous in LDS whatever their layout in memory.  Each
 // operand is fetched in one of three modes chosen by the host from its
 // strides: k-contiguous (16-byte row pieces), row-contiguous (a transposed
@@ -94,95 +95,306 @@ TM_DEV void store_elem(void* p, long long i, int dt, float v) { store_as_f32_rt(
 
 }  // namespace
 
+// Keep the first n elements of a piece (the rest zero): 16-bit elements in 4
+// dwords, or FP8 codes in the low 2.
+template <bool FP8> TM_DEV u4_t piece_keep(u4_t w, int n) {
+  const int bits = (FP8 ? 8 : 16) * n;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int lo = 32 * d;
+    w[d] = bits >= lo + 32 ? w[d] : bits <= lo ? 0u : w[d] & ((1u << (bits - lo)) - 1u);
+  }
+  return w;
+}
+
+// Epilogue of the tile kernels: lane holds rows wt wm + 16 i + 4 q + e,
+// column wt wn + 16 j + r16 of the workgroup's tile; the add-* bias in fp32,
+// then one store in the output dtype.  The element loop stays rolled:
+// unrolled, the runtime-dtype loads and stores of 4 x 4 tiles outgrow the
+// unroller and the accumulators go to scratch.
+template <int FT>
+TM_DEV void tile_epilogue(const DotParams& p, const f4_t (&acc)[FT][FT], int m0, int n0, int b,
+                          int wt, int wm, int wn, int q, int r16) {
+  const long long zb = (long long)b * p.sz_b;
+#pragma unroll
+  for (int i = 0; i < FT; ++i)
+#pragma unroll
+    for (int j = 0; j < FT; ++j) {
+      const int col = n0 + wt * wn + 16 * j + r16;
+      const f4_t a4 = acc[i][j];
+      if (col >= p.N) continue;
+#pragma unroll 1
+      for (int e = 0; e < 4; ++e) {
+        const int row = m0 + wt * wm + 16 * i + 4 * q + e;
+        if (row >= p.M) continue;
+        float v = a4[e];
+        if (p.epi == EPI_ADD_MATRIX)
+          v += load_elem(p.Z, zb + (long long)row * p.sz_m + (long long)col * p.sz_n, p.z_dt);
+        else if (p.epi == EPI_ADD_ROWS)
+          v += load_elem(p.Z, zb + (long long)row * p.sz_m, p.z_dt);
+        else if (p.epi == EPI_ADD_COLS)
+          v += load_elem(p.Z, zb + (long long)col * p.sz_n, p.z_dt);
+        store_elem(p.C, (long long)b * p.sc_b + (long long)row * p.sc_m + (long long)col * p.sc_n,
+                   p.out_dt, v);
+      }
+    }
+}
+
 // ----------------------------------------------------------------------------
-// dot_tile: grid (tiles_m * tiles_n, batch), block 256.
+// dot_tile{,128}_<f16|bf16|fp8>: both operands KC or RC, grid (tiles, batch),
+// block 256.  Output tile BT x BT (64 or 128), 2 x 2 waves of BT/2 x BT/2,
+// each (BT/32)^2 MFMA tiles of 16 x 16 (v_mfma_f32_16x16x32: lane l supplies
+// row l % 16, k 8 (l / 16) .. +7 of each operand and holds
+// D[4 (l / 16) + e][l % 16]).  K in steps of BK (64; 32 for the 128 tile, to
+// keep two waves per SIMD).  An operand's [BT rows][BK k] step is
+// BT BK / 2048 pieces of 8 elements per thread (piece h: rows + 64 (h %
+// (BT / 64)), k + 32 (h / (BT / 64))), each one 16-byte (FP8: 8-byte) load:
+//   KC  row tid / 4, k 8 (tid % 4) .. +7
+//   RC  rows 8 (tid % 8) .. +7, k tid / 8   (scattered into LDS as 8 halves)
+// kept packed in registers.  Loads run two steps ahead (two register sets):
+// step kt + 2 is loaded while step kt multiplies from LDS and step kt + 1
+// goes from registers to the other LDS buffer.  Every load is
+// unconditional: a piece starts at a multiple of 8 elements of an aligned
+// row, and one past the operand is moved to the last piece holding an
+// element of it (row at most rows - 1, k at most K - 1), so each load reads
+// an aligned chunk holding a valid element (never a page the operand does
+// not touch) and nothing writes its registers before the LDS store that
+// consumes it; that store zeroes the elements past the operand.
+// LDS: [row][BK k + 8 pad] halves, the 16-byte k chunk c of row r at
+// c ^ ((r / 16) % 4): the 16 rows of one operand read keep one chunk order
+// (each read touches every bank once) while the 8 row groups of one
+// scattered RC store land in distinct banks.
+// Workgroups are taken in XCD order (dispatch i runs on XCD i % 8): when the
+// tile count is a multiple of 8, XCD x takes tiles x T / 8 .. (x + 1) T / 8 - 1,
+// rows of tiles that share their A rows in one L2.
 // ----------------------------------------------------------------------------
-template <bool BF16>
-__device__ __forceinline__ void dot_tile_body(const DotParams& p) {
-  constexpr int BM = 64, BN = 64, BK = 32, LDK = BK + 8;
-  __shared__ __align__(16) uint16_t As[2][BM * LDK];
-  __shared__ __align__(16) uint16_t Bs[2][BN * LDK];
+TM_DEV int tile_lds(int row, int k, int ldk) {
+  return row * ldk + ((((k >> 3) ^ (row >> 4)) & 3) | (k >> 3 & ~3)) * 8 + (k & 7);
+}
+
+template <bool BF16, bool FP8, int BT>
+__device__ __forceinline__ void dot_tile_vec_body(const DotParams& p) {
+  constexpr int BK = BT == 64 ? 64 : 32, LDK = BK + 8;
+  constexpr int WT = BT / 2;   // wave tile edge
+  constexpr int FT = WT / 16;  // MFMA tiles per wave tile edge
+  constexpr int RP = BT / 64;  // row blocks of 64 per operand step
+  constexpr int NP = RP * BK / 32;  // pieces per thread and operand step
+  constexpr int esz = FP8 ? 1 : 2;
+  __shared__ __align__(16) uint16_t As[2][BT * LDK];
+  __shared__ __align__(16) uint16_t Bs[2][BT * LDK];
   __shared__ uint16_t lut[256];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int tiles_n = (p.N + BN - 1) / BN;
-  const int m0 = (blockIdx.x / tiles_n) * BM, n0 = (blockIdx.x % tiles_n) * BN;
+  const int tiles_n = (p.N + BT - 1) / BT;
+  const int ntiles = gridDim.x;
+  const int t = (ntiles & 7) ? (int)blockIdx.x
+                             : (int)(blockIdx.x & 7) * (ntiles >> 3) + (int)(blockIdx.x >> 3);
+  const int m0 = (t / tiles_n) * BT, n0 = (t % tiles_n) * BT;
   const int b = blockIdx.y;
-  const bool fp8 = is_fp8(p.in_dt);
-  const int esz = fp8 ? 1 : 2;
-  if (fp8) {
+  if constexpr (FP8) {
+    lut[tid] = f32_to_f16_bits(fp8_to_f32((uint32_t)tid, p.in_dt));
+  }
+  const uint8_t* Ab = (const uint8_t*)p.A + (long long)b * p.sa_b * esz;
+  const uint8_t* Bb = (const uint8_t*)p.B + (long long)b * p.sb_b * esz;
+
+  auto vload = [&](const uint8_t* X, long long i) -> u4_t {
+    if constexpr (FP8) {
+      const u2_t w = *(const u2_t*)(X + i);
+      return u4_t{w.x, w.y, 0u, 0u};
+    } else {
+      return ldg128(X + 2 * i);
+    }
+  };
+  // piece h of operand X [rows][K] (rows from r0) at k0
+  auto fetch = [&](const uint8_t* X, int mode, int rows, int r0, long long s_r, long long s_k,
+                   int k0, int h) -> u4_t {
+    const int rs = 64 * (h % RP), ks = 32 * (h / RP);
+    long long off;
+    if (mode == MODE_RC) {  // s_r == 1
+      const int rc = r0 + rs + 8 * (tid & 7), kk = k0 + ks + (tid >> 3);
+      off = (long long)min(rc, (rows - 1) & ~7) + (long long)min(kk, p.K - 1) * s_k;
+    } else {                // s_k == 1
+      const int r = r0 + rs + (tid >> 2), kc = k0 + ks + 8 * (tid & 3);
+      off = (long long)min(r, rows - 1) * s_r + (long long)min(kc, (p.K - 1) & ~7);
+    }
+    return vload(X, off);
+  };
+  auto elem = [&](const u4_t& w, int e) -> uint32_t {
+    if constexpr (FP8) return (w[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+    else return (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+  };
+  auto cvt = [&](uint32_t x) -> uint32_t {
+    if constexpr (FP8) return (uint32_t)lut[x];
+    else return x;
+  };
+  // piece h (fetched at k0) into LDS buffer Xs, elements past the operand zeroed
+  auto put = [&](uint16_t* Xs, int mode, u4_t w, int rows, int r0, int k0, int h) {
+    const int rs = 64 * (h % RP), ks = 32 * (h / RP);
+    if (mode == MODE_RC) {
+      const int rc = rs + 8 * (tid & 7), kk = ks + (tid >> 3);
+      const int n = k0 + kk < p.K ? max(0, min(rows - r0 - rc, 8)) : 0;
+      if (n < 8) w = piece_keep<FP8>(w, n);
+      uint16_t* dst = Xs + tile_lds(rc, kk, LDK);  // rows rc .. rc + 7 share (r / 16) % 4
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e * LDK] = (uint16_t)cvt(elem(w, e));
+      return;
+    }
+    const int r = rs + (tid >> 2), kc = ks + 8 * (tid & 3);
+    const int n = r0 + r < rows ? max(0, min(p.K - k0 - kc, 8)) : 0;
+    if (n < 8) w = piece_keep<FP8>(w, n);
+    u4_t o = w;
+    if constexpr (FP8) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] = cvt(elem(w, 2 * d)) | (cvt(elem(w, 2 * d + 1)) << 16);
+    }
+    *(u4_t*)(Xs + tile_lds(r, kc, LDK)) = o;
+  };
+
+  f4_t acc[FT][FT];
+#pragma unroll
+  for (int i = 0; i < FT; ++i)
+#pragma unroll
+    for (int j = 0; j < FT; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (p.K + BK - 1) / BK;
+  u4_t ra0[NP], rb0[NP], ra1[NP], rb1[NP];
+  auto load_step = [&](u4_t* ra, u4_t* rb, int kt) {
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+      ra[h] = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, kt * BK, h);
+      rb[h] = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, kt * BK, h);
+    }
+  };
+  auto put_step = [&](int buf, const u4_t* ra, const u4_t* rb, int kt) {
+#pragma unroll
+    for (int h = 0; h < NP; ++h) {
+      put(As[buf], p.a_mode, ra[h], p.M, m0, kt * BK, h);
+      put(Bs[buf], p.b_mode, rb[h], p.N, n0, kt * BK, h);
+    }
+  };
+  const int q = lane >> 4, r16 = lane & 15;
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int s = 0; s < BK / 32; ++s) {
+      u4_t af[FT], bfr[FT];
+#pragma unroll
+      for (int i = 0; i < FT; ++i)
+        af[i] = *(const u4_t*)(As[buf] + tile_lds(WT * wm + 16 * i + r16, 32 * s + 8 * q, LDK));
+#pragma unroll
+      for (int j = 0; j < FT; ++j)
+        bfr[j] = *(const u4_t*)(Bs[buf] + tile_lds(WT * wn + 16 * j + r16, 32 * s + 8 * q, LDK));
+#pragma unroll
+      for (int i = 0; i < FT; ++i)
+#pragma unroll
+        for (int j = 0; j < FT; ++j) acc[i][j] = mfma16<BF16>(af[i], bfr[j], acc[i][j]);
+    }
+  };
+  // step kt: its operands are in LDS buffer kt & 1, step kt + 1's in the
+  // registers (rn), and the other set (rf) is free for step kt + 2
+  auto step = [&](int kt, u4_t* rfa, u4_t* rfb, const u4_t* rna, const u4_t* rnb) {
+    if (kt + 2 < nk) load_step(rfa, rfb, kt + 2);
+    compute(kt & 1);
+    if (kt + 1 < nk) put_step((kt + 1) & 1, rna, rnb, kt + 1);
+    __syncthreads();
+  };
+
+  load_step(ra0, rb0, 0);
+  if (nk > 1) load_step(ra1, rb1, 1);
+  if constexpr (FP8) __syncthreads();  // the table before the first store
+  put_step(0, ra0, rb0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, ra0, rb0, ra1, rb1);
+    if (kt + 1 < nk) step(kt + 1, ra1, rb1, ra0, rb0);
+  }
+
+  tile_epilogue<FT>(p, acc, m0, n0, b, WT, wm, wn, q, r16);
+}
+
+// ----------------------------------------------------------------------------
+// dot_tile_s_<f16|bf16|fp8>: some operand with neither k nor its rows
+// contiguous (or unaligned), grid (tiles_m * tiles_n, batch), block 256.
+// 64 x 64 output tile, 2 x 2 waves of 32 x 32, each 2 x 2 MFMA tiles of
+// 16 x 16 (v_mfma_f32_16x16x32: lane l supplies row l % 16, k 8 (l / 16) ..
+// +7 of each operand and holds D[4 (l / 16) + e][l % 16]); K in steps of 32
+// through two LDS buffers ([row][32 k + 8 pad]).  Each thread fetches 8
+// elements per operand and step, one bounds-checked load each:
+//   KC / SCALAR  row tid / 4, k 8 (tid % 4) .. +7
+//   RC           rows 8 (tid % 8) .. +7, k tid / 8
+// packed in registers (8 halves, or 8 FP8 codes in the low 8 bytes).
+// ----------------------------------------------------------------------------
+template <bool BF16, bool FP8>
+__device__ __forceinline__ void dot_tile_s_body(const DotParams& p) {
+  constexpr int BT = 64, BK = 32, LDK = BK + 8;
+  constexpr int esz = FP8 ? 1 : 2;
+  __shared__ __align__(16) uint16_t As[2][BT * LDK];
+  __shared__ __align__(16) uint16_t Bs[2][BT * LDK];
+  __shared__ uint16_t lut[256];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tiles_n = (p.N + BT - 1) / BT;
+  const int m0 = (blockIdx.x / tiles_n) * BT, n0 = (blockIdx.x % tiles_n) * BT;
+  const int b = blockIdx.y;
+  if constexpr (FP8) {
     lut[tid] = f32_to_f16_bits(fp8_to_f32((uint32_t)tid, p.in_dt));
     __syncthreads();
   }
   const uint8_t* Ab = (const uint8_t*)p.A + (long long)b * p.sa_b * esz;
   const uint8_t* Bb = (const uint8_t*)p.B + (long long)b * p.sb_b * esz;
 
-  // A raw element (16-bit bits or an FP8 code) of operand X at element offset i
-  auto raw = [&](const uint8_t* X, long long i) -> uint32_t {
-    return fp8 ? (uint32_t)X[i] : (uint32_t)((const uint16_t*)X)[i];
+  auto elem = [&](const u4_t& w, int e) -> uint32_t {
+    if constexpr (FP8) return (w[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+    else return (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
   };
-  // Fetch of one operand tile [64 rows][32 k] (rows m or n): 8 raw values per
-  // thread.  KC / SCALAR: row r = tid / 4, k = 8 (tid % 4) + e.  RC: rows
-  // 8 (tid % 8) + e, k = tid / 8.
-  struct Frag { uint32_t v[8]; };
+  auto pack = [&](u4_t& w, int e, uint32_t v) {
+    if constexpr (FP8) w[e >> 2] |= v << (8 * (e & 3));
+    else w[e >> 1] |= v << (16 * (e & 1));
+  };
+  auto raw = [&](const uint8_t* X, long long i) -> uint32_t {
+    if constexpr (FP8) return (uint32_t)X[i];
+    else return (uint32_t)((const uint16_t*)X)[i];
+  };
+  // the thread's 8 elements of operand X [rows][K] (rows from r0) at k0
   auto fetch = [&](const uint8_t* X, int mode, int rows, int r0, long long s_r, long long s_k,
-                   int k0, Frag& f) {
+                   int k0) -> u4_t {
+    u4_t w = u4_t{0u, 0u, 0u, 0u};
     if (mode == MODE_RC) {
-      const int rc = 8 * (tid & 7), kk = k0 + (tid >> 3);
-      const long long base = (long long)(r0 + rc) * s_r + (long long)kk * s_k;
-      if (kk < p.K && r0 + rc + 8 <= rows) {
-        if (fp8) {
-          const u2_t w = *(const u2_t*)(X + base);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f.v[e] = ((e < 4 ? w.x : w.y) >> (8 * (e & 3))) & 0xFFu;
-        } else {
-          const u4_t w = ldg128(X + 2 * base);
-          const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f.v[e] = (d[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          f.v[e] = (kk < p.K && r0 + rc + e < rows) ? raw(X, base + (long long)e * s_r) : 0u;
-      }
-      return;
-    }
-    const int r = tid >> 2, kc = k0 + 8 * (tid & 3);
-    const long long base = (long long)(r0 + r) * s_r + (long long)kc * s_k;
-    if (mode == MODE_KC && r0 + r < rows && kc + 8 <= p.K) {
-      if (fp8) {
-        const u2_t w = *(const u2_t*)(X + base);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f.v[e] = ((e < 4 ? w.x : w.y) >> (8 * (e & 3))) & 0xFFu;
-      } else {
-        const u4_t w = ldg128(X + 2 * base);
-        const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f.v[e] = (d[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-      }
-    } else {
+      const int rc = r0 + 8 * (tid & 7), kk = k0 + (tid >> 3);
+      if (kk >= p.K) return w;
+      const long long base = (long long)rc * s_r + (long long)kk * s_k;
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        f.v[e] = (r0 + r < rows && kc + e < p.K) ? raw(X, base + (long long)e * s_k) : 0u;
+        if (rc + e < rows) pack(w, e, raw(X, base + (long long)e * s_r));
+      return w;
     }
+    const int r = r0 + (tid >> 2), kc = k0 + 8 * (tid & 3);
+    if (r >= rows) return w;
+    const long long base = (long long)r * s_r + (long long)kc * s_k;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (kc + e < p.K) pack(w, e, raw(X, base + (long long)e * s_k));
+    return w;
   };
-  auto cvt = [&](uint32_t x) -> uint32_t { return fp8 ? (uint32_t)lut[x] : x; };
-  auto put = [&](uint16_t* Xs, int mode, const Frag& f) {
+  auto cvt = [&](uint32_t x) -> uint32_t {
+    if constexpr (FP8) return (uint32_t)lut[x];
+    else return x;
+  };
+  auto put = [&](uint16_t* Xs, int mode, u4_t w) {
     if (mode == MODE_RC) {
       const int rc = 8 * (tid & 7), kk = tid >> 3;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Xs[(rc + e) * LDK + kk] = (uint16_t)cvt(f.v[e]);
-    } else {
-      const int r = tid >> 2, kc = 8 * (tid & 3);
-      u4_t w;
-      w.x = cvt(f.v[0]) | (cvt(f.v[1]) << 16);
-      w.y = cvt(f.v[2]) | (cvt(f.v[3]) << 16);
-      w.z = cvt(f.v[4]) | (cvt(f.v[5]) << 16);
-      w.w = cvt(f.v[6]) | (cvt(f.v[7]) << 16);
-      *(u4_t*)&Xs[r * LDK + kc] = w;
+      for (int e = 0; e < 8; ++e) Xs[(rc + e) * LDK + kk] = (uint16_t)cvt(elem(w, e));
+      return;
     }
+    const int r = tid >> 2, kc = 8 * (tid & 3);
+    u4_t o = w;
+    if constexpr (FP8) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) o[d] = cvt(elem(w, 2 * d)) | (cvt(elem(w, 2 * d + 1)) << 16);
+    }
+    *(u4_t*)&Xs[r * LDK + kc] = o;
   };
 
   f4_t acc[2][2];
@@ -191,10 +403,9 @@ __device__ __forceinline__ void dot_tile_body(const DotParams& p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  Frag fa, fb;
   const int nk = (p.K + BK - 1) / BK;
-  fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, 0, fa);
-  fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, 0, fb);
+  u4_t fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, 0);
+  u4_t fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, 0);
   put(As[0], p.a_mode, fa);
   put(Bs[0], p.b_mode, fb);
   __syncthreads();
@@ -202,8 +413,8 @@ __device__ __forceinline__ void dot_tile_body(const DotParams& p) {
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nk) {
-      fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, (kt + 1) * BK, fa);
-      fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, (kt + 1) * BK, fb);
+      fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, (kt + 1) * BK);
+      fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, (kt + 1) * BK);
     }
     u4_t af[2], bfr[2];
 #pragma unroll
@@ -222,38 +433,28 @@ __device__ __forceinline__ void dot_tile_body(const DotParams& p) {
     }
     __syncthreads();
   }
-
-  // epilogue: lane holds rows 32 wm + 16 i + 4 q + e, column 32 wn + 16 j + r16
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + 32 * wn + 16 * j + r16;
-      if (col >= p.N) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = m0 + 32 * wm + 16 * i + 4 * q + e;
-        if (row >= p.M) continue;
-        float v = acc[i][j][e];
-        const long long zb = (long long)b * p.sz_b;
-        if (p.epi == EPI_ADD_MATRIX)
-          v += load_elem(p.Z, zb + (long long)row * p.sz_m + (long long)col * p.sz_n, p.z_dt);
-        else if (p.epi == EPI_ADD_ROWS)
-          v += load_elem(p.Z, zb + (long long)row * p.sz_m, p.z_dt);
-        else if (p.epi == EPI_ADD_COLS)
-          v += load_elem(p.Z, zb + (long long)col * p.sz_n, p.z_dt);
-        store_elem(p.C, (long long)b * p.sc_b + (long long)row * p.sc_m + (long long)col * p.sc_n,
-                   p.out_dt, v);
-      }
-    }
+  tile_epilogue<2>(p, acc, m0, n0, b, 32, wm, wn, q, r16);
 }
 
-extern "C" __global__ __launch_bounds__(256) void dot_tile_f16(DotParams p) {
-  dot_tile_body<false>(p);
-}
-extern "C" __global__ __launch_bounds__(256) void dot_tile_bf16(DotParams p) {
-  dot_tile_body<true>(p);
-}
+// dot_tile{,128}_<f16|bf16|fp8> and dot_tile_s_<f16|bf16|fp8>: fp8 covers
+// the five FP8 formats (in_dt), decoded to fp16 through the table
+#define TM_DOT_TILE(NAME, BF16, FP8, BT)                                            \
+  extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {             \
+    dot_tile_vec_body<BF16, FP8, BT>(p);                                            \
+  }
+#define TM_DOT_TILE_S(NAME, BF16, FP8)                                              \
+  extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {             \
+    dot_tile_s_body<BF16, FP8>(p);                                                  \
+  }
+TM_DOT_TILE(dot_tile_f16, false, false, 64)
+TM_DOT_TILE(dot_tile_bf16, true, false, 64)
+TM_DOT_TILE(dot_tile_fp8, false, true, 64)
+TM_DOT_TILE(dot_tile128_f16, false, false, 128)
+TM_DOT_TILE(dot_tile128_bf16, true, false, 128)
+TM_DOT_TILE(dot_tile128_fp8, false, true, 128)
+TM_DOT_TILE_S(dot_tile_s_f16, false, false)
+TM_DOT_TILE_S(dot_tile_s_bf16, true, false)
+TM_DOT_TILE_S(dot_tile_s_fp8, false, true)
 
 // ----------------------------------------------------------------------------
 // dot_tile_f32: fp32 inputs with the none / add-* epilogues on the fp32 MFMA
@@ -263,13 +464,16 @@ extern "C" __global__ __launch_bounds__(256) void dot_tile_bf16(DotParams p) {
 // (A[l % 16][l / 16], B[l / 16][l % 16], D[4 (l / 16) + e][l % 16]).  K in
 // steps of 16 through two LDS buffers, both operands k-major there
 // ([16 k][64 + 16 pad] floats: a 16-lane operand read is 16 consecutive
-// floats, the four k rows of one read 16 banks apart).  Fetch modes of an
-// operand [64 rows][16 k]: KC  row tid / 4, 4 k from 4 (tid % 4), one
-// 16-byte load; RC  k tid / 16, 4 rows from 4 (tid % 16), one 16-byte load
-// stored as one 16-byte LDS write; SCALAR  the KC mapping element by element.
-// Rows and k past the operand read as zero.
+// floats, the four k rows of one read 16 banks apart).  Pieces of 4 floats
+// per thread and operand: KC / SCALAR  row tid / 4, k 4 (tid % 4) .. +3;
+// RC  k tid / 16, rows 4 (tid % 16) .. +3 (stored as one 16-byte LDS write).
+// VEC (both operands KC or RC): one unconditional 16-byte load per piece,
+// moved back to the last piece holding a valid element when past the
+// operand, and the elements past it zeroed at the LDS store, as in dot_tile;
+// dot_tile_s_f32: element loads, each bounds-checked.
 // ----------------------------------------------------------------------------
-extern "C" __global__ __launch_bounds__(256) void dot_tile_f32(DotParams p) {
+template <bool VEC>
+__device__ __forceinline__ void dot_tile_f32_body(const DotParams& p) {
   constexpr int TB = 64, TK = 16, TS = TB + 16;
   __shared__ __align__(16) float As[2][TK * TS], Bs[2][TK * TS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -280,37 +484,52 @@ extern "C" __global__ __launch_bounds__(256) void dot_tile_f32(DotParams p) {
   const float* Ab = (const float*)p.A + (long long)b * p.sa_b;
   const float* Bb = (const float*)p.B + (long long)b * p.sb_b;
 
+  // piece of operand X [rows][K] (rows from r0) at k0; n = its count of valid
+  // elements (VEC: applied when the piece is stored)
   auto fetch = [&](const float* X, int mode, int rows, int r0, long long s_r, long long s_k,
-                   int k0) -> f4_t {
-    f4_t v = f4_t{0.f, 0.f, 0.f, 0.f};
-    if (mode == MODE_RC) {  // s_r == 1
-      const int kk = k0 + (tid >> 4), rc = r0 + 4 * (tid & 15);
-      if (kk < p.K) {
-        const float* q = X + rc + (long long)kk * s_k;
-        if (rc + 3 < rows) {
-          v = *(const f4_t*)q;
-        } else {
+                   int k0, int& n) -> f4_t {
+    if constexpr (VEC) {
+      long long off;
+      if (mode == MODE_RC) {  // s_r == 1
+        const int rc = r0 + 4 * (tid & 15), kk = k0 + (tid >> 4);
+        off = (long long)min(rc, (rows - 1) & ~3) + (long long)min(kk, p.K - 1) * s_k;
+        n = kk < p.K ? max(0, min(rows - rc, 4)) : 0;
+      } else {                // s_k == 1
+        const int r = r0 + (tid >> 2), kc = k0 + 4 * (tid & 3);
+        off = (long long)min(r, rows - 1) * s_r + (long long)min(kc, (p.K - 1) & ~3);
+        n = r < rows ? max(0, min(p.K - kc, 4)) : 0;
+      }
+      return *(const f4_t*)(X + off);
+    } else {
+      n = 4;
+      f4_t v = f4_t{0.f, 0.f, 0.f, 0.f};
+      if (mode == MODE_RC) {
+        const int rc = r0 + 4 * (tid & 15), kk = k0 + (tid >> 4);
+        if (kk < p.K) {
+          const float* q = X + (long long)rc * s_r + (long long)kk * s_k;
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            if (rc + j < rows) v[j] = q[j];
+            if (rc + j < rows) v[j] = q[(long long)j * s_r];
         }
+        return v;
       }
-      return v;
-    }
-    const int r = r0 + (tid >> 2), kc = k0 + 4 * (tid & 3);
-    if (r < rows) {
-      const float* q = X + (long long)r * s_r + (long long)kc * s_k;
-      if (mode == MODE_KC && kc + 3 < p.K) {
-        v = *(const f4_t*)q;
-      } else {
+      const int r = r0 + (tid >> 2), kc = k0 + 4 * (tid & 3);
+      if (r < rows) {
+        const float* q = X + (long long)r * s_r + (long long)kc * s_k;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           if (kc + j < p.K) v[j] = q[(long long)j * s_k];
       }
+      return v;
     }
-    return v;
   };
-  auto put = [&](float* Xs, int mode, f4_t v) {
+  auto put = [&](float* Xs, int mode, f4_t v, int n) {
+    if constexpr (VEC) {
+      if (n < 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = j < n ? v[j] : 0.f;
+      }
+    }
     if (mode == MODE_RC) {
       *(f4_t*)&Xs[(tid >> 4) * TS + 4 * (tid & 15)] = v;
     } else {
@@ -325,17 +544,18 @@ extern "C" __global__ __launch_bounds__(256) void dot_tile_f32(DotParams p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
   const int nk = (p.K + TK - 1) / TK;
-  f4_t fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, 0);
-  f4_t fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, 0);
-  put(As[0], p.a_mode, fa);
-  put(Bs[0], p.b_mode, fb);
+  int xa, xb;
+  f4_t fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, 0, xa);
+  f4_t fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, 0, xb);
+  put(As[0], p.a_mode, fa, xa);
+  put(Bs[0], p.b_mode, fb, xb);
   __syncthreads();
   const int q = lane >> 4, r16 = lane & 15;
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nk) {
-      fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, (kt + 1) * TK);
-      fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, (kt + 1) * TK);
+      fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, (kt + 1) * TK, xa);
+      fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, (kt + 1) * TK, xb);
     }
     const float* as = As[buf];
     const float* bs = Bs[buf];
@@ -355,35 +575,20 @@ extern "C" __global__ __launch_bounds__(256) void dot_tile_f32(DotParams p) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], bv[j], acc[i][j], 0, 0, 0);
     }
     if (kt + 1 < nk) {
-      put(As[buf ^ 1], p.a_mode, fa);
-      put(Bs[buf ^ 1], p.b_mode, fb);
+      put(As[buf ^ 1], p.a_mode, fa, xa);
+      put(Bs[buf ^ 1], p.b_mode, fb, xb);
     }
     __syncthreads();
   }
 
-  // epilogue: lane holds rows 32 wm + 16 i + 4 q + e, column 32 wn + 16 j + r16
-  const long long zb = (long long)b * p.sz_b;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + 32 * wn + 16 * j + r16;
-      if (col >= p.N) continue;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = m0 + 32 * wm + 16 * i + 4 * q + e;
-        if (row >= p.M) continue;
-        float v = acc[i][j][e];
-        if (p.epi == EPI_ADD_MATRIX)
-          v += load_elem(p.Z, zb + (long long)row * p.sz_m + (long long)col * p.sz_n, p.z_dt);
-        else if (p.epi == EPI_ADD_ROWS)
-          v += load_elem(p.Z, zb + (long long)row * p.sz_m, p.z_dt);
-        else if (p.epi == EPI_ADD_COLS)
-          v += load_elem(p.Z, zb + (long long)col * p.sz_n, p.z_dt);
-        store_elem(p.C, (long long)b * p.sc_b + (long long)row * p.sc_m + (long long)col * p.sc_n,
-                   p.out_dt, v);
-      }
-    }
+  tile_epilogue<2>(p, acc, m0, n0, b, 32, wm, wn, q, r16);
+}
+
+extern "C" __global__ __launch_bounds__(256) void dot_tile_f32(DotParams p) {
+  dot_tile_f32_body<true>(p);
+}
+extern "C" __global__ __launch_bounds__(256) void dot_tile_s_f32(DotParams p) {
+  dot_tile_f32_body<false>(p);
 }
 
 // ----------------------------------------------------------------------------
