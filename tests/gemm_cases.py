@@ -30,13 +30,15 @@ for fam, (M, N, K) in FAMILIES.items():
             CASES.append(("nn", M, N, K, dt, out, False))
             for bias in (False, True):
                 CASES.append(("nt", M, N, K, dt, out, bias))
-# fp32 inputs (the fp32-MFMA 64-tile kernel), every output dtype, sizes that
-# are not multiples of its tiles
-F32_SHAPE = (150, 130, 70)
-for out in (F32, F16, BF16):
-    CASES.append(("nn", *F32_SHAPE, F32, out, False))
-    for bias in (False, True):
-        CASES.append(("nt", *F32_SHAPE, F32, out, bias))
+# fp32 inputs (the fp32-MFMA 64-tile kernels), every output dtype, sizes that
+# are not multiples of its tiles: leading dimensions multiples of 4 (16-byte
+# operand pieces, gemm_f32t64) and not (element loads, gemm_f32t64u)
+F32_SHAPES = {"f32t64": (150, 132, 68), "f32t64u": (150, 130, 70)}
+for shape in F32_SHAPES.values():
+    for out in (F32, F16, BF16):
+        CASES.append(("nn", *shape, F32, out, False))
+        for bias in (False, True):
+            CASES.append(("nt", *shape, F32, out, bias))
 # the general kernel: 16-bit inputs with K % 8 != 0
 CASES += [("nn", 37, 53, 29, F16, F16, False), ("nt", 40, 48, 20, BF16, F32, True)]
 

@@ -31,11 +31,11 @@ def test_cases_cover_every_dense_kernel(gemm_kernels):
 
 @pytest.mark.parametrize("case", CASES, ids=[case_id(c) for c in CASES])
 def test_case_reaches_its_family(case):
-    from gemm_cases import FAMILIES
+    from gemm_cases import F32_SHAPES, FAMILIES
     form, M, N, K, dt, out, bias = case
     fam = next((f for f, s in FAMILIES.items() if s == (M, N, K)), "general")
     if dt == torch.float32:
-        fam = "f32t64"
+        fam = next(f for f, s in F32_SHAPES.items() if s == (M, N, K))
     name = plan(case)
     assert name.startswith(f"gemm_{fam}_" if fam != "general" else "gemm_general"), name
 
@@ -44,8 +44,16 @@ def test_plan_follows_alignment_and_leading_dimensions():
     # unaligned A / B, or a leading dimension that is not a multiple of 8,
     # leave the MFMA kernels; an unaligned C leaves the 32-tile K-split kernel
     assert tm.gemm_kernel_for(512, 512, 512, align=_lib.TM_GEMM_ALIGN_C16)[0] == "gemm_general"
-    # fp32 inputs take the fp32-MFMA kernel whatever the alignment
-    assert tm.gemm_kernel_for(5, 7, 3, in_dtype=torch.float32, align=0)[0] == "gemm_f32t64_nn_f32"
+    # fp32 inputs take the fp32-MFMA kernels whatever the alignment: 16-byte
+    # pieces for aligned operands with leading dimensions multiples of 4
+    f32 = torch.float32
+    assert tm.gemm_kernel_for(5, 7, 3, in_dtype=f32, align=0)[0] == "gemm_f32t64u_nn_f32"
+    assert tm.gemm_kernel_for(5, 8, 4, in_dtype=f32)[0] == "gemm_f32t64_nn_f32"
+    assert tm.gemm_kernel_for(5, 8, 4, in_dtype=f32, align=_lib.TM_GEMM_ALIGN_C16)[0] == \
+        "gemm_f32t64u_nn_f32"
+    assert tm.gemm_kernel_for(5, 7, 4, in_dtype=f32, trans_b=True)[0] == "gemm_f32t64_nt_f32"
+    assert tm.gemm_kernel_for(5, 7, 4, in_dtype=f32, ldb=6, trans_b=True)[0] == \
+        "gemm_f32t64u_nt_f32"
     assert tm.gemm_kernel_for(512, 512, 512, lda=516)[0] == "gemm_general"
     assert tm.gemm_kernel_for(512, 512, 512)[0] == "gemm_s32k128_nn_f16_same"
     assert tm.gemm_kernel_for(512, 512, 512, align=_lib.TM_GEMM_ALIGN_AB16)[0].startswith(

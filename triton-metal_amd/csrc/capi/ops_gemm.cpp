@@ -330,8 +330,11 @@ void gemm_plan(int M, int N, int K, int lda, int ldb, int ldc, bool bt, bool bia
   pl->general = false;
   if (idt == TM_DT_F32) {
     // fp32 inputs (the reference's default dtype): 64 x 64 tiles on the fp32
-    // MFMA (gemm_f32.hip), any leading dimensions and alignment
-    snprintf(pl->name, sizeof pl->name, "gemm_f32t64_%s_%s%s", bt ? "nt" : "nn",
+    // MFMA (gemm_f32.hip); 16-byte operand pieces when A and B are 16-byte
+    // aligned with leading dimensions multiples of 4 (gemm_f32t64), else
+    // element loads (gemm_f32t64u)
+    const bool vec = ab16 && lda % 4 == 0 && ldb % 4 == 0;
+    snprintf(pl->name, sizeof pl->name, "gemm_f32t64%s_%s_%s%s", vec ? "" : "u", bt ? "nt" : "nn",
              odt == TM_DT_F32 ? "f32" : odt == TM_DT_F16 ? "f16" : "bf16",
              (bt && bias) ? "_bias" : "");
     pl->grid = (unsigned)(((M + 63) / 64) * ((N + 63) / 64));

@@ -14,9 +14,19 @@
 // next step's global loads are in flight in registers while the current step
 // multiplies.  Both operands sit in LDS k-major, [16 k][64 (+16 pad) m or n],
 // so a 16-lane operand read is 16 consecutive floats and the four k rows of
-// one read land 16 banks apart.  Global loads are 16-byte row pieces where
-// the leading dimension and base allow it, else single elements; rows and k
-// past the matrix read as zero.
+// one read land 16 banks apart.  Rows and k past the matrix count as zero.
+//
+// gemm_f32t64_* (A and B 16-byte aligned, leading dimensions multiples of 4):
+// each thread's piece of 4 floats per operand and step is one unconditional
+// 16-byte load.  A piece starts at a multiple of 4 of an aligned row; one
+// past the matrix is moved to the last piece holding an element of it (row
+// at most rows - 1, k or n at most its extent - 1), so every load reads an
+// aligned chunk holding a valid element (never a page the matrix does not
+// touch), and the elements past the matrix are zeroed when the piece is
+// stored to LDS.  A load whose registers another branch also wrote would
+// make the compiler wait for it on the spot, which is what the unconditional
+// form avoids: the next step's loads stay in flight across the MFMAs.
+// gemm_f32t64u_*: any alignment, element loads each bounds-checked.
 #include "common.h"
 
 namespace {
@@ -31,21 +41,34 @@ template <int ODT> TM_DEV void f32_store(void* C, size_t i, float v) {
   else ((uint16_t*)C)[i] = f32_to_bf16_bits(v);
 }
 
-// 4 consecutive floats of row r at k .. k+3 (zero past rows / k); vec: the
-// row pieces are 16-byte aligned
-TM_DEV f4_t f32_row4(const float* __restrict__ P, long ld, int r, int rows, int k, int K,
-                     bool vec) {
+// 4 consecutive floats of row r at k .. k+3, element by element (zero past
+// rows / k)
+TM_DEV f4_t f32_row4(const float* __restrict__ P, long ld, int r, int rows, int k, int K) {
   f4_t v = f4_t{0.f, 0.f, 0.f, 0.f};
   if (r >= rows) return v;
   const float* p = P + (size_t)r * ld + k;
-  if (vec && k + 3 < K) return *(const f4_t*)p;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
     if (k + j < K) v[j] = p[j];
   return v;
 }
 
-template <bool BT, int ODT, bool BIAS>
+// The 16-byte piece of row r at k .. k+3 (k a multiple of 4, rows >= 1,
+// K >= 1), moved back into the matrix when past it; its elements past the
+// matrix are zeroed by f32_keep.
+TM_DEV f4_t f32_piece(const float* __restrict__ P, long ld, int r, int rows, int k, int K) {
+  return *(const f4_t*)(P + (size_t)min(r, rows - 1) * ld + min(k, (K - 1) & ~3));
+}
+TM_DEV f4_t f32_keep(f4_t v, int r, int rows, int k, int K) {
+  const int n = r < rows ? max(0, min(K - k, 4)) : 0;
+  if (n < 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = j < n ? v[j] : 0.f;
+  }
+  return v;
+}
+
+template <bool BT, int ODT, bool BIAS, bool VEC>
 __device__ __forceinline__ void gemm_f32_body(const float* __restrict__ A,
                                               const float* __restrict__ B, void* __restrict__ C,
                                               const float* __restrict__ bias, int M, int N, int K,
@@ -55,32 +78,29 @@ __device__ __forceinline__ void gemm_f32_body(const float* __restrict__ A,
   const int wm = wave >> 1, wn = wave & 1;
   const int ntn = (N + FB - 1) / FB;
   const int m0 = (int)(blockIdx.x / ntn) * FB, n0 = (int)(blockIdx.x % ntn) * FB;
-  const bool avec = lda % 4 == 0 && ((uintptr_t)A & 15u) == 0;
-  const bool bvec = ldb % 4 == 0 && ((uintptr_t)B & 15u) == 0;
   // global -> registers: A (and W of nt) as row r = tid / 4, k piece 4 (tid % 4);
   // B of nn as k row tid / 16, n piece 4 (tid % 16)
   const int ar = tid >> 2, ak = 4 * (tid & 3);
   const int bk = tid >> 4, bn = 4 * (tid & 15);
   f4_t ra, rb;
   auto load = [&](int k0) {
-    ra = f32_row4(A, lda, m0 + ar, M, k0 + ak, K, avec);
-    if constexpr (BT) {
-      rb = f32_row4(B, ldb, n0 + ar, N, k0 + ak, K, bvec);
+    if constexpr (VEC) {
+      ra = f32_piece(A, lda, m0 + ar, M, k0 + ak, K);
+      if constexpr (BT) rb = f32_piece(B, ldb, n0 + ar, N, k0 + ak, K);
+      else rb = f32_piece(B, ldb, k0 + bk, K, n0 + bn, N);
     } else {
-      rb = f4_t{0.f, 0.f, 0.f, 0.f};
-      if (k0 + bk < K) {
-        const float* p = B + (size_t)(k0 + bk) * ldb + n0 + bn;
-        if (bvec && n0 + bn + 3 < N) {
-          rb = *(const f4_t*)p;
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (n0 + bn + j < N) rb[j] = p[j];
-        }
-      }
+      ra = f32_row4(A, lda, m0 + ar, M, k0 + ak, K);
+      if constexpr (BT) rb = f32_row4(B, ldb, n0 + ar, N, k0 + ak, K);
+      else rb = f32_row4(B, ldb, k0 + bk, K, n0 + bn, N);
     }
   };
-  auto stash = [&](int buf) {
+  // the pieces loaded at k0 into LDS buffer buf
+  auto stash = [&](int buf, int k0) {
+    if constexpr (VEC) {
+      ra = f32_keep(ra, m0 + ar, M, k0 + ak, K);
+      if constexpr (BT) rb = f32_keep(rb, n0 + ar, N, k0 + ak, K);
+      else rb = f32_keep(rb, k0 + bk, K, n0 + bn, N);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) As[buf][(ak + j) * FS + ar] = ra[j];
     if constexpr (BT) {
@@ -99,7 +119,7 @@ __device__ __forceinline__ void gemm_f32_body(const float* __restrict__ A,
   const int l16 = lane & 15, q = lane >> 4;
   const int nst = (K + FK - 1) / FK;
   load(0);
-  stash(0);
+  stash(0, 0);
   __syncthreads();
   for (int s = 0; s < nst; ++s) {
     const int buf = s & 1;
@@ -121,7 +141,7 @@ __device__ __forceinline__ void gemm_f32_body(const float* __restrict__ A,
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
-    if (s + 1 < nst) stash(buf ^ 1);
+    if (s + 1 < nst) stash(buf ^ 1, (s + 1) * FK);
     __syncthreads();
   }
   // D[4 q + e][l16] of tile (i, j)
@@ -142,14 +162,17 @@ __device__ __forceinline__ void gemm_f32_body(const float* __restrict__ A,
 
 }  // namespace
 
-// gemm_f32t64_<nn|nt>_<out>[_bias]: out f32 / f16 / bf16; grid =
+// gemm_f32t64{,u}_<nn|nt>_<out>[_bias]: out f32 / f16 / bf16; grid =
 // ceil(M / 64) * ceil(N / 64), block = 256
-#define TM_GEMM_F32(BTN, BT, OUT, ODT, BIAS, SUF)                                               \
-  extern "C" __global__ __launch_bounds__(256) void gemm_f32t64_##BTN##_##OUT##SUF(             \
+#define TM_GEMM_F32_V(KN, VEC, BTN, BT, OUT, ODT, BIAS, SUF)                                     \
+  extern "C" __global__ __launch_bounds__(256) void KN##_##BTN##_##OUT##SUF(                    \
       const float* A, const float* B, void* C, const float* bias, int M, int N, int K, int lda, \
       int ldb, int ldc) {                                                                       \
-    gemm_f32_body<BT, ODT, BIAS>(A, B, C, bias, M, N, K, lda, ldb, ldc);                        \
+    gemm_f32_body<BT, ODT, BIAS, VEC>(A, B, C, bias, M, N, K, lda, ldb, ldc);                   \
   }
+#define TM_GEMM_F32(BTN, BT, OUT, ODT, BIAS, SUF)                 \
+  TM_GEMM_F32_V(gemm_f32t64, true, BTN, BT, OUT, ODT, BIAS, SUF)  \
+  TM_GEMM_F32_V(gemm_f32t64u, false, BTN, BT, OUT, ODT, BIAS, SUF)
 #define TM_GEMM_F32_OUT(OUT, ODT)                 \
   TM_GEMM_F32(nn, false, OUT, ODT, false, )       \
   TM_GEMM_F32(nt, true, OUT, ODT, false, )        \
