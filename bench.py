@@ -346,6 +346,9 @@ EXTRA = {"hbm_copy": hbm_copy,
          "w4a16_m32_k14336": lambda d: w4a16_wide_k(d, 32),
          "w4a16_m64_k14336": lambda d: w4a16_wide_k(d, 64),
          "w4a16_m8_k28672": lambda d: w4a16_wide_k(d, 8, K=28672, N=8192),
+         # the 64 x 64 tiled kernel (int4, K = 11008 past the wide kernels)
+         "w4a16_m128_k11008": lambda d: w4a16_wide_k(d, 128, K=11008),
+         "w4a16_m512_k11008": lambda d: w4a16_wide_k(d, 512, K=11008),
          "w8a16_m1_k14336": lambda d: w8a16_wide_k(d, 1),
          "w8a16_m16_k14336": lambda d: w8a16_wide_k(d, 16),
          # split-K plans (the Python operators pass a workspace)

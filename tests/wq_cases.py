@@ -87,10 +87,16 @@ CASES += _each(4, 2, 64, 5120, G=256)
 CASES += _each(4, 2, 64, 36864, ws=False)
 CASES += _each(8, 1, 64, 1024)
 # tiled (M > 64 with K past the streaming kernels' 4096; int4 M > 16 with K
-# past 16384 and no workspace)
-CASES += _each(4, 80, 64, 8192)
+# past 16384 and no workspace): one launch without a workspace, split-K with
+# one (fewer tiles than CUs: 16 slices of 2 steps at K = 8192; 9 slices, the
+# last of one step, at K = 4352; 15 slices, the last of one step, at
+# K = 11008)
+CASES += _each(4, 80, 64, 8192, ws=False)
 CASES += _each(4, 20, 64, 20480, acts=(torch.bfloat16,), ws=False)
+CASES += _each(8, 80, 64, 4352, ws=False)
+CASES += _each(4, 80, 64, 8192)
 CASES += _each(8, 80, 64, 4352)
+CASES += _each(4, 128, 256, 11008, acts=(torch.float16,), zeros=("s",))
 # general fp32 kernel
 CASES += [(4, 3, 40, 100, 32, torch.float32, None, True),
           (8, 3, 40, 100, 1, torch.float32, "s", True)]

@@ -45,18 +45,21 @@ Kernel& kernel(const std::string& name) {
 // Split-K plans (split_ok: the caller supplies a workspace) run the split-K
 // form of a kernel over `splits` k-slices, grid (grid, splits), writing fp32
 // [splits][M][N] into the workspace, then wq_splitk_reduce_<act>.
-enum { WQ_ARGS_STD = 0, WQ_ARGS_G = 1, WQ_ARGS_GENERAL = 2, WQ_ARGS_SPLIT = 3 };
+enum { WQ_ARGS_STD = 0, WQ_ARGS_G = 1, WQ_ARGS_GENERAL = 2, WQ_ARGS_SPLIT = 3,
+       WQ_ARGS_SPLIT_G = 4 };
 struct WqPlan {
   char name[64];
   unsigned grid, block, lds;
   int form;       // argument list: WQ_ARGS_*
   int splits;     // k-slices (1: no split)
+  int kslice;     // k per slice (the last may be shorter: WQ_ARGS_SPLIT_G)
   size_t ws;      // workspace bytes (split-K plans)
 };
 
 void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, unsigned align,
              int cus, size_t max_lds, bool split_ok, WqPlan* pl) {
   pl->splits = 1;
+  pl->kslice = K;
   pl->ws = 0;
   auto set = [&](unsigned grid, unsigned block, size_t lds, int form) {
     pl->grid = grid;
@@ -108,6 +111,7 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
                  S > 1 ? "_k" : "");
         set(8 * mtl * ((ntl + 7) / 8), 512, wl, S > 1 ? WQ_ARGS_SPLIT : WQ_ARGS_STD);
         pl->splits = S;
+        pl->kslice = K / S;
         pl->ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
         return;
       }
@@ -221,6 +225,7 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
                  zc, nt, xr, multi ? 'm' : 's', nch, S > 1 ? "_k" : "");
         set((tiles + nt - 1) / nt, 64 * nwv, slds, S > 1 ? WQ_ARGS_SPLIT : WQ_ARGS_STD);
         pl->splits = S;
+        pl->kslice = K / S;
         pl->ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
         return;
       }
@@ -243,10 +248,24 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
     snprintf(pl->name, sizeof pl->name, "wq_skinny_q%d_%s_z%c%s", qbits, act, zc, vs ? "_v" : "");
     return set(N / 16, 256, lds, WQ_ARGS_G);
   }
+  // tiled kernel: 64 x 64 output tiles walking K in steps of 256.  With a
+  // workspace and fewer tiles than CUs: split-K over slices of whole steps
+  // (the last one shorter), about two workgroups per CU, at most 16 slices
   if (fast && K % 256 == 0 && N % 64 == 0) {
-    snprintf(pl->name, sizeof pl->name, "wq_tiled_q%d_%s_z%c", qbits, act, zc);
-    const int tiles = ((M + 63) / 64) * (N / 64);
-    return set((tiles + 7) / 8 * 8, 256, 0, WQ_ARGS_G);
+    const int tiles = ((M + 63) / 64) * (N / 64), steps = K / 256;
+    int S = 1, per = steps;
+    if (split_ok && tiles < cus && steps > 1) {
+      const int want = std::min(std::min(16, (2 * cus + tiles - 1) / tiles), steps);
+      per = (steps + want - 1) / want;
+      S = (steps + per - 1) / per;
+    }
+    snprintf(pl->name, sizeof pl->name, "wq_tiled_q%d_%s_z%c%s", qbits, act, zc,
+             S > 1 ? "_k" : "");
+    set((tiles + 7) / 8 * 8, 256, 0, S > 1 ? WQ_ARGS_SPLIT_G : WQ_ARGS_G);
+    pl->splits = S;
+    pl->kslice = per * 256;
+    pl->ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+    return;
   }
   snprintf(pl->name, sizeof pl->name, "wq_general");
   set((N + 3) / 4, 256, 0, WQ_ARGS_GENERAL);
@@ -293,10 +312,14 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
   Kernel& k = kernel(pl.name);
   const dim3 grid(pl.grid), block(pl.block);
   switch (pl.form) {
-    case WQ_ARGS_SPLIT: {
+    case WQ_ARGS_SPLIT:
+    case WQ_ARGS_SPLIT_G: {
       float* P = (float*)workspace;
-      int rc = launch(k, dim3(pl.grid, (unsigned)pl.splits), block, pl.lds, stream, X, W, P, S, Z,
-                      M, N, K / pl.splits, K);
+      int rc = pl.form == WQ_ARGS_SPLIT
+                   ? launch(k, dim3(pl.grid, (unsigned)pl.splits), block, pl.lds, stream, X, W, P,
+                            S, Z, M, N, pl.kslice, K)
+                   : launch(k, dim3(pl.grid, (unsigned)pl.splits), block, pl.lds, stream, X, W, P,
+                            S, Z, M, N, pl.kslice, K, G);
       if (rc) return rc;
       const size_t quads = (size_t)M * N / 4;
       return launch(kernel(adt == TM_DT_BF16 ? "wq_splitk_reduce_bf16" : "wq_splitk_reduce_f16"),

@@ -1079,15 +1079,25 @@ __device__ __forceinline__ void wq_stream_body(const uint16_t* X, const uint8_t*
 // Preconditions: K % 256 == 0, N % 64 == 0, int4: G % 128 == 0.
 // Grid: tiles enumerated so that the row blocks sharing one column block land
 // on the same XCD (blockIdx % 8 picks the XCD).
+// Split-K form (SPLIT, grid (tiles, slices)): slice blockIdx.y takes k
+// blockIdx.y * K .. +K (K here the slice length, a multiple of 256; the last
+// slice may be shorter) of rows of length ldk, and writes its fp32 sums,
+// scaled but without the bias, to P[slice][M][N] (wq_splitk_reduce adds the
+// slices and the bias).
 // ----------------------------------------------------------------------------
-template <int QB, bool BF16, int SDT, int ZDT>
+template <int QB, bool BF16, int SDT, int ZDT, bool SPLIT = false>
 __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
                                               const uint8_t* __restrict__ W,
                                               uint16_t* __restrict__ Y,
                                               const void* __restrict__ S,
                                               const void* __restrict__ Z, int M, int N, int K,
-                                              int G, const uint16_t* bias) {
+                                              int G, const uint16_t* bias, int ldk = 0,
+                                              float* __restrict__ P = nullptr) {
   constexpr int BM = 64, KS = 256, LDX = KS + 8;
+  // k range of this workgroup, and the row length of X and W
+  const int kbeg = SPLIT ? (int)blockIdx.y * K : 0;
+  const int kend = SPLIT ? min(ldk, kbeg + K) : K;
+  if constexpr (SPLIT) K = ldk;
   __shared__ __align__(16) uint16_t xs[2][BM * LDX];
   __shared__ __align__(16) float xsm[2][2][BM];  // [buf][chunk][row]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1114,14 +1124,15 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
   u4_t xr[8], wv[NL], wn[NL];
   typename Raw<SDT>::T scv[NL], scn[NL];
   typename Raw<ZDT>::T zbv[NL], zbn[NL];
+  // rows past M load row M - 1 and are zeroed when stored: zeroing them here
+  // would consume each load on the spot (the compiler waits for it), instead
+  // of leaving the loads in flight across the current step's MFMAs
   auto load_x = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       int c = tid + 256 * i;
       int r = c >> 5, kc = (c & 31) << 3;
-      const int gr = m0 + r;
-      xr[i] = ldg128(X + (size_t)min(gr, M - 1) * K + k0 + kc);
-      if (gr >= M) xr[i] = u4_t{0u, 0u, 0u, 0u};
+      xr[i] = ldg128(X + (size_t)min(m0 + r, M - 1) * K + k0 + kc);
     }
   };
   auto store_x = [&](int buf) {
@@ -1129,7 +1140,7 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
     for (int i = 0; i < 8; ++i) {
       int c = tid + 256 * i;
       int r = c >> 5, kc = (c & 31) << 3;
-      u4_t v = xr[i];
+      u4_t v = m0 + r < M ? xr[i] : u4_t{0u, 0u, 0u, 0u};
       float s = sum16(sum8<BF16>(v));
       if ((c & 15) == 0) xsm[buf][kc >> 7][r] = s;
       if constexpr (QB == 4) v = perm_x8(v);
@@ -1157,13 +1168,13 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
 #pragma unroll
   for (int t = 0; t < 4; ++t) xtot[t] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nsteps = K / KS;
-  load_w(0, wv, scv, zbv);
-  load_x(0);
+  const int nsteps = (kend - kbeg) / KS;
+  load_w(kbeg, wv, scv, zbv);
+  load_x(kbeg);
   store_x(0);
   __syncthreads();
   for (int st = 0; st < nsteps; ++st) {
-    const int k0 = st * KS, buf = st & 1;
+    const int k0 = kbeg + st * KS, buf = st & 1;
     const bool more = st + 1 < nsteps;
     if (more) {
       load_w(k0 + KS, wn, scn, zbn);
@@ -1236,7 +1247,11 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
       int row = m0 + t * 16 + 4 * q + e;
       float v = y[t][e];
       if constexpr (QB == 8) v = sc * (v - z * xtot[t][e]);
-      if (row < M) store_out(Y, (size_t)row * N + n, v + bias_at(bias, n, BF16), BF16);
+      if constexpr (SPLIT) {
+        if (row < M) P[((size_t)blockIdx.y * M + row) * N + n] = v;
+      } else {
+        if (row < M) store_out(Y, (size_t)row * N + n, v + bias_at(bias, n, BF16), BF16);
+      }
     }
 }
 
@@ -1786,6 +1801,23 @@ TM_WQ_Z(skinny, 8, false, f16, , , false)
 TM_WQ_Z(skinny, 8, true, bf16, , , false)
 TM_WQ_Z(tiled, 4, false, f16, , )
 TM_WQ_Z(tiled, 4, true, bf16, , )
+// tiled split-K forms: (X, W, P, S, Z, M, N, K of a slice, ldk, G), grid
+// (tiles, slices)
+#define TM_TILED_K(QB, BF, ACT, ZS, ZDT)                                                      \
+  extern "C" __global__ __launch_bounds__(256) void wq_tiled_q##QB##_##ACT##_z##ZS##_k(       \
+      const uint16_t* X, const uint8_t* W, float* P, const void* S, const void* Z, int M,     \
+      int N, int K, int ldk, int G) {                                                         \
+    wq_tiled_body<QB, BF, (BF ? TM_DT_BF16 : TM_DT_F16), ZDT, true>(X, W, nullptr, S, Z, M, N, \
+                                                                   K, G, nullptr, ldk, P);    \
+  }
+#define TM_TILED_K_Z(QB, BF, ACT)                            \
+  TM_TILED_K(QB, BF, ACT, n, -1)                             \
+  TM_TILED_K(QB, BF, ACT, s, (BF ? TM_DT_BF16 : TM_DT_F16))  \
+  TM_TILED_K(QB, BF, ACT, u, 3)
+TM_TILED_K_Z(4, false, f16)
+TM_TILED_K_Z(4, true, bf16)
+TM_TILED_K_Z(8, false, f16)
+TM_TILED_K_Z(8, true, bf16)
 TM_WQ_Z(tiled, 8, false, f16, , )
 TM_WQ_Z(tiled, 8, true, bf16, , )
 
