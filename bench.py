@@ -39,6 +39,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "W4A16 GEMM GB/s & %HBM roofline (M=1..128); FA-fwd TFLOP/s & %MFMA peak"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_PEAK_TFLOPS = 2516.6      # MI355X dense fp16/bf16 MFMA, TFLOP/s
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA, TFLOP/s
 ROTATE_BYTES = 600 << 20       # > 256 MB Infinity Cache
 
 
@@ -109,6 +110,35 @@ def dense(dev, M=512, N=512, K=512):
     launches = [tm.plan_matmul(A, B, C, M, N, K)]
     return dict(launches=launches, keep=(A, B, C), bytes=2 * (M * K + K * N + M * N),
                 flops=2 * M * N * K, bound="mfma", dtype="fp16", config={"workload": f"dense_{M}x{N}x{K}", "M": M, "N": N, "K": K})
+
+
+def dot_general(dev, layout, dt_name, M, N, K, batch=None, epilogue="none"):
+    """tm_dot (the strided tl.dot template) on layouts the dense kernels do not
+    take: "colmajor_a" (A stored [K, M]), "batched" (row-major [batch, M, K] @
+    [batch, K, N]) or "trans_b" with an add-matrix epilogue."""
+    import torch
+    import triton_metal_amd as tm
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt_name]
+    g = torch.Generator(device=dev).manual_seed(5)
+    bs = () if batch is None else (batch,)
+    A = torch.randn(*bs, M, K, device=dev, generator=g).to(dt)
+    B = torch.randn(*bs, K, N, device=dev, generator=g).to(dt)
+    if layout == "colmajor_a":
+        A = A.transpose(-1, -2).contiguous().transpose(-1, -2)
+    elif layout == "trans_b":
+        B = B.transpose(-1, -2).contiguous().transpose(-1, -2)
+    C = torch.empty(*bs, M, N, device=dev, dtype=dt)
+    Z = torch.randn(*bs, M, N, device=dev, generator=g).to(dt) if epilogue != "none" else None
+    launches = [tm.plan_dot(A, B, C, epilogue, z=Z)]
+    nb = batch or 1
+    esz = A.element_size()
+    w = dict(launches=launches, keep=(A, B, C, Z), bytes=esz * nb * (M * K + K * N + M * N),
+             flops=2 * nb * M * N * K, bound="mfma", dtype=dt_name,
+             config={"workload": f"dot_{dt_name}_{layout}", "M": M, "N": N, "K": K,
+                     "batch": batch, "epilogue": epilogue})
+    if dt == torch.float32:
+        w["peak_tflops"] = MFMA_F32_PEAK_TFLOPS
+    return w
 
 
 def flash(dev, causal, B=4, H=32, S=4096, D=128, const_data=False):
@@ -346,6 +376,13 @@ EXTRA = {"hbm_copy": hbm_copy,
          "w4a16_m32_k14336": lambda d: w4a16_wide_k(d, 32),
          "w4a16_m64_k14336": lambda d: w4a16_wide_k(d, 64),
          "w4a16_m8_k28672": lambda d: w4a16_wide_k(d, 8, K=28672, N=8192),
+         # tm_dot on layouts the dense kernels do not take (dot_tile*)
+         "dot_fp16_colmajor_a_4096": lambda d: dot_general(d, "colmajor_a", "fp16", 4096, 4096, 4096),
+         "dot_bf16_batched_8x1024": lambda d: dot_general(d, "batched", "bf16", 1024, 1024, 1024,
+                                                          batch=8),
+         "dot_fp16_addmatrix_2048": lambda d: dot_general(d, "trans_b", "fp16", 2048, 2048, 2048,
+                                                          epilogue="add-matrix"),
+         "dot_fp32_colmajor_a_4096": lambda d: dot_general(d, "colmajor_a", "fp32", 4096, 4096, 4096),
          # the 64 x 64 tiled kernel (int4, K = 11008 past the wide kernels)
          "w4a16_m128_k11008": lambda d: w4a16_wide_k(d, 128, K=11008),
          "w4a16_m512_k11008": lambda d: w4a16_wide_k(d, 512, K=11008),
@@ -415,8 +452,9 @@ def summarize(w, ms, mean_ms, eager_ms, replays):
         roof = dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=round(gbs / HBM_PEAK_GBS, 4))
     else:
-        roof = dict(bound="mfma", achieved=round(tfl, 2), peak=MFMA_PEAK_TFLOPS, unit="TFLOP/s",
-                    frac=round(tfl / MFMA_PEAK_TFLOPS, 4))
+        peak = w.get("peak_tflops", MFMA_PEAK_TFLOPS)
+        roof = dict(bound="mfma", achieved=round(tfl, 2), peak=peak, unit="TFLOP/s",
+                    frac=round(tfl / peak, 4))
     return dict(us_per_call=round(ms * 1e3, 3), mean_us_per_call=round(mean_ms * 1e3, 3),
                 replays=replays, eager_us_per_call=round(eager_ms * 1e3, 3),
                 GBps=round(gbs, 1), TFLOPs=round(tfl, 3), roofline=roof, config=w["config"])
