@@ -157,8 +157,11 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
   p.a_mode = fetch_mode(A, p.sa_b, p.sa_m, p.sa_k, batch, esz);
   p.b_mode = fetch_mode(B, p.sb_b, p.sb_n, p.sb_k, batch, esz);
   // [f16, bf16, fp8, f32]: both operands in 16-byte pieces (KC / RC) ->
-  // dot_tile (16-bit and FP8: 128 x 128 tiles once they give every CU a
-  // workgroup, else 64 x 64), else the element-load form dot_tile_s
+  // dot_tile (16-bit and FP8: 128 x 128 tiles from 1.5 of them per CU, else
+  // 64 x 64: two 128-tile workgroups fit a CU, four 64-tile ones, and at one
+  // 128 tile per CU the 64 tiles measured faster: fp16 2048^3 81 -> 57 us,
+  // 4 x 1024^3 46 -> 33 us, while 2560 x 2560 x 4096 (400 tiles of 128) kept
+  // the 128 tiles, 167 against 189 us), else the element-load form dot_tile_s
   static Kernel* k64[4] = {new Kernel("dot_tile_f16"), new Kernel("dot_tile_bf16"),
                            new Kernel("dot_tile_fp8"), new Kernel("dot_tile_f32")};
   static Kernel* k128[3] = {new Kernel("dot_tile128_f16"), new Kernel("dot_tile128_bf16"),
@@ -168,7 +171,7 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
   const int kind = in_dtype == TM_DT_F32 ? 3 : is_fp8(in_dtype) ? 2 : in_dtype == TM_DT_BF16 ? 1 : 0;
   const bool vec = p.a_mode != MODE_SCALAR && p.b_mode != MODE_SCALAR;
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
-  const bool big = vec && kind != 3 && t128 * batch >= 256;
+  const bool big = vec && kind != 3 && 2 * t128 * batch >= 3LL * cu_count();
   const int edge = big ? 128 : 64;
   const long long tiles = (long long)((M + edge - 1) / edge) * ((N + edge - 1) / edge);
   if (tiles > 0x7fffffffLL) return fail(TM_ERR_UNSUPPORTED, "%s: too many tiles", op);
