@@ -268,7 +268,10 @@ int tm_linear(const void* input, const void* weight, const void* bias, void* out
  * points make, as a pure function (no device is touched).  No counterpart in
  * the reference, whose callers pick a template; for tests and callers that
  * want to know the path.  FP8 inputs (the general dot) give
- * TM_ERR_UNSUPPORTED.  tm_linear's leading dimensions are K, K, N. */
+ * TM_ERR_UNSUPPORTED.  16-bit shapes the dense tile kernels do not take (K
+ * or a leading dimension not a multiple of 8, unaligned A / B) run tm_dot's
+ * tile kernels: name "tm_dot", grid and block 0 (tm_dot picks them).
+ * tm_linear's leading dimensions are K, K, N. */
 #define TM_GEMM_ALIGN_AB16 1u /* A and B 16-byte aligned */
 #define TM_GEMM_ALIGN_C16 2u  /* C 16-byte aligned */
 #define TM_GEMM_ALIGN_ALL 3u

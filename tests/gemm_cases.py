@@ -39,7 +39,7 @@ for shape in F32_SHAPES.values():
         CASES.append(("nn", *shape, F32, out, False))
         for bias in (False, True):
             CASES.append(("nt", *shape, F32, out, bias))
-# the general kernel: 16-bit inputs with K % 8 != 0
+# 16-bit inputs with K % 8 != 0: tm_dot's tile kernels
 CASES += [("nn", 37, 53, 29, F16, F16, False), ("nt", 40, 48, 20, BF16, F32, True)]
 
 

@@ -19,14 +19,16 @@ def gemm_kernels(tmp_path_factory):
     names = set()
     for stem in ("gemm", "gemm_big", "gemm_f32"):
         names |= {n for n, _, _ in _kernel_metadata(_built(stem), tmp)}
-    return {n for n in names if n.startswith("gemm_") and not n.startswith("gemm_dd_")}
+    # gemm_general is selected only for K = 0 (tests/test_gpu_gemm.py runs it)
+    return {n for n in names if n.startswith("gemm_") and not n.startswith("gemm_dd_")
+            and n != "gemm_general"}
 
 
 def test_cases_cover_every_dense_kernel(gemm_kernels):
     reached = {plan(c) for c in CASES}
     missing = sorted(gemm_kernels - reached)
     assert not missing, f"dense kernels no GPU case reaches: {missing}"
-    assert reached <= gemm_kernels | {"gemm_general"}, sorted(reached - gemm_kernels)
+    assert reached <= gemm_kernels | {"tm_dot"}, sorted(reached - gemm_kernels)
 
 
 @pytest.mark.parametrize("case", CASES, ids=[case_id(c) for c in CASES])
@@ -37,13 +39,14 @@ def test_case_reaches_its_family(case):
     if dt == torch.float32:
         fam = next(f for f, s in F32_SHAPES.items() if s == (M, N, K))
     name = plan(case)
-    assert name.startswith(f"gemm_{fam}_" if fam != "general" else "gemm_general"), name
+    assert name.startswith(f"gemm_{fam}_") if fam != "general" else name == "tm_dot", name
 
 
 def test_plan_follows_alignment_and_leading_dimensions():
     # unaligned A / B, or a leading dimension that is not a multiple of 8,
-    # leave the MFMA kernels; an unaligned C leaves the 32-tile K-split kernel
-    assert tm.gemm_kernel_for(512, 512, 512, align=_lib.TM_GEMM_ALIGN_C16)[0] == "gemm_general"
+    # leave the dense tile kernels for tm_dot's (grid and block tm_dot's own);
+    # an unaligned C leaves the 32-tile K-split kernel
+    assert tm.gemm_kernel_for(512, 512, 512, align=_lib.TM_GEMM_ALIGN_C16) == ("tm_dot", 0, 0)
     # fp32 inputs take the fp32-MFMA kernels whatever the alignment: 16-byte
     # pieces for aligned operands with leading dimensions multiples of 4
     f32 = torch.float32
@@ -54,7 +57,7 @@ def test_plan_follows_alignment_and_leading_dimensions():
     assert tm.gemm_kernel_for(5, 7, 4, in_dtype=f32, trans_b=True)[0] == "gemm_f32t64_nt_f32"
     assert tm.gemm_kernel_for(5, 7, 4, in_dtype=f32, ldb=6, trans_b=True)[0] == \
         "gemm_f32t64u_nt_f32"
-    assert tm.gemm_kernel_for(512, 512, 512, lda=516)[0] == "gemm_general"
+    assert tm.gemm_kernel_for(512, 512, 512, lda=516)[0] == "tm_dot"
     assert tm.gemm_kernel_for(512, 512, 512)[0] == "gemm_s32k128_nn_f16_same"
     assert tm.gemm_kernel_for(512, 512, 512, align=_lib.TM_GEMM_ALIGN_AB16)[0].startswith(
         "gemm_t32k_")

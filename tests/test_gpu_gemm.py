@@ -298,6 +298,78 @@ def test_matmul_large_tiles_padded_leading_dims(dev):
     assert (got[:, N:] == 0).all()  # the padding columns of C are untouched
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("form", ["nn", "nt", "nt_bias"])
+def test_off_tile_shapes_run_the_dot_tiles(dev, dt, form):
+    """16-bit shapes the dense tile kernels do not take run tm_dot's tile
+    kernels (tm_gemm_plan: "tm_dot"): K not a multiple of 8 (large and odd),
+    A one element off 16-byte alignment, a leading dimension not a multiple
+    of 8 (tm_matmul), with fp32 output and the linear bias."""
+    import ctypes
+    from triton_metal_amd import _lib
+    L = _lib.lib()
+    bt, bias = form != "nn", form == "nt_bias"
+    code = _lib.TM_DT_BF16 if dt == torch.bfloat16 else _lib.TM_DT_F16
+    # (M, N, K, lda, element offset of A, out dtype); tm_linear rows are contiguous
+    cases = ((300, 260, 1001, 1001, 0, dt), (130, 96, 64, 64 if bt else 68, 1, dt),
+             (64, 200, 36, 36 if bt else 44, 0, torch.float32))
+    for M, N, K, lda, off, out in cases:
+        ldb = K if bt else N
+        Ap = _rand((M * lda + off,), M + K, dt)
+        B = _rand((N, K) if bt else (K, N), N + K, dt)
+        b = _rand((N,), N, dt) if bias else None
+        C = torch.full((M, N), 7.0, dtype=out, device=dev)
+        Ad, Bd = Ap.to(dev), B.to(dev)
+        bd = None if b is None else b.to(dev)
+        a_ptr = ctypes.c_void_p(Ad.data_ptr() + off * Ad.element_size())
+        ocode = _lib.TM_DT_F32 if out == torch.float32 else code
+        align = _lib.TM_GEMM_ALIGN_C16 | (0 if off else _lib.TM_GEMM_ALIGN_AB16)
+        name = tm.gemm_kernel_for(M, N, K, lda=lda, ldb=ldb, trans_b=bt, bias=bias, in_dtype=dt,
+                                  out_dtype=out, align=align)[0]
+        assert name == "tm_dot", (M, N, K, name)
+        if bt:
+            rc = L.tm_linear(a_ptr, ctypes.c_void_p(Bd.data_ptr()),
+                             None if bd is None else ctypes.c_void_p(bd.data_ptr()),
+                             ctypes.c_void_p(C.data_ptr()), M, N, K, code, ocode, None)
+        else:
+            rc = L.tm_matmul(a_ptr, ctypes.c_void_p(Bd.data_ptr()), ctypes.c_void_p(C.data_ptr()),
+                             M, N, K, lda, ldb, N, code, ocode, None)
+        assert rc == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        A = Ap[off:off + M * lda].reshape(M, lda)[:, :K].float().numpy()
+        if bt:
+            ref = oracle.linear(A, B.float().numpy(), None if b is None else b.float().numpy())
+        else:
+            ref = oracle.matmul(A, B.float().numpy())
+        atol, rtol = (1e-3, 1e-4) if out == torch.float32 else (max(ATOL, 1e-3 * K ** 0.5), RTOL)
+        np.testing.assert_allclose(C.float().cpu().numpy(), ref, atol=atol, rtol=rtol)
+
+
+def test_k_zero_runs_the_general_kernel(dev):
+    """K = 0: a product of zeros (plus the linear bias) on gemm_general."""
+    import ctypes
+    from triton_metal_amd import _lib
+    L = _lib.lib()
+    M, N = 5, 24
+    A = torch.zeros(8, dtype=torch.float16, device=dev)
+    B = torch.zeros(8, dtype=torch.float16, device=dev)
+    b = _rand((N,), 3, torch.float16).to(dev)
+    C = torch.full((M, N), 7.0, dtype=torch.float16, device=dev)
+    rc = L.tm_matmul(ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(B.data_ptr()),
+                     ctypes.c_void_p(C.data_ptr()), M, N, 0, 0, N, N, _lib.TM_DT_F16,
+                     _lib.TM_DT_F16, None)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert (C == 0).all()
+    C.fill_(7.0)
+    rc = L.tm_linear(ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(B.data_ptr()),
+                     ctypes.c_void_p(b.data_ptr()), ctypes.c_void_p(C.data_ptr()), M, N, 0,
+                     _lib.TM_DT_F16, _lib.TM_DT_F16, None)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(C, b.expand(M, N))
+
+
 def test_fp32_general_path(dev):
     M, N, K = 13, 17, 19
     A, B = _rand((M, K), 8, torch.float32), _rand((K, N), 9, torch.float32)

@@ -341,11 +341,13 @@ int wq_matmul(int qbits, const void* X, const void* W, void* Y, const void* S, c
 // the transposed nn.Linear weight and a bias is given, pointer alignment): the
 // launch path and tm_gemm_plan share it.  FP8 inputs are not planned here (they
 // run the general dot); fp32 inputs take gemm_f32t64, 16-bit inputs the MFMA
-// tile kernels where sizes and alignment allow, else gemm_general.
+// tile kernels where sizes and alignment allow, else the strided dot's tile
+// kernels ("tm_dot": grid and block are the dot's own choice, reported as 0),
+// and K = 0 gemm_general.
 struct GemmPlan {
   char name[96];
   unsigned grid, block;
-  bool general;  // gemm_general's argument list
+  bool general;  // not a dense tile kernel: tm_dot, or gemm_general (K = 0)
 };
 
 void gemm_plan(int M, int N, int K, int lda, int ldb, int ldc, bool bt, bool bias, int idt,
@@ -407,10 +409,15 @@ void gemm_plan(int M, int N, int K, int lda, int ldb, int ldc, bool bt, bool bia
     pl->block = 256;
     return;
   }
+  pl->general = true;
+  if (K > 0) {
+    snprintf(pl->name, sizeof pl->name, "tm_dot");
+    pl->grid = pl->block = 0;
+    return;
+  }
   snprintf(pl->name, sizeof pl->name, "gemm_general");
   pl->grid = (unsigned)(((size_t)M * N + 255) / 256);
   pl->block = 256;
-  pl->general = true;
 }
 
 int dense(const void* A, const void* B, void* C, const void* bias, int M, int N, int K, int lda,
@@ -436,9 +443,21 @@ int dense(const void* A, const void* B, void* C, const void* bias, int M, int N,
   GemmPlan pl;
   gemm_plan(M, N, K, lda, ldb, ldc, bt, bias != nullptr, idt, odt, aligned16(A) && aligned16(B),
             aligned16(C), &pl);
-  if (pl.general)
+  if (pl.general) {
+    // 16-bit operands the tile kernels cannot take (K or a leading dimension
+    // not a multiple of 8, unaligned A / B): the strided dot's MFMA tile
+    // kernels, the bias as its add-cols epilogue; K = 0 (a product of zeros)
+    // on the one-thread-per-output kernel
+    if (K > 0) {
+      const long long st[14] = {0, lda, 1, 0, bt ? 1 : ldb, bt ? ldb : 1, 0, ldc, 1, 0, 0, 1,
+                                0, 0};
+      return dot_impl(op, A, B, C, bias, nullptr, 1, M, N, K, 0, st,
+                      bias ? TM_EPI_ADD_COLS : TM_EPI_NONE, idt, odt, bias ? idt : TM_DT_NONE,
+                      TM_DT_NONE, stream);
+    }
     return launch(kernel(pl.name), dim3(pl.grid), dim3(pl.block), 0, stream, A, B, C, bias, M, N,
                   K, lda, ldb, ldc, bt ? 1 : 0, idt, odt);
+  }
   return launch(kernel(pl.name), dim3(pl.grid), dim3(pl.block), 0, stream, A, B, C, bias, M, N,
                 K, lda, ldb, ldc);
 }

@@ -319,10 +319,14 @@ __device__ __forceinline__ void dot_tile_vec_body(const DotParams& p) {
 // 16 x 16 (v_mfma_f32_16x16x32: lane l supplies row l % 16, k 8 (l / 16) ..
 // +7 of each operand and holds D[4 (l / 16) + e][l % 16]); K in steps of 32
 // through two LDS buffers ([row][32 k + 8 pad]).  Each thread fetches 8
-// elements per operand and step, one bounds-checked load each:
+// elements per operand and step, one load each:
 //   KC / SCALAR  row tid / 4, k 8 (tid % 4) .. +7
 //   RC           rows 8 (tid % 8) .. +7, k tid / 8
-// packed in registers (8 halves, or 8 FP8 codes in the low 8 bytes).
+// at addresses clamped into the operand (row at most rows - 1, k at most
+// K - 1), unconditional and into registers of their own, so that the next
+// step's loads stay in flight across the MFMAs; the LDS store zeroes the
+// elements past the operand and packs them (8 halves, or FP8 codes decoded
+// to halves).
 // ----------------------------------------------------------------------------
 template <bool BF16, bool FP8>
 __device__ __forceinline__ void dot_tile_s_body(const DotParams& p) {
@@ -344,56 +348,51 @@ __device__ __forceinline__ void dot_tile_s_body(const DotParams& p) {
   const uint8_t* Ab = (const uint8_t*)p.A + (long long)b * p.sa_b * esz;
   const uint8_t* Bb = (const uint8_t*)p.B + (long long)b * p.sb_b * esz;
 
-  auto elem = [&](const u4_t& w, int e) -> uint32_t {
-    if constexpr (FP8) return (w[e >> 2] >> (8 * (e & 3))) & 0xFFu;
-    else return (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
-  };
-  auto pack = [&](u4_t& w, int e, uint32_t v) {
-    if constexpr (FP8) w[e >> 2] |= v << (8 * (e & 3));
-    else w[e >> 1] |= v << (16 * (e & 1));
-  };
   auto raw = [&](const uint8_t* X, long long i) -> uint32_t {
     if constexpr (FP8) return (uint32_t)X[i];
     else return (uint32_t)((const uint16_t*)X)[i];
   };
+  struct Raw8 { uint32_t v[8]; };
   // the thread's 8 elements of operand X [rows][K] (rows from r0) at k0
   auto fetch = [&](const uint8_t* X, int mode, int rows, int r0, long long s_r, long long s_k,
-                   int k0) -> u4_t {
-    u4_t w = u4_t{0u, 0u, 0u, 0u};
+                   int k0) -> Raw8 {
+    Raw8 f;
     if (mode == MODE_RC) {
-      const int rc = r0 + 8 * (tid & 7), kk = k0 + (tid >> 3);
-      if (kk >= p.K) return w;
-      const long long base = (long long)rc * s_r + (long long)kk * s_k;
+      const int rc = r0 + 8 * (tid & 7), kk = min(k0 + (tid >> 3), p.K - 1);
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (rc + e < rows) pack(w, e, raw(X, base + (long long)e * s_r));
-      return w;
+        f.v[e] = raw(X, (long long)min(rc + e, rows - 1) * s_r + (long long)kk * s_k);
+      return f;
     }
-    const int r = r0 + (tid >> 2), kc = k0 + 8 * (tid & 3);
-    if (r >= rows) return w;
-    const long long base = (long long)r * s_r + (long long)kc * s_k;
+    const int r = min(r0 + (tid >> 2), rows - 1), kc = k0 + 8 * (tid & 3);
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      if (kc + e < p.K) pack(w, e, raw(X, base + (long long)e * s_k));
-    return w;
+      f.v[e] = raw(X, (long long)r * s_r + (long long)min(kc + e, p.K - 1) * s_k);
+    return f;
   };
   auto cvt = [&](uint32_t x) -> uint32_t {
     if constexpr (FP8) return (uint32_t)lut[x];
     else return x;
   };
-  auto put = [&](uint16_t* Xs, int mode, u4_t w) {
+  // the elements fetched for rows from r0 at k0 into LDS buffer Xs, those
+  // past the operand zeroed
+  auto put = [&](uint16_t* Xs, int mode, const Raw8& f, int rows, int r0, int k0) {
     if (mode == MODE_RC) {
       const int rc = 8 * (tid & 7), kk = tid >> 3;
+      const bool kok = k0 + kk < p.K;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Xs[(rc + e) * LDK + kk] = (uint16_t)cvt(elem(w, e));
+      for (int e = 0; e < 8; ++e)
+        Xs[(rc + e) * LDK + kk] = kok && r0 + rc + e < rows ? (uint16_t)cvt(f.v[e]) : (uint16_t)0;
       return;
     }
     const int r = tid >> 2, kc = 8 * (tid & 3);
-    u4_t o = w;
-    if constexpr (FP8) {
+    const bool rok = r0 + r < rows;
+    uint32_t h[8];
 #pragma unroll
-      for (int d = 0; d < 4; ++d) o[d] = cvt(elem(w, 2 * d)) | (cvt(elem(w, 2 * d + 1)) << 16);
-    }
+    for (int e = 0; e < 8; ++e) h[e] = rok && k0 + kc + e < p.K ? cvt(f.v[e]) : 0u;
+    u4_t o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] = h[2 * d] | (h[2 * d + 1] << 16);
     *(u4_t*)&Xs[r * LDK + kc] = o;
   };
 
@@ -404,10 +403,10 @@ __device__ __forceinline__ void dot_tile_s_body(const DotParams& p) {
     for (int j = 0; j < 2; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nk = (p.K + BK - 1) / BK;
-  u4_t fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, 0);
-  u4_t fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, 0);
-  put(As[0], p.a_mode, fa);
-  put(Bs[0], p.b_mode, fb);
+  Raw8 fa = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, 0);
+  Raw8 fb = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, 0);
+  put(As[0], p.a_mode, fa, p.M, m0, 0);
+  put(Bs[0], p.b_mode, fb, p.N, n0, 0);
   __syncthreads();
   const int q = lane >> 4, r16 = lane & 15;
   for (int kt = 0; kt < nk; ++kt) {
@@ -428,8 +427,8 @@ __device__ __forceinline__ void dot_tile_s_body(const DotParams& p) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = mfma16<BF16>(af[i], bfr[j], acc[i][j]);
     if (kt + 1 < nk) {
-      put(As[buf ^ 1], p.a_mode, fa);
-      put(Bs[buf ^ 1], p.b_mode, fb);
+      put(As[buf ^ 1], p.a_mode, fa, p.M, m0, (kt + 1) * BK);
+      put(Bs[buf ^ 1], p.b_mode, fb, p.N, n0, (kt + 1) * BK);
     }
     __syncthreads();
   }
