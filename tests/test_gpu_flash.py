@@ -92,6 +92,54 @@ def test_flash_mfma_shapes(dev, S, D, causal, dtype):
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
 
 
+@pytest.mark.parametrize("S", [1, 100, 257, 777])
+@pytest.mark.parametrize("D", [48, 80, 96, 112])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_flash_mfma_inlaid_head_dims(dev, S, D, causal, dtype):
+    """Head dims 48 / 80 / 96 / 112 on the MFMA kernel in the 64 / 128 layout
+    (flash_fwd_d<64|128>v<D>): the chunks past D are neither copied nor read,
+    and the output columns past D are not written (checked against a sentinel
+    in a wider buffer)."""
+    B, H = 2, 3
+    q, k, v = (_rand((B, H, S, D), s, dtype, dev) for s in (11, 12, 13))
+    wide = torch.full((B, H, S, D + 16), 5.0, dtype=dtype, device=dev)
+    o = wide[..., :D]
+    lse = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    tm.plan_flash_attention(q, k, v, o, lse, causal=causal)()
+    torch.cuda.synchronize()
+    ref, ref_lse = _ref(q, k, v, causal)
+    np.testing.assert_allclose(o.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=1e-3, rtol=1e-4)
+    assert (wide[..., D:] == 5.0).all()
+
+
+@pytest.mark.parametrize("S", [1, 100, 257])
+@pytest.mark.parametrize("D", [32, 64, 96, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_fp32_mfma_head_dims(dev, S, D, causal):
+    """fp32 (the reference template's dtype) on the fp32-MFMA kernel,
+    flash_fwd_f32_d<D>: within 1e-4 of the oracle, LSE within 1e-4."""
+    B, H = 2, 3
+    q, k, v = (_rand((B, H, S, D), s, torch.float32, dev) for s in (21, 22, 23))
+    o, lse = tm.attention(q, k, v, causal=causal, return_lse=True)
+    ref, ref_lse = _ref(q, k, v, causal)
+    np.testing.assert_allclose(o.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=1e-4, rtol=1e-5)
+
+
+def test_flash_inlaid_head_dim_strided_views(dev):
+    """D = 96 through views of a packed [B, S, 3, H, D] tensor (row strides
+    3 H D), causal."""
+    B, S, H, D = 2, 200, 4, 96
+    qkv = _rand((B, S, 3, H, D), 17, torch.bfloat16, dev)
+    q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+    o = torch.empty(B, S, H, D, dtype=torch.bfloat16, device=dev).transpose(1, 2)
+    tm.plan_flash_attention(q, k, v, o, causal=True)()
+    ref, _ = _ref(q, k, v, True)
+    np.testing.assert_allclose(o.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+
+
 def test_flash_strided_views(dev):
     """q, k, v as views into a packed [B, S, 3, H, D] tensor."""
     B, S, H, D = 2, 96, 4, 64

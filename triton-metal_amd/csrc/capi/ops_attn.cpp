@@ -78,12 +78,19 @@ extern "C" int tm_flash_attention(const void* q, const void* k, const void* v, v
   const bool small_rows = 64LL * std::max(std::llabs(st[5]), std::llabs(st[8])) < (1LL << 31);
   bool st8 = small_rows;
   for (int i = 0; i < 12; ++i) st8 &= (st[i] % 8) == 0;
-  const bool mfma = is_half(dtype) && (head_dim == 32 || head_dim == 64 || head_dim == 128) &&
-                    st8 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  // head dims 32 / 64 / 128, and 48 / 80 / 96 / 112 in the layout of 64 / 128
+  const bool exact = head_dim == 32 || head_dim == 64 || head_dim == 128;
+  const bool inlaid = head_dim == 48 || head_dim == 80 || head_dim == 96 || head_dim == 112;
+  const bool mfma = is_half(dtype) && (exact || inlaid) && st8 && aligned16(q) && aligned16(k) &&
+                    aligned16(v) && aligned16(o);
   if (mfma) {
     char name[64];
-    snprintf(name, sizeof name, "flash_fwd_d%d_%s_%s", head_dim,
-             dtype == TM_DT_BF16 ? "bf16" : "f16", causal ? "causal" : "full");
+    if (exact)
+      snprintf(name, sizeof name, "flash_fwd_d%d_%s_%s", head_dim,
+               dtype == TM_DT_BF16 ? "bf16" : "f16", causal ? "causal" : "full");
+    else
+      snprintf(name, sizeof name, "flash_fwd_d%dv%d_%s_%s", head_dim <= 64 ? 64 : 128, head_dim,
+               dtype == TM_DT_BF16 ? "bf16" : "f16", causal ? "causal" : "full");
     // causal: one workgroup per pair of query blocks (i, nqb - 1 - i)
     const long long nqb = (seq_len + 127) / 128;
     const long long grid = (causal ? (nqb + 1) / 2 : nqb) * (long long)batch * heads;
@@ -91,10 +98,10 @@ extern "C" int tm_flash_attention(const void* q, const void* k, const void* v, v
     return launch(flash_kernel(name), dim3((unsigned)grid), dim3(256), 0, stream, p);
   }
   // fp32 (the reference template's dtype): the fp32-MFMA kernel for head dims
-  // 32 / 64 / 128 with 16-byte aligned rows
+  // 32 / 64 / 96 / 128 with 16-byte aligned rows
   bool st4 = true;
   for (int i = 0; i < 12; ++i) st4 &= (st[i] % 4) == 0;
-  if (dtype == TM_DT_F32 && (head_dim == 32 || head_dim == 64 || head_dim == 128) && st4 &&
+  if (dtype == TM_DT_F32 && head_dim % 32 == 0 && head_dim <= 128 && st4 &&
       aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o)) {
     char name[64];
     snprintf(name, sizeof name, "flash_fwd_f32_d%d_%s", head_dim, causal ? "causal" : "full");

@@ -88,15 +88,24 @@ TM_DEV u2_t lds_tr16(const uint16_t* p) {
   return __builtin_bit_cast(u2_t, v);
 }
 
-template <int D, bool BF16, bool CAUSAL>
+// DV < D: a head dim of DV (a multiple of 8 above D / 2) in the layout of D.
+// The copies skip the 16-byte chunks at or past DV (their lanes are masked
+// off, so those LDS slots are never written; the K slots are zeroed once),
+// Q's chunks past DV are zero, the contraction steps and O tiles wholly past
+// DV are skipped and O's columns past DV are not stored: the MFMA work of a
+// DV-wide kernel with D's swizzles and tiling.
+template <int D, bool BF16, bool CAUSAL, int DV = D>
 __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
   constexpr int BM = 128, BN = 64, NW = 4;
   constexpr int DC = D / 16;    // 16-wide contraction steps of Q K^T
   constexpr int DT = D / 32;    // 32-wide d tiles of O^T
+  constexpr int CV = DV / 8;    // 16-byte chunks of a row below DV
+  constexpr int DCV = (DV + 15) / 16, DTV = (DV + 31) / 32;  // steps / tiles used
   constexpr int NB = BN * D * 2 / 1024;  // 1 KB blocks per tile
   constexpr int BPW = NB / NW;           // blocks per wave
   constexpr int RPB = 512 / D;           // key rows per 1 KB block
   static_assert(D % 32 == 0 && D <= 128 && NB % NW == 0, "head dim");
+  static_assert(DV % 8 == 0 && DV <= D && 2 * DV > D, "valid head dim");
   // separate objects per buffer (chosen at compile time below) so that the
   // compiler can tell the reads of one buffer from the DMA into the other
   __shared__ __align__(16) uint16_t Ks0[BN * D], Ks1[BN * D];
@@ -166,11 +175,14 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
   // block base moves (32-bit offsets; the host checks 64 * stride < 2^31)
   const int prow = lane / (D / 8), pch = lane % (D / 8);
   uint32_t koff[BPW], voff[BPW];  // byte offsets
+  bool kin[BPW], vin[BPW];        // the lane's chunk lies below DV
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     const int r = (wave * BPW + i) * RPB + prow;
     koff[i] = 2u * (uint32_t)(r * (int)p.sks + 8 * (pch ^ k_swz<D>(r)));
     voff[i] = 2u * (uint32_t)(r * (int)p.svs + 8 * (pch ^ v_swz<D>(r)));
+    kin[i] = DV == D || (pch ^ k_swz<D>(r)) < CV;
+    vin[i] = DV == D || (pch ^ v_swz<D>(r)) < CV;
   }
   auto issue_kv = [&](uint16_t* kd, uint16_t* vd, int kv0) {
     const uint16_t* kt = kg + (long long)kv0 * p.sks;
@@ -179,8 +191,8 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int blk = wave * BPW + i;
-        dma16s(kt, koff[i], lds_off(kd) + blk * 1024);
-        dma16s(vt, voff[i], lds_off(vd) + blk * 1024);
+        if (kin[i]) dma16s(kt, koff[i], lds_off(kd) + blk * 1024);
+        if (vin[i]) dma16s(vt, voff[i], lds_off(vd) + blk * 1024);
       }
     } else {
       // rows past the end re-read row S - 1 (their scores are masked)
@@ -189,11 +201,23 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
         const int blk = wave * BPW + i;
         const int r = blk * RPB + prow;
         const int back = r - min(r, S - 1 - kv0);
-        dma16s(kt, koff[i] - 2u * (uint32_t)(back * (int)p.sks), lds_off(kd) + blk * 1024);
-        dma16s(vt, voff[i] - 2u * (uint32_t)(back * (int)p.svs), lds_off(vd) + blk * 1024);
+        if (kin[i])
+          dma16s(kt, koff[i] - 2u * (uint32_t)(back * (int)p.sks), lds_off(kd) + blk * 1024);
+        if (vin[i])
+          dma16s(vt, voff[i] - 2u * (uint32_t)(back * (int)p.svs), lds_off(vd) + blk * 1024);
       }
     }
   };
+  if constexpr (DV < D) {
+    // the K slots of the chunks past DV: zero once (no copy writes them)
+    constexpr int NPAD = D / 8 - CV;
+    for (int sidx = tid; sidx < BN * NPAD; sidx += NW * 64) {
+      const int r = sidx / NPAD, c = CV + sidx % NPAD;
+      const int off = r * D + 8 * (c ^ k_swz<D>(r));
+      *(u4_t*)(Ks0 + off) = u4_t{0u, 0u, 0u, 0u};
+      *(u4_t*)(Ks1 + off) = u4_t{0u, 0u, 0u, 0u};
+    }
+  }
 
   // ---- LDS read addresses, fixed per lane --------------------------------------
   // K operand rows r = 32 kt + l32 keep their swizzle k_swz(r) = k_swz(l32)
@@ -226,12 +250,13 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
     const int qlast_blk = min(qb * BM + BM - 1, S - 1);
     const int nkb = CAUSAL ? qlast_blk / BN + 1 : (S + BN - 1) / BN;
 
-    // Q^T operands: qreg[c] = Q[qi][16c + 8*h32 .. +8]
+    // Q^T operands: qreg[c] = Q[qi][16c + 8*h32 .. +8] (zero past DV)
     u4_t qreg[DC];
 #pragma unroll
-    for (int c = 0; c < DC; ++c) {
+    for (int c = 0; c < DCV; ++c) {
       qreg[c] = u4_t{0u, 0u, 0u, 0u};
-      if (qi < S) qreg[c] = ldg128(qg + (long long)qi * p.sqs + 16 * c + 8 * h32);
+      if (qi < S && (DV == D || 2 * c + h32 < CV))
+        qreg[c] = ldg128(qg + (long long)qi * p.sqs + 16 * c + 8 * h32);
     }
 
     f16_t oacc[DT];
@@ -275,15 +300,15 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
 #pragma unroll
         for (int c = 0; c < KPD; ++c) kread(c);
 #pragma unroll
-        for (int c = 0; c < DC; ++c) {
-          if (c + KPD < DC) kread(c + KPD);
+        for (int c = 0; c < DCV; ++c) {
+          if (c + KPD < DCV) kread(c + KPD);
 #pragma unroll
           for (int kt = 0; kt < 2; ++kt) s[kt] = mfma32<BF16>(ka[c][kt], qreg[c], s[kt]);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * KPD, 0);
 #pragma unroll
-        for (int c = 0; c < DC; ++c) {
-          if (c + KPD < DC) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        for (int c = 0; c < DCV; ++c) {
+          if (c + KPD < DCV) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
         }
         __builtin_amdgcn_s_setprio(0);
@@ -335,16 +360,16 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
         l_run = l_run * alpha + lsum;
         if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // some row's max moved
 #pragma unroll
-          for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+          for (int t = 0; t < DTV; ++t) oacc[t] *= alpha;
         }
         // O^T[d][q] += V^T[d][kv] P^T[kv][q]; MFMA u covers keys
         //   32 (u/2) + 16 (u%2) + 8 (e/4) + 4 h32 + e % 4
         __builtin_amdgcn_s_setprio(1);
-        // operand i = DT u + t; the V^T operands of i + VPD are read while i multiplies
-        constexpr int NVO = 4 * DT, VPD = 2;
+        // operand i = DTV u + t; the V^T operands of i + VPD are read while i multiplies
+        constexpr int NVO = 4 * DTV, VPD = 2;
         u4_t va[NVO];
         auto vread = [&](int i) {
-          const int u = i / DT, t = i % DT;
+          const int u = i / DTV, t = i % DTV;
           const u2_t lo = lds_tr16((const uint16_t*)(vs + vro[t] + 16 * u * D * 2));
           const u2_t hi = lds_tr16((const uint16_t*)(vs + vro[t] + (16 * u + 8) * D * 2));
           va[i].x = lo.x; va[i].y = lo.y; va[i].z = hi.x; va[i].w = hi.y;
@@ -354,7 +379,7 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
 #pragma unroll
         for (int i = 0; i < NVO; ++i) {
           if (i + VPD < NVO) vread(i + VPD);
-          oacc[i % DT] = mfma32<BF16>(va[i], pop[i / DT], oacc[i % DT]);
+          oacc[i % DTV] = mfma32<BF16>(va[i], pop[i / DTV], oacc[i % DTV]);
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * VPD, 0);
 #pragma unroll
@@ -380,10 +405,11 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
     if (qi < S) {
       uint16_t* orow = og + (long long)qi * p.sos;
 #pragma unroll
-      for (int t = 0; t < DT; ++t)
+      for (int t = 0; t < DTV; ++t)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d = t * 32 + 8 * g + 4 * h32;
+          if (DV < D && d >= DV) continue;
           u2_t w;
           if (BF16) {
             w.x = pack_bf16x2(oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv);
@@ -414,6 +440,22 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
 TM_FLASH_D(128)
 TM_FLASH_D(64)
 TM_FLASH_D(32)
+// head dims 48 (in the 64 layout) and 80, 96, 112 (in the 128 layout):
+// flash_fwd_d<D>v<DV>_<dt>_<mask>
+#define TM_FLASH_INST_V(D, DV, BF, DT, CAUSAL, MASK)                                        \
+  extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void \
+      flash_fwd_d##D##v##DV##_##DT##_##MASK(FlashParams p) {                                \
+    flash_fwd_body<D, BF, CAUSAL, DV>(p);                                                   \
+  }
+#define TM_FLASH_DV(D, DV)                                 \
+  TM_FLASH_INST_V(D, DV, true, bf16, false, full)          \
+  TM_FLASH_INST_V(D, DV, true, bf16, true, causal)         \
+  TM_FLASH_INST_V(D, DV, false, f16, false, full)          \
+  TM_FLASH_INST_V(D, DV, false, f16, true, causal)
+TM_FLASH_DV(64, 48)
+TM_FLASH_DV(128, 80)
+TM_FLASH_DV(128, 96)
+TM_FLASH_DV(128, 112)
 
 // ----------------------------------------------------------------------------
 // General kernel: one thread per query row, keys streamed through LDS in
