@@ -57,9 +57,40 @@ def _check(dev, q, k, v, lens, scale, dtype, page_table=None, kp=None, vp=None, 
 # (B, Hq, Hkv, D, S): MFMA kernels (D 64/128, 16-bit caches) with one slice and
 # with many slices (long S, few heads: up to 32 slices merge in one round of
 # loads, (1, 2, 1, 128, 9000) makes 36 and takes the looped merge), GQA groups
-# below / above 16, and the general kernel (other head dims)
+# below / above 16, D 96 in the 128 layout, and the general kernel (D 40)
 SHAPES = [(1, 8, 8, 128, 1000), (2, 32, 8, 128, 4096), (3, 12, 4, 64, 300),
-          (1, 40, 2, 128, 700), (2, 4, 4, 96, 100), (1, 2, 1, 64, 17), (1, 2, 1, 128, 9000)]
+          (1, 40, 2, 128, 700), (2, 4, 4, 96, 100), (1, 2, 1, 64, 17), (1, 2, 1, 128, 9000),
+          (2, 4, 4, 40, 100)]
+
+
+# head dims 48 / 80 / 96 / 112 on the MFMA kernel in the 64 / 128 layout
+# (decode_attn_d<64|128>v<D>): one slice and many, a GQA group above 16
+@pytest.mark.parametrize("D", [48, 80, 96, 112])
+@pytest.mark.parametrize("shape", [(2, 8, 2, 300), (1, 4, 1, 5000), (1, 24, 1, 700)],
+                         ids=["B2-S300", "B1-S5000", "G24-S700"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_inlaid_head_dims(dev, D, shape, dtype):
+    B, Hq, Hkv, S = shape
+    q, k, v = _problem(B, Hq, Hkv, D, S, dtype, seed=D + S)
+    lens = [S] + [S // 2 + 1] * (B - 1)
+    _check(dev, q, k, v, lens, D ** -0.5, dtype)
+
+
+@pytest.mark.parametrize("D", [80, 96])
+def test_decode_inlaid_head_dims_paged_and_fp32_query(dev, D):
+    """Paged caches (16-position pages) and an fp32 query over an fp16 cache
+    (the hi + lo split form), D in the 128 layout."""
+    B, Hq, Hkv, S = 2, 8, 2, 700
+    q, k, v = _problem(B, Hq, Hkv, D, S, torch.float16, seed=D)
+    kp, vp, table = _paged(k, v, 16, seed=D + 1)
+    _check(dev, q, k, v, [S, 333], D ** -0.5, torch.float16, page_table=table, kp=kp, vp=vp)
+    q32 = torch.randn(B, Hq, D, generator=_gen(D + 2))
+    o = torch.empty(B, Hq, D, dtype=torch.float32, device=dev)
+    tm.decode_attention(q32.to(dev), k.to(dev), v.to(dev), scale=D ** -0.5, o=o)
+    ref, _ = oracle.decode_attention(q32.numpy(), k.float().numpy(), v.float().numpy(), [S] * B,
+                                     D ** -0.5)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(o.cpu().numpy(), ref, atol=1e-4, rtol=1e-4)
 
 
 @pytest.mark.parametrize("shape", SHAPES, ids=[str(s) for s in SHAPES])

@@ -1,5 +1,6 @@
 // Typed entry point for decode-time attention (one query token per head over
-// a contiguous or paged KV cache): decode_attn_d<D>_<dt> (16-bit caches) or
+// a contiguous or paged KV cache): decode_attn_d<D>_<dt> or, for head dims
+// 48 / 80 / 96 / 112, decode_attn_d<64|128>v<D>_<dt> (16-bit caches) or
 // decode_attn_f32_d<D> (fp32), + decode_attn_combine when the sequence is
 // split into slices, or decode_attn_general.
 #include <cmath>
@@ -129,8 +130,11 @@ static int decode_attention(const char* op, bool noalloc, const void* q, const v
                    (head_dim == 64 || head_dim == 128) && p.sB % 4 == 0 && p.sH % 4 == 0 &&
                    p.sS % 4 == 0 && aligned16(k_cache) && aligned16(v_cache) && aligned16(q) &&
                    seq_len > 0;
-  bool mfma = f32 || (is16(kv_dtype) && (head_dim == 64 || head_dim == 128) && rows16 &&
-                      aligned16(k_cache) && aligned16(v_cache) && seq_len > 0 &&
+  // 16-bit caches: head dims 64 / 128, and 48 / 80 / 96 / 112 in the layout
+  // of 64 / 128 (the kernel skips the pieces past the head dim)
+  const bool inlaid = head_dim == 48 || head_dim == 80 || head_dim == 96 || head_dim == 112;
+  bool mfma = f32 || (is16(kv_dtype) && (head_dim == 64 || head_dim == 128 || inlaid) &&
+                      rows16 && aligned16(k_cache) && aligned16(v_cache) && seq_len > 0 &&
                       (q_dtype == kv_dtype ? aligned16(q) : true));
   if (mfma) {
     int ns = 1, sl = 0;
@@ -168,12 +172,27 @@ static int decode_attention(const char* op, bool noalloc, const void* q, const v
           {{new Kernel("decode_attn_d128_f16"), new Kernel("decode_attn_d128_f16_x")},
            {new Kernel("decode_attn_d128_bf16"), new Kernel("decode_attn_d128_bf16_x")}}};
       static Kernel kf128("decode_attn_f32_d128"), kf64("decode_attn_f32_d64");
-      Kernel& kk = f32 ? (head_dim == 128 ? kf128 : kf64)
-                       : *kd[head_dim == 128][kv_dtype == TM_DT_BF16][q_dtype != kv_dtype];
-      // 16-bit: a 3-slot ring of 32-position K and V tiles; fp32: a 2-slot
-      // ring of 16-position tiles with rows padded by 4 floats
+      // inlaid head dims [48, 80, 96, 112][cache dtype][split query]
+      static Kernel* kv[4][2][2] = {
+          {{new Kernel("decode_attn_d64v48_f16"), new Kernel("decode_attn_d64v48_f16_x")},
+           {new Kernel("decode_attn_d64v48_bf16"), new Kernel("decode_attn_d64v48_bf16_x")}},
+          {{new Kernel("decode_attn_d128v80_f16"), new Kernel("decode_attn_d128v80_f16_x")},
+           {new Kernel("decode_attn_d128v80_bf16"), new Kernel("decode_attn_d128v80_bf16_x")}},
+          {{new Kernel("decode_attn_d128v96_f16"), new Kernel("decode_attn_d128v96_f16_x")},
+           {new Kernel("decode_attn_d128v96_bf16"), new Kernel("decode_attn_d128v96_bf16_x")}},
+          {{new Kernel("decode_attn_d128v112_f16"), new Kernel("decode_attn_d128v112_f16_x")},
+           {new Kernel("decode_attn_d128v112_bf16"), new Kernel("decode_attn_d128v112_bf16_x")}}};
+      const int bf = kv_dtype == TM_DT_BF16, xq = q_dtype != kv_dtype;
+      const int vi = head_dim == 48 ? 0 : head_dim == 80 ? 1 : head_dim == 96 ? 2 : 3;
+      Kernel& kk = f32      ? (head_dim == 128 ? kf128 : kf64)
+                   : inlaid ? *kv[vi][bf][xq]
+                            : *kd[head_dim == 128][bf][xq];
+      // 16-bit: a 3-slot ring of 32-position K and V tiles in the layout's
+      // head dim; fp32: a 2-slot ring of 16-position tiles with rows padded by
+      // 4 floats
+      const unsigned layout_d = head_dim <= 64 ? 64u : 128u;
       const unsigned lds = f32 ? 2u * 2u * 16u * (unsigned)(head_dim + 4) * 4u
-                               : 3u * 2u * 32u * (unsigned)head_dim * 2u;
+                               : 3u * 2u * 32u * layout_d * 2u;
       int rc = launch(kk, dim3(ns, kv_heads * hbn, batch), dim3(64), lds, stream, p);
       if (rc || ns == 1) return rc;
       static Kernel comb("decode_attn_combine");

@@ -124,15 +124,22 @@ TM_DEV void st_any(void* ptr, long long i, int dt, float v) {
 // pair carries 22 (fp16) or 16 (bf16) significant bits, so scores and the
 // weighted sum keep fp32-level accuracy against the fp32 computation of the
 // reference template instead of one 16-bit rounding of q and P.
-template <int D, bool BF16, bool SPLIT>
+// DV < D: a head dim of DV (a multiple of 16 above D / 2) in the LDS layout of
+// D: the copies skip the 16-byte pieces at or past DV (masked-off lanes write
+// no LDS slot; the K slots are zeroed once, as a k-step may cover them), the
+// query's pieces past DV are zero, the k-steps and d tiles wholly past DV are
+// skipped, and q, o and the slice partials are addressed with DV.
+template <int D, bool BF16, bool SPLIT, int DV = D>
 __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
   constexpr int NST = 3;
   constexpr int PR = D / 8;             // 16-byte pieces per row
   constexpr int TB = 32 * D * 2;        // bytes of one K (or V) tile
   constexpr int NCP = TB / 1024;        // 1 KB copies per tile
   constexpr int RPC = 64 / PR;          // rows per copy
-  constexpr int KS = D / 32;            // k-steps of S^T = K Q^T
-  constexpr int DT = D / 16;            // 16-row d tiles of O^T
+  constexpr int KS = (DV + 31) / 32;    // k-steps of S^T = K Q^T
+  constexpr int DT = DV / 16;           // 16-row d tiles of O^T
+  constexpr int PV = DV / 8;            // pieces of a row below DV
+  static_assert(DV % 16 == 0 && DV <= D && 2 * DV > D, "head dim");
   extern __shared__ __align__(16) uint8_t lds[];
   const int lane = threadIdx.x, l16 = lane & 15, q4 = lane >> 4;
   const int group = p.Hq / p.Hkv, hbn = (group + 15) / 16;
@@ -150,8 +157,8 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
   for (int ks = 0; ks < KS; ++ks) {
     qop[ks] = u4_t{0u, 0u, 0u, 0u};
     if constexpr (SPLIT) qlo[ks] = u4_t{0u, 0u, 0u, 0u};
-    if (hvalid) {
-      const long long qi = ((long long)b * p.Hq + hq) * D + 32 * ks + 8 * q4;
+    if (hvalid && (DV == D || 4 * ks + q4 < PV)) {
+      const long long qi = ((long long)b * p.Hq + hq) * DV + 32 * ks + 8 * q4;
       if constexpr (!SPLIT) {
         qop[ks] = ldg128((const uint16_t*)p.q + qi);
       } else {
@@ -187,6 +194,24 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
     }
     return (long long)b * p.sB + hoff + (long long)pos * p.sS;
   };
+  // the lane's piece of copy i lies below DV (its slot in the ring is fixed)
+  auto piece_in = [&](int i) -> bool {
+    if constexpr (DV == D) {
+      return true;
+    } else {
+      const int r = RPC * i + lane / PR, sl = lane % PR;
+      return (sl ^ (r & (PR - 1))) < PV;
+    }
+  };
+  if constexpr (DV < D) {
+    // the K slots of the pieces past DV in every ring stage: zero once
+    for (int sidx = lane; sidx < NST * 32 * (PR - PV); sidx += 64) {
+      const int stg = sidx / (32 * (PR - PV)), rem = sidx - stg * 32 * (PR - PV);
+      const int r = rem / (PR - PV), c = PV + rem % (PR - PV);
+      *(u4_t*)(lds + stg * 2 * TB + 2 * (r * D + 8 * (c ^ (r & (PR - 1))))) =
+          u4_t{0u, 0u, 0u, 0u};
+    }
+  }
   auto issue = [&](int t) {
     const uint32_t st = lbase + (uint32_t)((t % NST) * 2 * TB);
     // all row offsets first (paged: the page fetches overlap), then the copies
@@ -201,8 +226,10 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
     // 56.4 -> 52.3 us contiguous, 63.8 -> 61.4 us paged)
 #pragma unroll
     for (int i = 0; i < NCP; ++i) {
-      dma16_nt(p.k + e[i], st + 1024 * i);
-      dma16_nt(p.v + e[i], st + TB + 1024 * i);
+      if (piece_in(i)) {
+        dma16_nt(p.k + e[i], st + 1024 * i);
+        dma16_nt(p.v + e[i], st + TB + 1024 * i);
+      }
     }
   };
 #pragma unroll
@@ -290,7 +317,7 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
   // lane holds O^T[16 dt + 4 q4 + e][head l16]
   if (p.nsplit == 1) {
     const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    const long long ob = ((long long)b * p.Hq + hq) * D;
+    const long long ob = ((long long)b * p.Hq + hq) * DV;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -298,12 +325,12 @@ __device__ __forceinline__ void decode_mfma_body(const DecodeParams& p) {
     if (p.lse && q4 == 0)
       p.lse[(long long)b * p.Hq + hq] = l_run > 0.0f ? (m_run + __log2f(l_run)) * kLn2f : -INFINITY;
   } else {
-    float* w = p.ws + (((long long)b * p.Hq + hq) * p.nsplit + split) * (D + 4);
+    float* w = p.ws + (((long long)b * p.Hq + hq) * p.nsplit + split) * (DV + 4);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) *(f4_t*)(w + 16 * dt + 4 * q4) = oacc[dt];
     if (q4 == 0) {
-      w[D] = m_run;
-      w[D + 1] = l_run;
+      w[DV] = m_run;
+      w[DV + 1] = l_run;
     }
   }
 }
@@ -319,6 +346,21 @@ TM_DECODE(128, f16, false)
 TM_DECODE(128, bf16, true)
 TM_DECODE(64, f16, false)
 TM_DECODE(64, bf16, true)
+// head dims 48 (in the 64 layout) and 80, 96, 112 (in the 128 layout):
+// decode_attn_d<D>v<DV>_<dt>[_x]
+#define TM_DECODE_V(D, DV, DT, BF)                                                             \
+  extern "C" __global__ __launch_bounds__(64) void decode_attn_d##D##v##DV##_##DT(DecodeParams p) { \
+    decode_mfma_body<D, BF, false, DV>(p);                                                     \
+  }                                                                                            \
+  extern "C" __global__ __launch_bounds__(64) void decode_attn_d##D##v##DV##_##DT##_x(          \
+      DecodeParams p) {                                                                        \
+    decode_mfma_body<D, BF, true, DV>(p);                                                      \
+  }
+#define TM_DECODE_VD(D, DV) TM_DECODE_V(D, DV, f16, false) TM_DECODE_V(D, DV, bf16, true)
+TM_DECODE_VD(64, 48)
+TM_DECODE_VD(128, 80)
+TM_DECODE_VD(128, 96)
+TM_DECODE_VD(128, 112)
 
 // ----------------------------------------------------------------------------
 // fp32 caches and queries (the dtype of the reference's decode templates other

@@ -175,15 +175,29 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
   // block base moves (32-bit offsets; the host checks 64 * stride < 2^31)
   const int prow = lane / (D / 8), pch = lane % (D / 8);
   uint32_t koff[BPW], voff[BPW];  // byte offsets
-  bool kin[BPW], vin[BPW];        // the lane's chunk lies below DV
 #pragma unroll
   for (int i = 0; i < BPW; ++i) {
     const int r = (wave * BPW + i) * RPB + prow;
     koff[i] = 2u * (uint32_t)(r * (int)p.sks + 8 * (pch ^ k_swz<D>(r)));
     voff[i] = 2u * (uint32_t)(r * (int)p.svs + 8 * (pch ^ v_swz<D>(r)));
-    kin[i] = DV == D || (pch ^ k_swz<D>(r)) < CV;
-    vin[i] = DV == D || (pch ^ v_swz<D>(r)) < CV;
   }
+  // the lane's K / V chunk of block i lies below DV
+  auto kin = [&](int i) -> bool {
+    if constexpr (DV == D) {
+      return true;
+    } else {
+      const int r = (wave * BPW + i) * RPB + prow;
+      return (pch ^ k_swz<D>(r)) < CV;
+    }
+  };
+  auto vin = [&](int i) -> bool {
+    if constexpr (DV == D) {
+      return true;
+    } else {
+      const int r = (wave * BPW + i) * RPB + prow;
+      return (pch ^ v_swz<D>(r)) < CV;
+    }
+  };
   auto issue_kv = [&](uint16_t* kd, uint16_t* vd, int kv0) {
     const uint16_t* kt = kg + (long long)kv0 * p.sks;
     const uint16_t* vt = vg + (long long)kv0 * p.svs;
@@ -191,8 +205,8 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
 #pragma unroll
       for (int i = 0; i < BPW; ++i) {
         const int blk = wave * BPW + i;
-        if (kin[i]) dma16s(kt, koff[i], lds_off(kd) + blk * 1024);
-        if (vin[i]) dma16s(vt, voff[i], lds_off(vd) + blk * 1024);
+        if (kin(i)) dma16s(kt, koff[i], lds_off(kd) + blk * 1024);
+        if (vin(i)) dma16s(vt, voff[i], lds_off(vd) + blk * 1024);
       }
     } else {
       // rows past the end re-read row S - 1 (their scores are masked)
@@ -201,9 +215,9 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
         const int blk = wave * BPW + i;
         const int r = blk * RPB + prow;
         const int back = r - min(r, S - 1 - kv0);
-        if (kin[i])
+        if (kin(i))
           dma16s(kt, koff[i] - 2u * (uint32_t)(back * (int)p.sks), lds_off(kd) + blk * 1024);
-        if (vin[i])
+        if (vin(i))
           dma16s(vt, voff[i] - 2u * (uint32_t)(back * (int)p.svs), lds_off(vd) + blk * 1024);
       }
     }
@@ -255,8 +269,9 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
 #pragma unroll
     for (int c = 0; c < DCV; ++c) {
       qreg[c] = u4_t{0u, 0u, 0u, 0u};
-      if (qi < S && (DV == D || 2 * c + h32 < CV))
-        qreg[c] = ldg128(qg + (long long)qi * p.sqs + 16 * c + 8 * h32);
+      bool qin = qi < S;
+      if constexpr (DV < D) qin = qin && 2 * c + h32 < CV;
+      if (qin) qreg[c] = ldg128(qg + (long long)qi * p.sqs + 16 * c + 8 * h32);
     }
 
     f16_t oacc[DT];
@@ -409,7 +424,9 @@ __device__ __forceinline__ void flash_fwd_body(const FlashParams& p) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d = t * 32 + 8 * g + 4 * h32;
-          if (DV < D && d >= DV) continue;
+          if constexpr (DV < D) {
+            if (d >= DV) continue;
+          }
           u2_t w;
           if (BF16) {
             w.x = pack_bf16x2(oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv);
