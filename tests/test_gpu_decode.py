@@ -115,6 +115,15 @@ def test_decode_fp32_cache_general_kernel(dev):
     _check(dev, q, k, v, [300, 123], 64 ** -0.5, torch.float32)
 
 
+@pytest.mark.parametrize("D", [32, 48, 80, 96, 112, 128])
+@pytest.mark.parametrize("S", [300, 5000])
+def test_decode_fp32_mfma_head_dims(dev, D, S):
+    """fp32 caches and queries on the fp32-MFMA kernel (decode_attn_f32_d<D>,
+    head dims multiples of 16), one slice and many, within 1e-4."""
+    q, k, v = _problem(2, 8, 2, D, S, torch.float32, seed=D + S)
+    _check(dev, q, k, v, [S, S // 3], D ** -0.5, torch.float32)
+
+
 def test_decode_no_workspace_single_slice(dev):
     """Without room for slice partials the MFMA kernel runs one slice per wave."""
     B, Hq, Hkv, D, S = 1, 8, 8, 128, 3000

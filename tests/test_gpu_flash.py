@@ -115,7 +115,7 @@ def test_flash_mfma_inlaid_head_dims(dev, S, D, causal, dtype):
 
 
 @pytest.mark.parametrize("S", [1, 100, 257])
-@pytest.mark.parametrize("D", [32, 64, 96, 128])
+@pytest.mark.parametrize("D", [32, 48, 64, 80, 96, 112, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_flash_fp32_mfma_head_dims(dev, S, D, causal):
     """fp32 (the reference template's dtype) on the fp32-MFMA kernel,

@@ -98,10 +98,10 @@ extern "C" int tm_flash_attention(const void* q, const void* k, const void* v, v
     return launch(flash_kernel(name), dim3((unsigned)grid), dim3(256), 0, stream, p);
   }
   // fp32 (the reference template's dtype): the fp32-MFMA kernel for head dims
-  // 32 / 64 / 96 / 128 with 16-byte aligned rows
+  // 32, 48, ..., 128 with 16-byte aligned rows
   bool st4 = true;
   for (int i = 0; i < 12; ++i) st4 &= (st[i] % 4) == 0;
-  if (dtype == TM_DT_F32 && head_dim % 32 == 0 && head_dim <= 128 && st4 &&
+  if (dtype == TM_DT_F32 && head_dim % 16 == 0 && head_dim >= 32 && head_dim <= 128 && st4 &&
       aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o)) {
     char name[64];
     snprintf(name, sizeof name, "flash_fwd_f32_d%d_%s", head_dim, causal ? "causal" : "full");

@@ -126,8 +126,8 @@ static int decode_attention(const char* op, bool noalloc, const void* q, const v
   const bool rows16 = p.sB % 8 == 0 && p.sH % 8 == 0 && p.sS % 8 == 0;
   // fp32 caches with fp32 queries (the reference templates' dtype): the fp32
   // MFMA kernel, same slices, partials and combine
-  const bool f32 = kv_dtype == TM_DT_F32 && q_dtype == TM_DT_F32 &&
-                   (head_dim == 64 || head_dim == 128) && p.sB % 4 == 0 && p.sH % 4 == 0 &&
+  const bool f32 = kv_dtype == TM_DT_F32 && q_dtype == TM_DT_F32 && head_dim % 16 == 0 &&
+                   head_dim >= 32 && head_dim <= 128 && p.sB % 4 == 0 && p.sH % 4 == 0 &&
                    p.sS % 4 == 0 && aligned16(k_cache) && aligned16(v_cache) && aligned16(q) &&
                    seq_len > 0;
   // 16-bit caches: head dims 64 / 128, and 48 / 80 / 96 / 112 in the layout
@@ -171,7 +171,11 @@ static int decode_attention(const char* op, bool noalloc, const void* q, const v
            {new Kernel("decode_attn_d64_bf16"), new Kernel("decode_attn_d64_bf16_x")}},
           {{new Kernel("decode_attn_d128_f16"), new Kernel("decode_attn_d128_f16_x")},
            {new Kernel("decode_attn_d128_bf16"), new Kernel("decode_attn_d128_bf16_x")}}};
-      static Kernel kf128("decode_attn_f32_d128"), kf64("decode_attn_f32_d64");
+      // fp32: head dims 32, 48, ..., 128
+      static Kernel* kf[7] = {new Kernel("decode_attn_f32_d32"), new Kernel("decode_attn_f32_d48"),
+                              new Kernel("decode_attn_f32_d64"), new Kernel("decode_attn_f32_d80"),
+                              new Kernel("decode_attn_f32_d96"), new Kernel("decode_attn_f32_d112"),
+                              new Kernel("decode_attn_f32_d128")};
       // inlaid head dims [48, 80, 96, 112][cache dtype][split query]
       static Kernel* kv[4][2][2] = {
           {{new Kernel("decode_attn_d64v48_f16"), new Kernel("decode_attn_d64v48_f16_x")},
@@ -184,7 +188,7 @@ static int decode_attention(const char* op, bool noalloc, const void* q, const v
            {new Kernel("decode_attn_d128v112_bf16"), new Kernel("decode_attn_d128v112_bf16_x")}}};
       const int bf = kv_dtype == TM_DT_BF16, xq = q_dtype != kv_dtype;
       const int vi = head_dim == 48 ? 0 : head_dim == 80 ? 1 : head_dim == 96 ? 2 : 3;
-      Kernel& kk = f32      ? (head_dim == 128 ? kf128 : kf64)
+      Kernel& kk = f32      ? *kf[head_dim / 16 - 2]
                    : inlaid ? *kv[vi][bf][xq]
                             : *kd[head_dim == 128][bf][xq];
       // 16-bit: a 3-slot ring of 32-position K and V tiles in the layout's

@@ -377,6 +377,7 @@ TM_DECODE_VD(128, 112)
 // ----------------------------------------------------------------------------
 template <int D>
 __device__ __forceinline__ void decode_f32_body(const DecodeParams& p) {
+  static_assert(D % 16 == 0 && D >= 32 && D <= 128, "head dim");
   constexpr int DS = D + 4;           // LDS row stride (floats)
   constexpr int TILE = 16 * DS;       // floats of one K (or V) tile
   constexpr int PPT = 16 * D / 4 / 64;  // float4 pieces per lane and tile
@@ -514,12 +515,18 @@ __device__ __forceinline__ void decode_f32_body(const DecodeParams& p) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(64) void decode_attn_f32_d128(DecodeParams p) {
-  decode_f32_body<128>(p);
-}
-extern "C" __global__ __launch_bounds__(64) void decode_attn_f32_d64(DecodeParams p) {
-  decode_f32_body<64>(p);
-}
+// decode_attn_f32_d<D>, D = 32, 48, ..., 128
+#define TM_DECODE_F32(D)                                                                    \
+  extern "C" __global__ __launch_bounds__(64) void decode_attn_f32_d##D(DecodeParams p) {   \
+    decode_f32_body<D>(p);                                                                  \
+  }
+TM_DECODE_F32(32)
+TM_DECODE_F32(48)
+TM_DECODE_F32(64)
+TM_DECODE_F32(80)
+TM_DECODE_F32(96)
+TM_DECODE_F32(112)
+TM_DECODE_F32(128)
 
 // ----------------------------------------------------------------------------
 // Combine the slices: grid = B * Hq, block = 64 (D <= 256, 4 per lane).  The

@@ -6,8 +6,8 @@
 // by l only when l > 0 (1747-1754); LSE is the natural-log logsumexp.
 // Products and sums stay fp32 (the MFMA adds 4 fp32 products per step).
 //
-// flash_fwd_f32_d<D>_<mask>, D = 32 / 64 / 96 / 128 with a contiguous head dim
-// and 16-byte aligned rows.  A workgroup of 4 waves owns 64 query rows of one
+// flash_fwd_f32_d<D>_<mask>, D = 32, 48, ..., 128 (multiples of 16) with a
+// contiguous head dim and 16-byte aligned rows.  A workgroup of 4 waves owns 64 query rows of one
 // (b, h), a wave 16.  Per block of 32 keys:
 //   S^T = K Q^T   A = K rows from LDS (lane l: key l % 16, d 4 s + l / 16),
 //                 B = Q^T from registers (query l % 16); the result leaves
@@ -37,8 +37,10 @@ __device__ __forceinline__ void flash_f32_body(const FlashParams& p) {
   constexpr int DSTEP = D / 4;               // k-steps of S^T
   constexpr int DT = D / 16;                 // 16-row d tiles of O^T
   constexpr int TILE = F32_BN * DS;          // floats of one K (or V) tile in LDS
-  constexpr int PPT = F32_BN * D / 4 / 256;  // float4 pieces per thread and tile
-  static_assert(D % 32 == 0 && PPT >= 1 && PPT * 256 * 4 == F32_BN * D, "head dim");
+  constexpr int NPC = F32_BN * D / 4;          // float4 pieces of one tile
+  constexpr int PPT = (NPC + 255) / 256;       // per thread (the last round partial
+                                               // unless D % 32 == 0)
+  static_assert(D % 16 == 0 && D <= 128, "head dim");
   extern __shared__ __align__(16) float smem[];  // [2][K tile, V tile]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -71,7 +73,7 @@ __device__ __forceinline__ void flash_f32_body(const FlashParams& p) {
       const int e = tid + 256 * i, row = e / (D / 4), c4 = e - row * (D / 4);
       const int key = j * F32_BN + row;
       rk[i] = rv[i] = f4_t{0.f, 0.f, 0.f, 0.f};
-      if (key < S) {
+      if ((NPC % 256 == 0 || e < NPC) && key < S) {
         rk[i] = *(const f4_t*)(kg + (long long)key * p.sks + 4 * c4);
         rv[i] = *(const f4_t*)(vg + (long long)key * p.svs + 4 * c4);
       }
@@ -82,6 +84,7 @@ __device__ __forceinline__ void flash_f32_body(const FlashParams& p) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const int e = tid + 256 * i, row = e / (D / 4), c4 = e - row * (D / 4);
+      if (NPC % 256 != 0 && e >= NPC) continue;
       *(f4_t*)(ks + row * DS + 4 * c4) = rk[i];
       *(f4_t*)(ks + TILE + row * DS + 4 * c4) = rv[i];
     }
@@ -178,9 +181,15 @@ __device__ __forceinline__ void flash_f32_body(const FlashParams& p) {
   }
 TM_FLASH_F32(32, false, full)
 TM_FLASH_F32(32, true, causal)
+TM_FLASH_F32(48, false, full)
+TM_FLASH_F32(48, true, causal)
 TM_FLASH_F32(64, false, full)
 TM_FLASH_F32(64, true, causal)
+TM_FLASH_F32(80, false, full)
+TM_FLASH_F32(80, true, causal)
 TM_FLASH_F32(96, false, full)
 TM_FLASH_F32(96, true, causal)
+TM_FLASH_F32(112, false, full)
+TM_FLASH_F32(112, true, causal)
 TM_FLASH_F32(128, false, full)
 TM_FLASH_F32(128, true, causal)
