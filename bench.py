@@ -383,7 +383,8 @@ EXTRA = {"hbm_copy": hbm_copy,
          "dot_fp16_addmatrix_2048": lambda d: dot_general(d, "trans_b", "fp16", 2048, 2048, 2048,
                                                           epilogue="add-matrix"),
          "dot_fp32_colmajor_a_4096": lambda d: dot_general(d, "colmajor_a", "fp32", 4096, 4096, 4096),
-         # the 64 x 64 tiled kernel (int4, K = 11008 past the wide kernels)
+         # int4 K = 11008 (43 units of 256 k): the wide kernel's split form in
+         # uneven slices (the tiled kernel with uint8 zero-points or bf16)
          "w4a16_m128_k11008": lambda d: w4a16_wide_k(d, 128, K=11008),
          "w4a16_m512_k11008": lambda d: w4a16_wide_k(d, 512, K=11008),
          "w8a16_m1_k14336": lambda d: w8a16_wide_k(d, 1),

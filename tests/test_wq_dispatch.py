@@ -99,13 +99,19 @@ def test_split_k_plans():
     d0 = tm.wq_kernel_for(4, 24, 1024, 20480, zero_dtype=torch.float16, with_workspace=False,
                           details=True)
     assert d0["name"].startswith("wq_tiled_") and d0["splits"] == 1 and d0["workspace_bytes"] == 0
-    # the tiled kernel with fewer tiles than CUs: slices of whole 256-k steps,
-    # about two workgroups per CU, at most 16 slices, the last one shorter
+    # int4 K = 11008 (43 units of 256, K % 512 != 0): the wide kernel's split
+    # form in slices of whole units, the last one shorter; uint8 zero-points
+    # (whose split gathers need 512-k slices) and bf16 activations take the
+    # tiled kernel, split when its tiles fill fewer than the CUs
     d = tm.wq_kernel_for(4, 128, 4096, 11008, zero_dtype=torch.float16, details=True)
-    assert d["name"] == "wq_tiled_q4_f16_zs_k" and d["splits"] == 4
+    assert d["name"] == "wq_wide_q4_f16_zs_k" and d["splits"] == 4
     assert d["workspace_bytes"] == 4 * 128 * 4096 * 4
     d = tm.wq_kernel_for(4, 512, 4096, 11008, zero_dtype=torch.float16, details=True)
-    assert d["name"] == "wq_tiled_q4_f16_zs" and d["splits"] == 1
+    assert d["name"] == "wq_wide_q4_f16_zs_k" and d["splits"] == 3
+    d = tm.wq_kernel_for(4, 128, 4096, 11008, zero_dtype=torch.uint8, details=True)
+    assert d["name"] == "wq_tiled_q4_f16_zu_k" and d["splits"] == 4
+    d = tm.wq_kernel_for(4, 512, 4096, 11008, act_dtype=torch.bfloat16, details=True)
+    assert d["name"] == "wq_tiled_q4_bf16_zn" and d["splits"] == 1
     d = tm.wq_kernel_for(8, 80, 64, 4352, details=True)
     assert d["name"] == "wq_tiled_q8_f16_zn_k" and d["splits"] == 9
     # shapes a single launch covers never split, with or without a workspace

@@ -30,6 +30,11 @@ CASES += _each(8, 80, 256, 512, zeros=(None,), ws=False)
 CASES += _each(4, 96, 1024, 8192, acts=(torch.float16,))
 CASES += _each(8, 96, 1024, 4096, zeros=(None,))
 CASES += _each(4, 128, 4096, 14336, acts=(torch.float16,), zeros=("s",))
+# int4 K % 512 == 256 (fp16 or no zero-points): one launch (K = 3840), and
+# split-K into slices of 256-k units with a shorter last one (K = 11008 = 43
+# units: 4 slices of 11, 11, 11, 10)
+CASES += _each(4, 80, 256, 3840, acts=(torch.float16,), zeros=(None, "s"), ws=False)
+CASES += _each(4, 128, 256, 11008, acts=(torch.float16,), zeros=(None, "s"))
 # two-tile int4 GEMV, 2 <= M <= 6, K = 4096
 CASES += _each(4, 3, 64, 4096)
 # streaming kernels: x8s (M <= 8), x16s (M <= 16), x16m (M <= 64 / 128)

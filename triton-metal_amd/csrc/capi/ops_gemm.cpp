@@ -79,14 +79,18 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
   // int8: fp16 or bf16).  With a workspace, split-K over S k-slices when its
   // tiles would fill less than half the CUs, or when int4 K exceeds the 4096
   // whose scales fit in LDS
+  // (int4: K % 512 == 0 with uint8 zero-points, whose per-row bytes the
+  // split form gathers as dwords; K % 256 == 0 otherwise.  Where no equal
+  // slicing fits, slices of whole units with a shorter last one.)
+  const bool w4k = qbits == 4 && (K % 512 == 0 || (K % 256 == 0 && zdt != TM_DT_U8));
   if (fast && M > 64 && N % 128 == 0 && s16 && z16 &&
-      ((qbits == 4 && adt == TM_DT_F16 && G == 128 && K % 512 == 0) ||
+      ((w4k && adt == TM_DT_F16 && G == 128) ||
        (qbits == 8 && zdt == TM_DT_NONE && K % 128 == 0))) {
     const int ns = qbits == 4 ? 3 : 4, ck = qbits == 4 ? 64 : 32;
-    const int unit = qbits == 4 ? 512 : 128;  // slice granularity
+    const int unit = qbits == 4 ? (K % 512 == 0 ? 512 : 256) : 128;  // slice granularity
     const int mtl = (M + 63) / 64, ntl = N / 128;
     const long tiles = (long)mtl * ntl;
-    int S = 1;
+    int S = 1, Ks = K;
     if (split_ok && (tiles < cus / 2 || (qbits == 4 && K > 4096))) {
       S = 0;
       // the largest valid slice count up to the one that fills the CUs, else
@@ -98,9 +102,19 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
         if (ok(s2)) S = s2;
       for (int s2 = want + 1; s2 <= 16 && !S; ++s2)
         if (ok(s2)) S = s2;
-      if (!S && !(qbits == 4 && K > 4096)) S = 1;
+      if (S) {
+        Ks = K / S;
+      } else if (qbits == 4 && K > 4096) {
+        // slices of whole units, the last one shorter
+        const int units = K / unit, per = (units + want - 1) / want;
+        if ((long)per * unit <= 4096) {
+          S = (units + per - 1) / per;
+          Ks = per * unit;
+        }
+      } else {
+        S = 1;
+      }
     }
-    const int Ks = S ? K / S : K;
     if (S && (qbits == 8 || Ks <= 4096)) {
       size_t wl = (size_t)ns * 4 * (64 * 2 * ck + 4096);  // ring stages
       if (qbits == 4)  // scales and zero-points of the 128 columns
@@ -111,7 +125,7 @@ void wq_plan(int qbits, int M, int N, int K, int G, int adt, int sdt, int zdt, u
                  S > 1 ? "_k" : "");
         set(8 * mtl * ((ntl + 7) / 8), 512, wl, S > 1 ? WQ_ARGS_SPLIT : WQ_ARGS_STD);
         pl->splits = S;
-        pl->kslice = K / S;
+        pl->kslice = Ks;
         pl->ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
         return;
       }

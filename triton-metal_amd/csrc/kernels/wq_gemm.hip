@@ -1256,8 +1256,9 @@ __device__ __forceinline__ void wq_tiled_body(const uint16_t* __restrict__ X,
 }
 
 // ----------------------------------------------------------------------------
-// Wide kernel: fp16 activations, M > 64; int4 with G = 128 (K % 512 == 0,
-// K <= 4096) or int8 without zero-points (K % 128 == 0); N % 128 == 0.
+// Wide kernel: fp16 activations, M > 64; int4 with G = 128 (K % 256 == 0,
+// K % 512 == 0 with uint8 zero-points; K <= 4096) or int8 without
+// zero-points (K % 128 == 0); N % 128 == 0.
 // A workgroup owns 64 rows x 128 columns.  Its 8 waves are 2 column halves
 // (64 columns) x 4 K-quarters; each wave accumulates a 64 x 64 block with
 // v_mfma_f32_32x32x16_f16 (2 x 2 tiles of 32 x 32), and the four K-quarter
@@ -1318,9 +1319,10 @@ TM_DEV u4_t w4_exact(uint32_t w, float z, float s) {
 }  // namespace
 
 // Split-K form (SPLIT): workgroup row blockIdx.y takes the k-slice
-// [blockIdx.y K, + K) of rows ldk long and writes its fp32 sums (scaled, no
-// bias) to P[blockIdx.y][M][N]; the int4 scale / zero-point rows of the slice
-// are gathered row by row (ldk / 128 groups apart).
+// [blockIdx.y K, + K) of rows ldk long (the last slice ends at ldk, so it may
+// be shorter) and writes its fp32 sums (scaled, no bias) to
+// P[blockIdx.y][M][N]; the int4 scale / zero-point rows of the slice are
+// gathered row by row (ldk / 128 groups apart).
 // BF16: bf16 activations, int8 only (q is exact in bf16 and the per-channel
 // scale multiplies the fp32 sums; an int4 operand dequantised to bf16 would
 // round every weight to 8 bits).
@@ -1355,9 +1357,10 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
   const int mb = j % mtl, nb = 8 * (j / mtl) + (blockIdx.x & 7);
   if (nb >= ntl) return;
   const int m0 = mb * 64, n0 = nb * 128;
-  const int NC = K / (4 * CK);  // stages of 4 CK k
   if constexpr (!SPLIT) ldk = K;
   const int ks0 = SPLIT ? (int)blockIdx.y * K : 0;
+  if constexpr (SPLIT) K = min(K, ldk - ks0);  // the last slice may be shorter
+  const int NC = K / (4 * CK);  // stages of 4 CK k
   X += ks0;
   W += QB == 4 ? ks0 >> 1 : ks0;
   const size_t wrow = QB == 4 ? (size_t)(ldk >> 1) : (size_t)ldk;
@@ -1380,8 +1383,9 @@ __device__ __forceinline__ void wq_wide_body(const uint16_t* __restrict__ X,
           if (o + 16 * lane < zb)
             dma16((const uint8_t*)Z + (size_t)n0 * ng * ZRB + o + 16 * lane, sbase + sb + o);
     } else {
-      // dword d of the [row][group] block: row d / (ng * ZB / 4) (K % 512 == 0
-      // keeps every row a whole number of dwords)
+      // dword d of the [row][group] block: row d / (ng * ZB / 4) (slices of
+      // 256 k keep every row of scales and fp16 zero-points a whole number of
+      // dwords; uint8 zero-points take slices of 512)
       const int sdw = ng / 2, zdw = ng * ZRB / 4;
       for (int o = 64 * wave; o < 128 * sdw; o += 512) {
         const int d = o + lane, r = d / sdw, j = d - r * sdw;
