@@ -162,12 +162,9 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
   // 128 tile per CU the 64 tiles measured faster: fp16 2048^3 81 -> 57 us,
   // 4 x 1024^3 46 -> 33 us, while 2560 x 2560 x 4096 (400 tiles of 128) kept
   // the 128 tiles, 167 against 189 us), else the element-load form dot_tile_s
-  static Kernel* k64[4] = {new Kernel("dot_tile_f16"), new Kernel("dot_tile_bf16"),
-                           new Kernel("dot_tile_fp8"), new Kernel("dot_tile_f32")};
-  static Kernel* k128[3] = {new Kernel("dot_tile128_f16"), new Kernel("dot_tile128_bf16"),
-                            new Kernel("dot_tile128_fp8")};
   static Kernel* ks[4] = {new Kernel("dot_tile_s_f16"), new Kernel("dot_tile_s_bf16"),
                           new Kernel("dot_tile_s_fp8"), new Kernel("dot_tile_s_f32")};
+  static Kernel* k32 = new Kernel("dot_tile_f32");
   const int kind = in_dtype == TM_DT_F32 ? 3 : is_fp8(in_dtype) ? 2 : in_dtype == TM_DT_BF16 ? 1 : 0;
   const bool vec = p.a_mode != MODE_SCALAR && p.b_mode != MODE_SCALAR;
   const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
@@ -175,7 +172,16 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
   const int edge = big ? 128 : 64;
   const long long tiles = (long long)((M + edge - 1) / edge) * ((N + edge - 1) / edge);
   if (tiles > 0x7fffffffLL) return fail(TM_ERR_UNSUPPORTED, "%s: too many tiles", op);
-  Kernel& kt = big ? *k128[kind] : vec ? *k64[kind] : *ks[kind];
+  Kernel* kp = vec ? k32 : ks[kind];
+  if (vec && kind != 3) {
+    // dot_tile{,128}_<dt>_<a><b>: each operand k- (k) or row-contiguous (r)
+    static const char* dts[3] = {"f16", "bf16", "fp8"};
+    char name[64];
+    snprintf(name, sizeof name, "dot_tile%s_%s_%c%c", big ? "128" : "", dts[kind],
+             p.a_mode == MODE_RC ? 'r' : 'k', p.b_mode == MODE_RC ? 'r' : 'k');
+    kp = &kernel_named(name);
+  }
+  Kernel& kt = *kp;
   return launch(kt, dim3((unsigned)tiles, (unsigned)batch), dim3(256), 0, stream, p);
 }
 

@@ -25,19 +25,7 @@ const char* dt_name(int dt) {
   }
 }
 
-// Kernel registry keyed by name (names are compile-time constants of the
-// instantiations in the .hip sources).
-Kernel& kernel(const std::string& name) {
-  static std::mutex mu;
-  static std::map<std::string, Kernel*> table;
-  std::lock_guard<std::mutex> lk(mu);
-  auto it = table.find(name);
-  if (it != table.end()) return *it->second;
-  char* stored = strdup(name.c_str());
-  Kernel* k = new Kernel(stored);
-  table[name] = k;
-  return *k;
-}
+Kernel& kernel(const std::string& name) { return tmhip::kernel_named(name); }
 
 // ---- W-only kernel selection ------------------------------------------------
 // A pure function of the problem (sizes, dtypes, pointer alignment, the
@@ -727,3 +715,17 @@ int tm_linear(const void* input, const void* weight, const void* bias, void* out
 }
 
 }  // extern "C"
+
+// Kernel registry keyed by name (names are compile-time constants of the
+// instantiations in the .hip sources).
+Kernel& tmhip::kernel_named(const std::string& name) {
+  static std::mutex mu;
+  static std::map<std::string, Kernel*> table;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = table.find(name);
+  if (it != table.end()) return *it->second;
+  char* stored = strdup(name.c_str());
+  Kernel* k = new Kernel(stored);
+  table[name] = k;
+  return *k;
+}

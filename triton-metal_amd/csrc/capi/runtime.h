@@ -83,6 +83,8 @@ int current_device(int* dev);
 int max_dynamic_lds();
 // Compute units of the current device (256 if the query fails).
 int cu_count();
+// The kernel of this name (created on first use, kept for the process).
+Kernel& kernel_named(const std::string& name);
 
 // Launch helper: args are passed by value and forwarded as kernelParams.
 template <class... Args>

@@ -168,20 +168,29 @@ TM_DEV void tile_epilogue(const DotParams& p, const f4_t (&acc)[FT][FT], int m0,
 // tile count is a multiple of 8, XCD x takes tiles x T / 8 .. (x + 1) T / 8 - 1,
 // rows of tiles that share their A rows in one L2.
 // ----------------------------------------------------------------------------
+typedef short dot_s4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) dot_s4_t dot_lds_s4_t;
+TM_DEV u2_t dot_tr16(const uint16_t* p) {
+  dot_s4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((dot_lds_s4_t*)(p));
+  return __builtin_bit_cast(u2_t, v);
+}
+
 TM_DEV int tile_lds(int row, int k, int ldk) {
   return row * ldk + ((((k >> 3) ^ (row >> 4)) & 3) | (k >> 3 & ~3)) * 8 + (k & 7);
 }
 
-template <bool BF16, bool FP8, int BT>
+template <bool BF16, bool FP8, int BT, bool ARC, bool BRC>
 __device__ __forceinline__ void dot_tile_vec_body(const DotParams& p) {
   constexpr int BK = BT == 64 ? 64 : 32, LDK = BK + 8;
+  constexpr int LDT = BT + 16;  // RC operands: [k][BT rows + 16 pad]
   constexpr int WT = BT / 2;   // wave tile edge
   constexpr int FT = WT / 16;  // MFMA tiles per wave tile edge
   constexpr int RP = BT / 64;  // row blocks of 64 per operand step
   constexpr int NP = RP * BK / 32;  // pieces per thread and operand step
   constexpr int esz = FP8 ? 1 : 2;
-  __shared__ __align__(16) uint16_t As[2][BT * LDK];
-  __shared__ __align__(16) uint16_t Bs[2][BT * LDK];
+  constexpr int ASZ = ARC ? BK * LDT : BT * LDK, BSZ = BRC ? BK * LDT : BT * LDK;
+  __shared__ __align__(16) uint16_t As[2][ASZ];
+  __shared__ __align__(16) uint16_t Bs[2][BSZ];
   __shared__ uint16_t lut[256];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -228,27 +237,47 @@ __device__ __forceinline__ void dot_tile_vec_body(const DotParams& p) {
     if constexpr (FP8) return (uint32_t)lut[x];
     else return x;
   };
-  // piece h (fetched at k0) into LDS buffer Xs, elements past the operand zeroed
-  auto put = [&](uint16_t* Xs, int mode, u4_t w, int rows, int r0, int k0, int h) {
+  // piece h (fetched at k0) into LDS buffer Xs, elements past the operand
+  // zeroed: KC pieces into [row][k] (swizzled), RC pieces (8 rows at one k)
+  // as they are into [k][rows]
+  auto put = [&](auto rcc, uint16_t* Xs, u4_t w, int rows, int r0, int k0, int h) {
+    constexpr bool RC = decltype(rcc)::value;
     const int rs = 64 * (h % RP), ks = 32 * (h / RP);
-    if (mode == MODE_RC) {
+    int n, off;
+    if constexpr (RC) {
       const int rc = rs + 8 * (tid & 7), kk = ks + (tid >> 3);
-      const int n = k0 + kk < p.K ? max(0, min(rows - r0 - rc, 8)) : 0;
-      if (n < 8) w = piece_keep<FP8>(w, n);
-      uint16_t* dst = Xs + tile_lds(rc, kk, LDK);  // rows rc .. rc + 7 share (r / 16) % 4
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dst[e * LDK] = (uint16_t)cvt(elem(w, e));
-      return;
+      n = k0 + kk < p.K ? max(0, min(rows - r0 - rc, 8)) : 0;
+      off = kk * LDT + rc;
+    } else {
+      const int r = rs + (tid >> 2), kc = ks + 8 * (tid & 3);
+      n = r0 + r < rows ? max(0, min(p.K - k0 - kc, 8)) : 0;
+      off = tile_lds(r, kc, LDK);
     }
-    const int r = rs + (tid >> 2), kc = ks + 8 * (tid & 3);
-    const int n = r0 + r < rows ? max(0, min(p.K - k0 - kc, 8)) : 0;
     if (n < 8) w = piece_keep<FP8>(w, n);
     u4_t o = w;
     if constexpr (FP8) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) o[d] = cvt(elem(w, 2 * d)) | (cvt(elem(w, 2 * d + 1)) << 16);
     }
-    *(u4_t*)(Xs + tile_lds(r, kc, LDK)) = o;
+    *(u4_t*)(Xs + off) = o;
+  };
+  // MFMA operand of rows r0 .. r0 + 15 at k kb .. kb + 31: lane l supplies row
+  // l % 16, k kb + 8 (l / 16) .. +7.  KC: one 16-byte read.  RC: two
+  // transposing reads (ds_read_b64_tr_b16: lane i of a 16-lane group gets
+  // element i % 4 of the 8 bytes lane 4 e + i / 4 addresses, for e = 0..3),
+  // lane j addressing rows r0 + 4 (j % 4) .. +3 at k kb + 8 (l / 16) + j / 4
+  // (+ 4 for the second read)
+  const std::integral_constant<bool, true> rc_c;
+  const std::integral_constant<bool, false> kc_c;
+  auto frag = [&](auto rcc, const uint16_t* Xs, int r0, int kb) -> u4_t {
+    if constexpr (decltype(rcc)::value) {
+      const int j = lane & 15;
+      const uint16_t* a = Xs + (kb + 8 * (lane >> 4) + (j >> 2)) * LDT + r0 + 4 * (j & 3);
+      const u2_t lo = dot_tr16(a), hi = dot_tr16(a + 4 * LDT);
+      return u4_t{lo.x, lo.y, hi.x, hi.y};
+    } else {
+      return *(const u4_t*)(Xs + tile_lds(r0 + (lane & 15), kb + 8 * (lane >> 4), LDK));
+    }
   };
 
   f4_t acc[FT][FT];
@@ -259,18 +288,21 @@ __device__ __forceinline__ void dot_tile_vec_body(const DotParams& p) {
 
   const int nk = (p.K + BK - 1) / BK;
   u4_t ra0[NP], rb0[NP], ra1[NP], rb1[NP];
+  constexpr int AM = ARC ? MODE_RC : MODE_KC, BM = BRC ? MODE_RC : MODE_KC;
   auto load_step = [&](u4_t* ra, u4_t* rb, int kt) {
 #pragma unroll
     for (int h = 0; h < NP; ++h) {
-      ra[h] = fetch(Ab, p.a_mode, p.M, m0, p.sa_m, p.sa_k, kt * BK, h);
-      rb[h] = fetch(Bb, p.b_mode, p.N, n0, p.sb_n, p.sb_k, kt * BK, h);
+      ra[h] = fetch(Ab, AM, p.M, m0, p.sa_m, p.sa_k, kt * BK, h);
+      rb[h] = fetch(Bb, BM, p.N, n0, p.sb_n, p.sb_k, kt * BK, h);
     }
   };
   auto put_step = [&](int buf, const u4_t* ra, const u4_t* rb, int kt) {
 #pragma unroll
     for (int h = 0; h < NP; ++h) {
-      put(As[buf], p.a_mode, ra[h], p.M, m0, kt * BK, h);
-      put(Bs[buf], p.b_mode, rb[h], p.N, n0, kt * BK, h);
+      if constexpr (ARC) put(rc_c, As[buf], ra[h], p.M, m0, kt * BK, h);
+      else put(kc_c, As[buf], ra[h], p.M, m0, kt * BK, h);
+      if constexpr (BRC) put(rc_c, Bs[buf], rb[h], p.N, n0, kt * BK, h);
+      else put(kc_c, Bs[buf], rb[h], p.N, n0, kt * BK, h);
     }
   };
   const int q = lane >> 4, r16 = lane & 15;
@@ -279,11 +311,15 @@ __device__ __forceinline__ void dot_tile_vec_body(const DotParams& p) {
     for (int s = 0; s < BK / 32; ++s) {
       u4_t af[FT], bfr[FT];
 #pragma unroll
-      for (int i = 0; i < FT; ++i)
-        af[i] = *(const u4_t*)(As[buf] + tile_lds(WT * wm + 16 * i + r16, 32 * s + 8 * q, LDK));
+      for (int i = 0; i < FT; ++i) {
+        if constexpr (ARC) af[i] = frag(rc_c, As[buf], WT * wm + 16 * i, 32 * s);
+        else af[i] = frag(kc_c, As[buf], WT * wm + 16 * i, 32 * s);
+      }
 #pragma unroll
-      for (int j = 0; j < FT; ++j)
-        bfr[j] = *(const u4_t*)(Bs[buf] + tile_lds(WT * wn + 16 * j + r16, 32 * s + 8 * q, LDK));
+      for (int j = 0; j < FT; ++j) {
+        if constexpr (BRC) bfr[j] = frag(rc_c, Bs[buf], WT * wn + 16 * j, 32 * s);
+        else bfr[j] = frag(kc_c, Bs[buf], WT * wn + 16 * j, 32 * s);
+      }
 #pragma unroll
       for (int i = 0; i < FT; ++i)
 #pragma unroll
@@ -437,10 +473,16 @@ __device__ __forceinline__ void dot_tile_s_body(const DotParams& p) {
 
 // dot_tile{,128}_<f16|bf16|fp8> and dot_tile_s_<f16|bf16|fp8>: fp8 covers
 // the five FP8 formats (in_dt), decoded to fp16 through the table
-#define TM_DOT_TILE(NAME, BF16, FP8, BT)                                            \
+#define TM_DOT_TILE_M(NAME, BF16, FP8, BT, ARC, BRC)                                \
   extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {             \
-    dot_tile_vec_body<BF16, FP8, BT>(p);                                            \
+    dot_tile_vec_body<BF16, FP8, BT, ARC, BRC>(p);                                  \
   }
+// _<a><b>: each operand k-contiguous (k) or row-contiguous (r)
+#define TM_DOT_TILE(NAME, BF16, FP8, BT)                         \
+  TM_DOT_TILE_M(NAME##_kk, BF16, FP8, BT, false, false)          \
+  TM_DOT_TILE_M(NAME##_kr, BF16, FP8, BT, false, true)           \
+  TM_DOT_TILE_M(NAME##_rk, BF16, FP8, BT, true, false)           \
+  TM_DOT_TILE_M(NAME##_rr, BF16, FP8, BT, true, true)
 #define TM_DOT_TILE_S(NAME, BF16, FP8)                                              \
   extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {             \
     dot_tile_s_body<BF16, FP8>(p);                                                  \
