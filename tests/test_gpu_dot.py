@@ -91,6 +91,23 @@ def test_dot_fp32_layouts(dev, layout, M, N, K, out):
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,K", [(5, 3, 40), (7, 70, 130), (130, 6, 33)])
+def test_dot_row_contiguous_operands_with_few_rows(dev, dt, M, N, K):
+    """Row-contiguous operands (A stored [K, M], B [K, N]) with fewer rows
+    than one 16-byte piece holds, as narrow views of buffers whose leading
+    dimension is a multiple of 8: the 16-byte loads read past the operand
+    inside the buffer's rows, and those elements must not reach C."""
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    lda, ldb = (M + 7) // 8 * 8, (N + 7) // 8 * 8
+    Ab = torch.randn(K, lda, generator=g).to(dt)
+    Bb = torch.randn(K, ldb, generator=g).to(dt)
+    a, b = Ab[:, :M].t(), Bb[:, :N]  # logical [M, K] and [K, N] views
+    c = torch.empty(M, N, dtype=torch.float32, device=dev)
+    tm.dot(Ab.to(dev)[:, :M].t(), Bb.to(dev)[:, :N], c)
+    _check(c, oracle.dot(_np(a), _np(b)), torch.float32, np.abs(_np(a)), np.abs(_np(b)))
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 def test_dot_column_major_output(dev, dt):
     """The reference's "trans" case: C written through column-major strides."""
     M, N, K = 96, 80, 64
