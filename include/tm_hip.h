@@ -291,7 +291,9 @@ int tm_gemm_plan(int M, int N, int K, int lda, int ldb, int ldc, int trans_b, in
  * gives O = 0 and lse = -inf (1747-1754).  Replaces the template's buffer ABI
  * Q, K, V, O, seq_len, scale (1624-1634) and the @triton.jit _flash_attn_fwd
  * signature (tests/test_flash_attention.py:24-33).
- * dtype F16/BF16 (MFMA kernel for head_dim 32/64/128) or F32; head_dim <= 128. */
+ * dtype F16/BF16 (MFMA kernel for head_dim 32, 48, 64, 80, 96, 112, 128) or
+ * F32 (MFMA kernel for head_dim a multiple of 16 from 32 to 128); other head
+ * dims (<= 128) and strides on a one-thread-per-row kernel. */
 int tm_flash_attention(const void* q, const void* k, const void* v, void* o, float* lse,
                        int batch, int heads, int seq_len, int head_dim,
                        const long long* strides, float scale, int causal, int dtype,
@@ -319,8 +321,9 @@ int tm_flash_attention(const void* q, const void* k, const void* v, void* o, flo
  * position p sits in page page_table[b][p / page_size], slot p % page_size.
  * workspace: scratch for per-slice partials of long sequences, at least
  * tm_decode_attention_workspace_size(...) bytes (NULL or smaller: no slices).
- * fp16 / bf16 caches with head_dim 64 or 128 run on MFMA kernels; everything
- * else (head_dim <= 256) on an fp32 kernel.  With a query dtype other than
+ * fp16 / bf16 caches with head_dim 48, 64, 80, 96, 112 or 128, and fp32 caches
+ * with fp32 queries and head_dim a multiple of 16 from 32 to 128, run on MFMA
+ * kernels; everything else (head_dim <= 256) on an fp32 kernel.  With a query dtype other than
  * the cache's (an fp32 query over a 16-bit cache, as
  * make_fp16_kv_attention_kernel, _msl_templates.py:2558-2576, computes it) the
  * MFMA kernels carry the query and the softmax weights as hi + lo pairs of
