@@ -207,6 +207,23 @@ def test_dot_softmax(dev, dt, N):
     np.testing.assert_allclose(c.sum(-1).cpu().numpy(), 1.0, rtol=1e-5)
 
 
+@pytest.mark.parametrize("layout", ["row", "trans_a", "trans_b", "strided"])
+@pytest.mark.parametrize("out", [torch.float32, torch.float16])
+def test_dot_softmax_batched(dev, layout, out):
+    """Batched softmax: an fp32 output takes the tile kernels and the in-place
+    row softmax (dot_softmax_rows), a 16-bit one dot_rows; both against the
+    softmax of the fp64 product."""
+    B, M, N, K = 3, 70, 300, 96
+    da, db, a, b = _views(M, N, K, torch.bfloat16, layout, seed=47, batch=B)
+    c = torch.empty(B, M, N, dtype=out, device=dev)
+    tm.dot(da, db, c, "softmax")
+    ref = oracle.dot(_np(a), _np(b), "softmax")
+    if out == torch.float32:
+        np.testing.assert_allclose(c.cpu().numpy(), ref, atol=1e-6, rtol=1e-4)
+    else:
+        np.testing.assert_allclose(c.float().cpu().numpy(), ref, atol=1e-3, rtol=1e-2)
+
+
 @pytest.mark.parametrize("dt", [torch.float16, torch.float32])
 def test_dot_chain(dev, dt):
     M, N, K, L = 50, 64, 80, 24

@@ -122,6 +122,23 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
     }
   }
   if (!rows_kernel && batch > 65535) rows_kernel = true;
+  // softmax with an fp32 output that shares no memory with A or B: the
+  // product (unrounded fp32) through the tile kernels into C, then each row
+  // replaced by its softmax (dot_rows re-reads all of B for every row)
+  if (epilogue == TM_EPI_SOFTMAX && out_dtype == TM_DT_F32 && K > 0 && batch <= 65535) {
+    uintptr_t al, ah, bl, bh, cl, chh;
+    const int isz = elem_size(in_dtype);
+    extent(A, isz, batch, M, K, st[0], st[1], st[2], &al, &ah);
+    extent(B, isz, batch, K, N, st[3], st[4], st[5], &bl, &bh);
+    extent(C, 4, batch, M, N, st[6], st[7], st[8], &cl, &chh);
+    if (!(cl < ah && al < chh) && !(cl < bh && bl < chh)) {
+      int rc = dot_impl(op, A, B, C, nullptr, nullptr, batch, M, N, K, 0, st, TM_EPI_NONE,
+                        in_dtype, TM_DT_F32, TM_DT_NONE, TM_DT_NONE, stream);
+      if (rc) return rc;
+      static Kernel ksm("dot_softmax_rows");
+      return launch(ksm, dim3((unsigned)((long long)batch * M)), dim3(256), 0, stream, p);
+    }
+  }
   // fp32 without an epilogue, one batch, k- and n-contiguous rows (B as [K, N]
   // or [N, K]): the fp32-MFMA dense kernel
   const auto fits = [](long long v) { return v >= 0 && v <= 0x7fffffffLL; };

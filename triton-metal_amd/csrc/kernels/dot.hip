@@ -31,7 +31,8 @@
 // dot_rows: one workgroup per (batch, row), fp32 FMA, any dtype and strides,
 // every epilogue.  The softmax and chain-dot epilogues need the whole row of
 // the product, which the workgroup keeps in LDS (N <= 8192); it also serves
-// K = 0 and a bias read in place across rows.
+// K = 0 and a bias read in place across rows.  With an fp32 output the
+// softmax takes the tile kernels and dot_softmax_rows instead.
 #include "common.h"
 
 enum { EPI_NONE = 0, EPI_ADD_MATRIX = 1, EPI_ADD_ROWS = 2, EPI_ADD_COLS = 3, EPI_SOFTMAX = 4,
@@ -630,6 +631,39 @@ extern "C" __global__ __launch_bounds__(256) void dot_tile_f32(DotParams p) {
 }
 extern "C" __global__ __launch_bounds__(256) void dot_tile_s_f32(DotParams p) {
   dot_tile_f32_body<false>(p);
+}
+
+// ----------------------------------------------------------------------------
+// dot_softmax_rows: grid batch * M, block 256.  The softmax epilogue with an
+// fp32 output after the tile kernels have written the unrounded fp32 product
+// into C: each workgroup replaces its row by exp(x - max) / sum, with the
+// arithmetic of dot_rows' softmax (N <= 8192).
+// ----------------------------------------------------------------------------
+extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) {
+  constexpr int NMAX = 8192;
+  __shared__ float prow[NMAX];
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x / p.M, m = blockIdx.x - b * p.M;
+  float* crow = (float*)p.C + (long long)b * p.sc_b + (long long)m * p.sc_m;
+  for (int n = tid; n < p.N; n += 256) prow[n] = crow[(long long)n * p.sc_n];
+  __syncthreads();
+  float mx = -__builtin_inff();
+  for (int n = tid; n < p.N; n += 256) mx = fmaxf(mx, prow[n]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float sm = 0.0f;
+  for (int n = tid; n < p.N; n += 256) sm += expf(prow[n] - mx);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sm += __shfl_xor(sm, o, 64);
+  if (lane == 0) red[wave] = sm;
+  __syncthreads();
+  sm = red[0] + red[1] + red[2] + red[3];
+  for (int n = tid; n < p.N; n += 256) crow[(long long)n * p.sc_n] = expf(prow[n] - mx) / sm;
 }
 
 // ----------------------------------------------------------------------------
