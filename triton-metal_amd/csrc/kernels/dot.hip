@@ -16,12 +16,12 @@
 // dot_tile: MFMA kernel for 16-bit and FP8 inputs with the none / add-*
 // epilogues.  64 x 64 output tile (dot_tile128: 128 x 128, for problems with
 // enough tiles to fill the chip) per 256-thread workgroup (2 x 2 waves,
-// v_mfma_f32_16x16x32), K in steps of 32 through two LDS buffers,
-// operands stored k-contiguous in LDS whatever their layout in memory.  Each
-// operand is fetched in one of three modes chosen by the host from its
-// strides: k-contiguous (16-byte row pieces), row-contiguous (a transposed
-// view: 16-byte pieces of 8 rows at one k, scattered into LDS) or scalar
-// (any strides).  FP8 codes are decoded to fp16 through a 256-entry table in
+// v_mfma_f32_16x16x32), K in steps of 64 (32 for the 128 tile) through two
+// LDS buffers.  Each operand is fetched in one of three modes chosen by the
+// host from its strides: k-contiguous (16-byte row pieces, kept [row][k] in
+// LDS), row-contiguous (a transposed view: 16-byte pieces of 8 rows at one k,
+// kept [k][row] in LDS and read back through the transposing LDS read) or
+// scalar (any strides, element loads, the 64 tile only).  FP8 codes are decoded to fp16 through a 256-entry table in
 // LDS: every FP8 value of the five formats is exactly an fp16 value, so the
 // fp16 MFMA forms the same products the reference forms in fp32.
 //
@@ -151,7 +151,7 @@ TM_DEV void tile_epilogue(const DotParams& p, const f4_t (&acc)[FT][FT], int m0,
 // BT BK / 2048 pieces of 8 elements per thread (piece h: rows + 64 (h %
 // (BT / 64)), k + 32 (h / (BT / 64))), each one 16-byte (FP8: 8-byte) load:
 //   KC  row tid / 4, k 8 (tid % 4) .. +7
-//   RC  rows 8 (tid % 8) .. +7, k tid / 8   (scattered into LDS as 8 halves)
+//   RC  rows 8 (tid % 8) .. +7, k tid / 8
 // kept packed in registers.  Loads run two steps ahead (two register sets):
 // step kt + 2 is loaded while step kt multiplies from LDS and step kt + 1
 // goes from registers to the other LDS buffer.  Every load is
@@ -161,10 +161,12 @@ TM_DEV void tile_epilogue(const DotParams& p, const f4_t (&acc)[FT][FT], int m0,
 // an aligned chunk holding a valid element (never a page the operand does
 // not touch) and nothing writes its registers before the LDS store that
 // consumes it; that store zeroes the elements past the operand.
-// LDS: [row][BK k + 8 pad] halves, the 16-byte k chunk c of row r at
-// c ^ ((r / 16) % 4): the 16 rows of one operand read keep one chunk order
-// (each read touches every bank once) while the 8 row groups of one
-// scattered RC store land in distinct banks.
+// LDS, KC operands: [row][BK k + 8 pad] halves, the 16-byte k chunk c of
+// row r at c ^ ((r / 16) % 4), so the 16 rows of one MFMA operand read touch
+// every bank once.  RC operands: [k][BT rows + 16 pad] halves, each piece
+// stored whole at its k; an operand is read with two ds_read_b64_tr_b16 per
+// lane (rows r0 + 4 (j % 4) .. +3, j = lane % 16), which hand each lane the
+// 4 k values of one row.
 // Workgroups are taken in XCD order (dispatch i runs on XCD i % 8): when the
 // tile count is a multiple of 8, XCD x takes tiles x T / 8 .. (x + 1) T / 8 - 1,
 // rows of tiles that share their A rows in one L2.
