@@ -237,6 +237,53 @@ def test_dot_chain(dev, dt):
     assert (np.abs(c.cpu().numpy() - ref) <= bound).all()
 
 
+def _chain_check(c, ref, absPW):
+    """fp32 accumulation bound of both products; a 16-bit C adds its rounding
+    (half an ulp: 2^-11 fp16, 2^-8 bf16 relative)."""
+    got = c.double().cpu().numpy()
+    rel = {torch.float32: 0.0, torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8}[c.dtype]
+    bound = (1e-4 + rel) * np.abs(ref) + 2.0 ** -16 * absPW
+    err = np.abs(got - ref)
+    assert (err <= bound).all(), f"max err {err.max():.3e}, worst {(err / bound).max():.2f}"
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["row", "trans_a", "trans_b", "strided"])
+@pytest.mark.parametrize("batch,M,N,K,L", [(None, 50, 64, 80, 24), (3, 70, 200, 96, 130),
+                                           (3, 1100, 130, 40, 140)])
+@pytest.mark.parametrize("out", ["f32", "in"])
+def test_dot_chain_fused(dev, dt, layout, batch, M, N, K, L, out):
+    """chain-dot on the fused kernel (16-bit inputs, C apart from A, B and W):
+    ragged N and L (several 64-wide L tiles), batches, both C tile heights
+    (16 rows; 32 once those make a workgroup per CU: 3 x 35 x 3 tiles), W of
+    another dtype and layout, C in fp32 and in the input dtype."""
+    da, db, a, b = _views(M, N, K, dt, layout, seed=M + N + L, batch=batch)
+    wdt = torch.bfloat16 if dt == torch.float16 else torch.float32
+    w = _rand((N, L), 59, wdt)
+    dw = w.to(dev) if layout == "row" else w.t().contiguous().to(dev).t()
+    odt = torch.float32 if out == "f32" else dt
+    c = torch.empty(((batch,) if batch else ()) + (M, L), dtype=odt, device=dev)
+    tm.dot(da, db, c, "chain-dot", w=dw)
+    ref = oracle.dot(_np(a), _np(b), "chain-dot", W=_np(w))
+    absPW = (np.abs(_np(a)) @ np.abs(_np(b))) @ np.abs(_np(w))
+    _chain_check(c, ref.reshape(c.shape), absPW.reshape(c.shape))
+
+
+@pytest.mark.parametrize("fmt", FP8)
+def test_dot_chain_fused_fp8(dev, fmt):
+    """chain-dot with FP8 inputs (codes over each format's whole range) on the
+    fused kernel: P from the exactly decoded codes, unrounded, times an fp16 W."""
+    M, N, K, L = 96, 150, 72, 40
+    a = _fp8_codes((M, K), fmt, 81)
+    b = _fp8_codes((K, N), fmt, 83)
+    w = _rand((N, L), 85, torch.float16)
+    c = torch.empty(M, L, dtype=torch.float32, device=dev)
+    tm.dot(a.to(dev), b.t().contiguous().to(dev).t(), c, "chain-dot", w=w.to(dev), fp8_format=fmt)
+    av, bv = oracle.fp8_decode(a.numpy(), fmt), oracle.fp8_decode(b.numpy(), fmt)
+    ref = oracle.dot(av, bv, "chain-dot", W=_np(w))
+    _chain_check(c, ref.reshape(c.shape), (np.abs(av) @ np.abs(bv)) @ np.abs(_np(w)))
+
+
 def _fp8_codes(shape, fmt, seed):
     """Codes over the whole format, NaN / inf codes replaced by 0."""
     c = torch.randint(0, 256, shape, generator=_gen(seed), dtype=torch.uint8)

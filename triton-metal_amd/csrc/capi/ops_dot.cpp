@@ -1,7 +1,8 @@
 // Typed entry point for tl.dot in general form (strided / transposed
-// operands, a batch dimension, FP8 inputs, epilogues): dot_tile_{f16,bf16,f32}
-// (MFMA, the none / add-* epilogues) or dot_rows (softmax, chain-dot).  Also
-// the FP8 path of tm_matmul.
+// operands, a batch dimension, FP8 inputs, epilogues): the dot_tile kernels
+// (MFMA, the none / add-* epilogues, and the product before dot_softmax_rows),
+// dot_chain (chain-dot) or dot_rows (every epilogue, any case the others do
+// not take).  Also the FP8 path of tm_matmul.
 #include <cstring>
 
 #include "runtime.h"
@@ -137,6 +138,29 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
       if (rc) return rc;
       static Kernel ksm("dot_softmax_rows");
       return launch(ksm, dim3((unsigned)((long long)batch * M)), dim3(256), 0, stream, p);
+    }
+  }
+  // chain-dot with 16-bit or FP8 inputs, C sharing no memory with A, B or W:
+  // dot_chain keeps each P tile on chip and multiplies it into C at once
+  // (dot_rows re-reads all of B for every row).  32-row C tiles when they
+  // already make a workgroup per CU, else 16-row ones for twice as many.
+  if (chain && K > 0 && N > 0 && in_dtype != TM_DT_F32 && batch <= 65535) {
+    uintptr_t al, ah, bl, bh, wl, wh, cl, chh;
+    const int isz = elem_size(in_dtype);
+    extent(A, isz, batch, M, K, st[0], st[1], st[2], &al, &ah);
+    extent(B, isz, batch, K, N, st[3], st[4], st[5], &bl, &bh);
+    extent(W, elem_size(w_dtype), 1, N, L, 0, st[12], st[13], &wl, &wh);
+    extent(C, elem_size(out_dtype), batch, M, L, st[6], st[7], st[8], &cl, &chh);
+    const auto apart = [&](uintptr_t lo, uintptr_t hi) { return !(cl < hi && lo < chh); };
+    const long long tl = (L + 63) / 64;
+    const bool b32 = (long long)((M + 31) / 32) * tl * batch >= cu_count();
+    const long long groups = (long long)((M + (b32 ? 31 : 15)) / (b32 ? 32 : 16)) * tl;
+    if (apart(al, ah) && apart(bl, bh) && apart(wl, wh) && groups <= 0x7fffffffLL) {
+      char name[32];
+      snprintf(name, sizeof name, "dot_chain%d_%s", b32 ? 32 : 16,
+               is_fp8(in_dtype) ? "fp8" : in_dtype == TM_DT_BF16 ? "bf16" : "f16");
+      return launch(kernel_named(name), dim3((unsigned)groups, (unsigned)batch), dim3(256), 0,
+                    stream, p);
     }
   }
   // fp32 without an epilogue, one batch, k- and n-contiguous rows (B as [K, N]

@@ -32,7 +32,8 @@
 // every epilogue.  The softmax and chain-dot epilogues need the whole row of
 // the product, which the workgroup keeps in LDS (N <= 8192); it also serves
 // K = 0 and a bias read in place across rows.  With an fp32 output the
-// softmax takes the tile kernels and dot_softmax_rows instead.
+// softmax takes the tile kernels and dot_softmax_rows instead, and chain-dot
+// with 16-bit or FP8 inputs the fused dot_chain kernels.
 #include "common.h"
 
 enum { EPI_NONE = 0, EPI_ADD_MATRIX = 1, EPI_ADD_ROWS = 2, EPI_ADD_COLS = 3, EPI_SOFTMAX = 4,
@@ -667,6 +668,188 @@ extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) 
   sm = red[0] + red[1] + red[2] + red[3];
   for (int n = tid; n < p.N; n += 256) crow[(long long)n * p.sc_n] = expf(prow[n] - mx) / sm;
 }
+
+// ----------------------------------------------------------------------------
+// dot_chain{16,32}_<f16|bf16|fp8>: the chain-dot epilogue fused,
+//   C[b, m, l] = sum_n P[b, m, n] W[n, l],  P = A @ B in fp32, never rounded,
+// for 16-bit and FP8 inputs at any strides.  Grid (ceil(M / BM) * ceil(L /
+// 64), batch), block 256: each workgroup owns a BM x 64 tile of C and walks N
+// in chunks of 64.  For each chunk the P tile [BM][64] is formed over K in
+// steps of 32 on v_mfma_f32_16x16x32 (wave w: columns 16 w .. +15 of the
+// chunk, BM / 16 tiles of 16 rows; FP8 decoded exactly to fp16 through the
+// LDS table, as in dot_tile), written to LDS as fp32 and multiplied into the
+// C tile on v_mfma_f32_16x16x4_f32 (wave w: columns 16 w .. +15 of the C
+// tile) against the chunk's W [64][64] (any input dtype, as fp32).  Every
+// operand is read by element loads whose lane order follows its smaller
+// stride, at addresses clamped into the operand; the LDS store zeroes the
+// elements past it.  The loads of step s + 1 (and a chunk's W with its first
+// step) are issued before step s's MFMAs.
+// LDS, halves: A [BM][32 k + 8], B [64 n][32 k + 8] (16-byte operand reads at
+// an 80-byte row pitch); floats: P [BM][64 + 4] (the 16 rows x 4 k of one
+// read on 64 distinct banks), W [64 n][64 + 16].
+// ----------------------------------------------------------------------------
+namespace {
+template <bool BF16, bool FP8, int BM>
+__device__ __forceinline__ void dot_chain_body(const DotParams& p) {
+  constexpr int BN = 64, BK = 32, BL = 64, LDK = BK + 8, LDP = BN + 4, LDW = BL + 16;
+  constexpr int RI = BM / 16;        // MFMA row tiles per wave
+  constexpr int AE = BM * BK / 256;  // A elements per thread and step
+  constexpr int BE = BN * BK / 256;  // B elements per thread and step
+  constexpr int WE = BN * BL / 256;  // W elements per thread and chunk
+  __shared__ __align__(16) uint16_t As[BM * LDK];
+  __shared__ __align__(16) uint16_t Bs[BN * LDK];
+  __shared__ __align__(16) float Ps[BM * LDP];
+  __shared__ __align__(16) float Ws[BN * LDW];
+  __shared__ uint16_t lut[256];
+  using raw_t = typename std::conditional<FP8, uint8_t, uint16_t>::type;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, r16 = lane & 15;
+  const int tiles_l = (p.L + BL - 1) / BL;
+  const int m0 = (int)(blockIdx.x / tiles_l) * BM, l0 = (int)(blockIdx.x % tiles_l) * BL;
+  const int b = blockIdx.y;
+  if constexpr (FP8) lut[tid] = f32_to_f16_bits(fp8_to_f32((uint32_t)tid, p.in_dt));
+  const raw_t* Ab = (const raw_t*)p.A + (long long)b * p.sa_b;
+  const raw_t* Bb = (const raw_t*)p.B + (long long)b * p.sb_b;
+
+  // element e of a thread: A (row, k), B (n, k), W (n, l), the lanes along
+  // the operand's smaller stride
+  const bool a_kf = p.sa_k <= p.sa_m, b_kf = p.sb_k <= p.sb_n, w_lf = p.sw_l <= p.sw_n;
+  auto a_at = [&](int e, int& r, int& k) {
+    const int i = tid + 256 * e;
+    if (a_kf) { r = i / BK; k = i % BK; } else { r = i % BM; k = i / BM; }
+  };
+  auto b_at = [&](int e, int& n, int& k) {
+    const int i = tid + 256 * e;
+    if (b_kf) { n = i / BK; k = i % BK; } else { n = i % BN; k = i / BN; }
+  };
+  auto w_at = [&](int e, int& n, int& l) {
+    const int i = tid + 256 * e;
+    if (w_lf) { n = i / BL; l = i % BL; } else { n = i % BN; l = i / BN; }
+  };
+
+  const int ksteps = (p.K + BK - 1) / BK, nchunks = (p.N + BN - 1) / BN;
+  const int nsteps = ksteps * nchunks;
+  uint32_t ra[AE], rb[BE];
+  float rw[WE];
+  auto load_ab = [&](int s) {
+    const int c = s / ksteps, k0 = (s - c * ksteps) * BK, n0 = c * BN;
+#pragma unroll
+    for (int e = 0; e < AE; ++e) {
+      int r, k;
+      a_at(e, r, k);
+      ra[e] = Ab[(long long)min(m0 + r, p.M - 1) * p.sa_m + (long long)min(k0 + k, p.K - 1) * p.sa_k];
+    }
+#pragma unroll
+    for (int e = 0; e < BE; ++e) {
+      int n, k;
+      b_at(e, n, k);
+      rb[e] = Bb[(long long)min(n0 + n, p.N - 1) * p.sb_n + (long long)min(k0 + k, p.K - 1) * p.sb_k];
+    }
+  };
+  auto put_ab = [&](int s) {
+    const int c = s / ksteps, k0 = (s - c * ksteps) * BK, n0 = c * BN;
+#pragma unroll
+    for (int e = 0; e < AE; ++e) {
+      int r, k;
+      a_at(e, r, k);
+      const uint32_t v = FP8 ? (uint32_t)lut[ra[e]] : ra[e];
+      As[r * LDK + k] = (uint16_t)(m0 + r < p.M && k0 + k < p.K ? v : 0u);
+    }
+#pragma unroll
+    for (int e = 0; e < BE; ++e) {
+      int n, k;
+      b_at(e, n, k);
+      const uint32_t v = FP8 ? (uint32_t)lut[rb[e]] : rb[e];
+      Bs[n * LDK + k] = (uint16_t)(n0 + n < p.N && k0 + k < p.K ? v : 0u);
+    }
+  };
+  auto load_w = [&](int c) {
+    const int n0 = c * BN;
+#pragma unroll
+    for (int e = 0; e < WE; ++e) {
+      int n, l;
+      w_at(e, n, l);
+      const float v = load_elem(p.W, (long long)min(n0 + n, p.N - 1) * p.sw_n +
+                                         (long long)min(l0 + l, p.L - 1) * p.sw_l, p.w_dt);
+      rw[e] = n0 + n < p.N && l0 + l < p.L ? v : 0.0f;
+    }
+  };
+
+  f4_t accp[RI], accc[RI];
+#pragma unroll
+  for (int i = 0; i < RI; ++i) {
+    accp[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+    accc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  if constexpr (FP8) __syncthreads();  // the decode table
+  load_ab(0);
+  load_w(0);
+  put_ab(0);
+  __syncthreads();
+  for (int s = 0; s < nsteps; ++s) {
+    const int c = s / ksteps, ks = s - c * ksteps;
+    const bool last = ks == ksteps - 1;
+    if (s + 1 < nsteps) load_ab(s + 1);
+    if (ks == 0 && c > 0) load_w(c);
+    const u4_t bv = *(const u4_t*)(Bs + (16 * wave + r16) * LDK + 8 * q);
+#pragma unroll
+    for (int i = 0; i < RI; ++i) {
+      const u4_t av = *(const u4_t*)(As + (16 * i + r16) * LDK + 8 * q);
+      accp[i] = mfma16<BF16 && !FP8>(av, bv, accp[i]);
+    }
+    __syncthreads();
+    if (s + 1 < nsteps) put_ab(s + 1);
+    if (last) {
+#pragma unroll
+      for (int i = 0; i < RI; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) Ps[(16 * i + 4 * q + e) * LDP + 16 * wave + r16] = accp[i][e];
+        accp[i] = f4_t{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int e = 0; e < WE; ++e) {
+        int n, l;
+        w_at(e, n, l);
+        Ws[n * LDW + l] = rw[e];
+      }
+    }
+    __syncthreads();
+    if (last) {
+#pragma unroll 4
+      for (int kk = 0; kk < BN; kk += 4) {
+        const float wv = Ws[(kk + q) * LDW + 16 * wave + r16];
+#pragma unroll
+        for (int i = 0; i < RI; ++i)
+          accc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ps[(16 * i + r16) * LDP + kk + q], wv,
+                                                        accc[i], 0, 0, 0);
+      }
+    }
+  }
+
+  const long long cb = (long long)b * p.sc_b;
+  const int l = l0 + 16 * wave + r16;
+  if (l >= p.L) return;
+#pragma unroll
+  for (int i = 0; i < RI; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = m0 + 16 * i + 4 * q + e;
+      if (m < p.M) store_elem(p.C, cb + (long long)m * p.sc_m + (long long)l * p.sc_n, p.out_dt, accc[i][e]);
+    }
+}
+}  // namespace
+
+#define TM_DOT_CHAIN(NAME, BF, F8, BM)                                            \
+  extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {         \
+    dot_chain_body<BF, F8, BM>(p);                                              \
+  }
+TM_DOT_CHAIN(dot_chain16_f16, false, false, 16)
+TM_DOT_CHAIN(dot_chain16_bf16, true, false, 16)
+TM_DOT_CHAIN(dot_chain16_fp8, false, true, 16)
+TM_DOT_CHAIN(dot_chain32_f16, false, false, 32)
+TM_DOT_CHAIN(dot_chain32_bf16, true, false, 32)
+TM_DOT_CHAIN(dot_chain32_fp8, false, true, 32)
 
 // ----------------------------------------------------------------------------
 // dot_rows: grid batch * M, block 256.  Columns in groups of 1024 (4 per
