@@ -95,6 +95,15 @@ TM_DEV float load_elem(const void* p, long long i, int dt) {
 
 TM_DEV void store_elem(void* p, long long i, int dt, float v) { store_as_f32_rt(p, i, dt, v); }
 
+// The element at byte `byte` (0..3) of an aligned 4-byte word, as float.
+TM_DEV float word_elem(uint32_t w, int byte, int dt) {
+  if (dt == TM_DT_F32) return __uint_as_float(w);
+  const uint16_t h = (uint16_t)(w >> (8 * (byte & 2)));
+  if (dt == TM_DT_F16) return f16_bits_to_f32(h);
+  if (dt == TM_DT_BF16) return bf16_bits_to_f32(h);
+  return fp8_to_f32((w >> (8 * byte)) & 0xFFu, dt);
+}
+
 }  // namespace
 
 // Keep the first n elements of a piece (the rest zero): 16-bit elements in 4
@@ -681,12 +690,16 @@ extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) 
 // C tile on v_mfma_f32_16x16x4_f32 (wave w: columns 16 w .. +15 of the C
 // tile) against the chunk's W [64][64] (any input dtype, as fp32).  Every
 // operand is read by element loads whose lane order follows its smaller
-// stride, at addresses clamped into the operand; the LDS store zeroes the
-// elements past it.  The loads of step s + 1 (and a chunk's W with its first
-// step) are issued before step s's MFMAs.
+// stride, at addresses clamped into the operand (W: the aligned 4-byte word
+// holding the element, decoded at the LDS store); the LDS store zeroes the
+// elements past the operand.  Loads run two steps ahead in two register sets,
+// since a step holds few MFMAs; every step loads its chunk's W (stored to LDS
+// with the chunk's last k step), so that each step issues the same loads and
+// the waits for the older set stay exact, and the stores mask with integer
+// ANDs rather than selects, which the compiler turns into branches.
 // LDS, halves: A [BM][32 k + 8], B [64 n][32 k + 8] (16-byte operand reads at
 // an 80-byte row pitch); floats: P [BM][64 + 4] (the 16 rows x 4 k of one
-// read on 64 distinct banks), W [64 n][64 + 16].
+// read on 64 distinct banks), W [2 chunks][64 n][64 + 16].
 // ----------------------------------------------------------------------------
 namespace {
 template <bool BF16, bool FP8, int BM>
@@ -699,7 +712,7 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
   __shared__ __align__(16) uint16_t As[BM * LDK];
   __shared__ __align__(16) uint16_t Bs[BN * LDK];
   __shared__ __align__(16) float Ps[BM * LDP];
-  __shared__ __align__(16) float Ws[BN * LDW];
+  __shared__ __align__(16) float Ws[2][BN * LDW];
   __shared__ uint16_t lut[256];
   using raw_t = typename std::conditional<FP8, uint8_t, uint16_t>::type;
 
@@ -730,9 +743,23 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
 
   const int ksteps = (p.K + BK - 1) / BK, nchunks = (p.N + BN - 1) / BN;
   const int nsteps = ksteps * nchunks;
-  uint32_t ra[AE], rb[BE];
-  float rw[WE];
-  auto load_ab = [&](int s) {
+  // step s: k step s % ksteps of chunk s / ksteps
+  auto is_last = [&](int s) { return s % ksteps == ksteps - 1; };
+  // W element (n, l) of chunk c: its byte address.  The aligned 4-byte word
+  // holding it is loaded (no dtype branch between a load and its use, which
+  // would wait for the load there) and decoded when stored to LDS.
+  const int wsz = p.w_dt == TM_DT_F32 ? 4 : p.w_dt == TM_DT_F16 || p.w_dt == TM_DT_BF16 ? 2 : 1;
+  auto w_addr = [&](int c, int n, int l) -> uintptr_t {
+    return (uintptr_t)p.W + (uintptr_t)(((long long)min(c * BN + n, p.N - 1) * p.sw_n +
+                                         (long long)min(l0 + l, p.L - 1) * p.sw_l) * wsz);
+  };
+  // its offset in the 4-byte word (the address's low bits, in 32 bits)
+  auto w_byte = [&](int c, int n, int l) -> int {
+    const uint32_t i = (uint32_t)min(c * BN + n, p.N - 1) * (uint32_t)p.sw_n +
+                       (uint32_t)min(l0 + l, p.L - 1) * (uint32_t)p.sw_l;
+    return (int)((i * (uint32_t)wsz + (uint32_t)(uintptr_t)p.W) & 3u);
+  };
+  auto load_step = [&](uint32_t* ra, uint32_t* rb, uint32_t* rw, int s) {
     const int c = s / ksteps, k0 = (s - c * ksteps) * BK, n0 = c * BN;
 #pragma unroll
     for (int e = 0; e < AE; ++e) {
@@ -746,33 +773,54 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
       b_at(e, n, k);
       rb[e] = Bb[(long long)min(n0 + n, p.N - 1) * p.sb_n + (long long)min(k0 + k, p.K - 1) * p.sb_k];
     }
+    {
+#pragma unroll
+      for (int e = 0; e < WE; ++e) {
+        int n, l;
+        w_at(e, n, l);
+        rw[e] = *(const uint32_t*)(w_addr(c, n, l) & ~(uintptr_t)3);
+      }
+    }
   };
-  auto put_ab = [&](int s) {
+  auto put_step = [&](const uint32_t* ra, const uint32_t* rb, const uint32_t* rw, int s) {
     const int c = s / ksteps, k0 = (s - c * ksteps) * BK, n0 = c * BN;
 #pragma unroll
     for (int e = 0; e < AE; ++e) {
       int r, k;
       a_at(e, r, k);
       const uint32_t v = FP8 ? (uint32_t)lut[ra[e]] : ra[e];
-      As[r * LDK + k] = (uint16_t)(m0 + r < p.M && k0 + k < p.K ? v : 0u);
+      As[r * LDK + k] = (uint16_t)(v & (0u - (uint32_t)(m0 + r < p.M && k0 + k < p.K)));
     }
 #pragma unroll
     for (int e = 0; e < BE; ++e) {
       int n, k;
       b_at(e, n, k);
       const uint32_t v = FP8 ? (uint32_t)lut[rb[e]] : rb[e];
-      Bs[n * LDK + k] = (uint16_t)(n0 + n < p.N && k0 + k < p.K ? v : 0u);
+      Bs[n * LDK + k] = (uint16_t)(v & (0u - (uint32_t)(n0 + n < p.N && k0 + k < p.K)));
     }
-  };
-  auto load_w = [&](int c) {
-    const int n0 = c * BN;
+    if (is_last(s)) {
+      float* ws = Ws[c & 1];
+      // one dtype branch around the whole chunk, so the loop is straight-line
+      auto put_w = [&](auto dtc) {
+        constexpr int DT = decltype(dtc)::value;
 #pragma unroll
-    for (int e = 0; e < WE; ++e) {
-      int n, l;
-      w_at(e, n, l);
-      const float v = load_elem(p.W, (long long)min(n0 + n, p.N - 1) * p.sw_n +
-                                         (long long)min(l0 + l, p.L - 1) * p.sw_l, p.w_dt);
-      rw[e] = n0 + n < p.N && l0 + l < p.L ? v : 0.0f;
+        for (int e = 0; e < WE; ++e) {
+          int n, l;
+          w_at(e, n, l);
+          const int byte = w_byte(c, n, l);
+          float v;
+          if constexpr (DT == TM_DT_F32) v = __uint_as_float(rw[e]);
+          else if constexpr (DT == TM_DT_F16) v = f16_bits_to_f32((uint16_t)(rw[e] >> (8 * (byte & 2))));
+          else if constexpr (DT == TM_DT_BF16) v = bf16_bits_to_f32((uint16_t)(rw[e] >> (8 * (byte & 2))));
+          else v = word_elem(rw[e], byte, p.w_dt);
+          const uint32_t keep = 0u - (uint32_t)(n0 + n < p.N && l0 + l < p.L);
+          ws[n * LDW + l] = __uint_as_float(__float_as_uint(v) & keep);
+        }
+      };
+      if (p.w_dt == TM_DT_F16) put_w(std::integral_constant<int, TM_DT_F16>());
+      else if (p.w_dt == TM_DT_BF16) put_w(std::integral_constant<int, TM_DT_BF16>());
+      else if (p.w_dt == TM_DT_F32) put_w(std::integral_constant<int, TM_DT_F32>());
+      else put_w(std::integral_constant<int, -1>());
     }
   };
 
@@ -782,16 +830,14 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
     accp[i] = f4_t{0.f, 0.f, 0.f, 0.f};
     accc[i] = f4_t{0.f, 0.f, 0.f, 0.f};
   }
-  if constexpr (FP8) __syncthreads();  // the decode table
-  load_ab(0);
-  load_w(0);
-  put_ab(0);
-  __syncthreads();
-  for (int s = 0; s < nsteps; ++s) {
-    const int c = s / ksteps, ks = s - c * ksteps;
-    const bool last = ks == ksteps - 1;
-    if (s + 1 < nsteps) load_ab(s + 1);
-    if (ks == 0 && c > 0) load_w(c);
+  // step s multiplies from LDS while step s + 1 goes from registers to LDS
+  // (after the barrier) and step s + 2 is loaded into the registers step s
+  // came through.  P goes to LDS after the chunk's last k step; W has two
+  // LDS buffers, as chunk c + 1's is stored before chunk c's is read.
+  auto step = [&](int s, uint32_t* ra_n, uint32_t* rb_n, uint32_t* rw_n, const uint32_t* ra_p,
+                  const uint32_t* rb_p, const uint32_t* rw_p) {
+    const bool last = is_last(s);
+    load_step(ra_n, rb_n, rw_n, min(s + 2, nsteps - 1));
     const u4_t bv = *(const u4_t*)(Bs + (16 * wave + r16) * LDK + 8 * q);
 #pragma unroll
     for (int i = 0; i < RI; ++i) {
@@ -799,7 +845,7 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
       accp[i] = mfma16<BF16 && !FP8>(av, bv, accp[i]);
     }
     __syncthreads();
-    if (s + 1 < nsteps) put_ab(s + 1);
+    if (s + 1 < nsteps) put_step(ra_p, rb_p, rw_p, s + 1);
     if (last) {
 #pragma unroll
       for (int i = 0; i < RI; ++i) {
@@ -807,24 +853,29 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
         for (int e = 0; e < 4; ++e) Ps[(16 * i + 4 * q + e) * LDP + 16 * wave + r16] = accp[i][e];
         accp[i] = f4_t{0.f, 0.f, 0.f, 0.f};
       }
-#pragma unroll
-      for (int e = 0; e < WE; ++e) {
-        int n, l;
-        w_at(e, n, l);
-        Ws[n * LDW + l] = rw[e];
-      }
     }
     __syncthreads();
     if (last) {
+      const float* ws = Ws[(s / ksteps) & 1];
 #pragma unroll 4
       for (int kk = 0; kk < BN; kk += 4) {
-        const float wv = Ws[(kk + q) * LDW + 16 * wave + r16];
+        const float wv = ws[(kk + q) * LDW + 16 * wave + r16];
 #pragma unroll
         for (int i = 0; i < RI; ++i)
           accc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ps[(16 * i + r16) * LDP + kk + q], wv,
                                                         accc[i], 0, 0, 0);
       }
     }
+  };
+  uint32_t ra0[AE], rb0[BE], rw0[WE], ra1[AE], rb1[BE], rw1[WE];
+  if constexpr (FP8) __syncthreads();  // the decode table
+  load_step(ra0, rb0, rw0, 0);
+  load_step(ra1, rb1, rw1, min(1, nsteps - 1));
+  put_step(ra0, rb0, rw0, 0);
+  __syncthreads();
+  for (int s = 0; s < nsteps; s += 2) {
+    step(s, ra0, rb0, rw0, ra1, rb1, rw1);
+    if (s + 1 < nsteps) step(s + 1, ra1, rb1, rw1, ra0, rb0, rw0);
   }
 
   const long long cb = (long long)b * p.sc_b;
