@@ -684,7 +684,7 @@ extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) 
 // for 16-bit and FP8 inputs at any strides.  Grid (ceil(M / BM) * ceil(L /
 // 64), batch), block 256: each workgroup owns a BM x 64 tile of C and walks N
 // in chunks of 64.  For each chunk the P tile [BM][64] is formed over K in
-// steps of 32 on v_mfma_f32_16x16x32 (wave w: columns 16 w .. +15 of the
+// steps of 64 on v_mfma_f32_16x16x32 (wave w: columns 16 w .. +15 of the
 // chunk, BM / 16 tiles of 16 rows; FP8 decoded exactly to fp16 through the
 // LDS table, as in dot_tile), written to LDS as fp32 and multiplied into the
 // C tile on v_mfma_f32_16x16x4_f32 (wave w: columns 16 w .. +15 of the C
@@ -697,14 +697,14 @@ extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) 
 // with the chunk's last k step), so that each step issues the same loads and
 // the waits for the older set stay exact, and the stores mask with integer
 // ANDs rather than selects, which the compiler turns into branches.
-// LDS, halves: A [BM][32 k + 8], B [64 n][32 k + 8] (16-byte operand reads at
-// an 80-byte row pitch); floats: P [BM][64 + 4] (the 16 rows x 4 k of one
+// LDS, halves: A [BM][64 k + 8], B [64 n][64 k + 8] (16-byte operand reads at
+// a 144-byte row pitch: the 16 rows of one read start on distinct 4-bank groups); floats: P [BM][64 + 4] (the 16 rows x 4 k of one
 // read on 64 distinct banks), W [2 chunks][64 n][64 + 16].
 // ----------------------------------------------------------------------------
 namespace {
 template <bool BF16, bool FP8, int BM>
 __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
-  constexpr int BN = 64, BK = 32, BL = 64, LDK = BK + 8, LDP = BN + 4, LDW = BL + 16;
+  constexpr int BN = 64, BK = 64, BL = 64, LDK = BK + 8, LDP = BN + 4, LDW = BL + 16;
   constexpr int RI = BM / 16;        // MFMA row tiles per wave
   constexpr int AE = BM * BK / 256;  // A elements per thread and step
   constexpr int BE = BN * BK / 256;  // B elements per thread and step
@@ -838,11 +838,14 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
                   const uint32_t* rb_p, const uint32_t* rw_p) {
     const bool last = is_last(s);
     load_step(ra_n, rb_n, rw_n, min(s + 2, nsteps - 1));
-    const u4_t bv = *(const u4_t*)(Bs + (16 * wave + r16) * LDK + 8 * q);
 #pragma unroll
-    for (int i = 0; i < RI; ++i) {
-      const u4_t av = *(const u4_t*)(As + (16 * i + r16) * LDK + 8 * q);
-      accp[i] = mfma16<BF16 && !FP8>(av, bv, accp[i]);
+    for (int kb = 0; kb < BK; kb += 32) {
+      const u4_t bv = *(const u4_t*)(Bs + (16 * wave + r16) * LDK + kb + 8 * q);
+#pragma unroll
+      for (int i = 0; i < RI; ++i) {
+        const u4_t av = *(const u4_t*)(As + (16 * i + r16) * LDK + kb + 8 * q);
+        accp[i] = mfma16<BF16 && !FP8>(av, bv, accp[i]);
+      }
     }
     __syncthreads();
     if (s + 1 < nsteps) put_step(ra_p, rb_p, rw_p, s + 1);
