@@ -115,7 +115,9 @@ def dense(dev, M=512, N=512, K=512):
 def dot_general(dev, layout, dt_name, M, N, K, batch=None, epilogue="none"):
     """tm_dot (the strided tl.dot template) on layouts the dense kernels do not
     take: "colmajor_a" (A stored [K, M]), "batched" (row-major [batch, M, K] @
-    [batch, K, N]) or "trans_b" with an add-matrix epilogue."""
+    [batch, K, N]) or "trans_b" with an add-matrix epilogue; "row" with the
+    chain-dot epilogue: (A @ B) @ W, W [N, L = K] in the input dtype, C [M, L]
+    in fp32."""
     import torch
     import triton_metal_amd as tm
     dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt_name]
@@ -127,13 +129,18 @@ def dot_general(dev, layout, dt_name, M, N, K, batch=None, epilogue="none"):
         A = A.transpose(-1, -2).contiguous().transpose(-1, -2)
     elif layout == "trans_b":
         B = B.transpose(-1, -2).contiguous().transpose(-1, -2)
-    C = torch.empty(*bs, M, N, device=dev, dtype=dt)
-    Z = torch.randn(*bs, M, N, device=dev, generator=g).to(dt) if epilogue != "none" else None
-    launches = [tm.plan_dot(A, B, C, epilogue, z=Z)]
+    chain = epilogue == "chain-dot"
+    L = K
+    C = torch.empty(*bs, M, L if chain else N, device=dev,
+                    dtype=torch.float32 if chain else dt)
+    Z = (torch.randn(*bs, M, N, device=dev, generator=g).to(dt)
+         if epilogue not in ("none", "chain-dot") else None)
+    W = torch.randn(N, L, device=dev, generator=g).to(dt) if chain else None
+    launches = [tm.plan_dot(A, B, C, epilogue, z=Z, w=W)]
     nb = batch or 1
     esz = A.element_size()
-    w = dict(launches=launches, keep=(A, B, C, Z), bytes=esz * nb * (M * K + K * N + M * N),
-             flops=2 * nb * M * N * K, bound="mfma", dtype=dt_name,
+    w = dict(launches=launches, keep=(A, B, C, Z, W), bytes=esz * nb * (M * K + K * N + M * N),
+             flops=2 * nb * M * N * (K + L if chain else K), bound="mfma", dtype=dt_name,
              config={"workload": f"dot_{dt_name}_{layout}", "M": M, "N": N, "K": K,
                      "batch": batch, "epilogue": epilogue})
     if dt == torch.float32:
@@ -380,6 +387,10 @@ EXTRA = {"hbm_copy": hbm_copy,
          "dot_fp16_colmajor_a_4096": lambda d: dot_general(d, "colmajor_a", "fp16", 4096, 4096, 4096),
          "dot_bf16_batched_8x1024": lambda d: dot_general(d, "batched", "bf16", 1024, 1024, 1024,
                                                           batch=8),
+         "dot_fp16_chain_1024": lambda d: dot_general(d, "row", "fp16", 1024, 1024, 64,
+                                                      epilogue="chain-dot"),
+         "dot_fp16_chain_4096x1024x128": lambda d: dot_general(d, "row", "fp16", 4096, 1024, 128,
+                                                               epilogue="chain-dot"),
          "dot_fp16_addmatrix_2048": lambda d: dot_general(d, "trans_b", "fp16", 2048, 2048, 2048,
                                                           epilogue="add-matrix"),
          "dot_fp32_colmajor_a_4096": lambda d: dot_general(d, "colmajor_a", "fp32", 4096, 4096, 4096),
