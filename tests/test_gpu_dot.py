@@ -247,13 +247,13 @@ def _chain_check(c, ref, absPW):
     assert (err <= bound).all(), f"max err {err.max():.3e}, worst {(err / bound).max():.2f}"
 
 
-@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("layout", ["row", "trans_a", "trans_b", "strided"])
 @pytest.mark.parametrize("batch,M,N,K,L", [(None, 50, 64, 80, 24), (3, 70, 200, 96, 130),
                                            (3, 1100, 130, 40, 140)])
 @pytest.mark.parametrize("out", ["f32", "in"])
 def test_dot_chain_fused(dev, dt, layout, batch, M, N, K, L, out):
-    """chain-dot on the fused kernel (16-bit inputs, C apart from A, B and W):
+    """chain-dot on the fused kernel (C apart from A, B and W):
     ragged N and L (several 64-wide L tiles), batches, both C tile heights
     (16 rows; 32 once those make a workgroup per CU: 3 x 35 x 3 tiles), W of
     another dtype and layout, C in fp32 and in the input dtype."""

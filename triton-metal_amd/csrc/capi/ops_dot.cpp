@@ -140,11 +140,11 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
       return launch(ksm, dim3((unsigned)((long long)batch * M)), dim3(256), 0, stream, p);
     }
   }
-  // chain-dot with 16-bit or FP8 inputs, C sharing no memory with A, B or W:
+  // chain-dot with C sharing no memory with A, B or W:
   // dot_chain keeps each P tile on chip and multiplies it into C at once
   // (dot_rows re-reads all of B for every row).  32-row C tiles when they
   // already make a workgroup per CU, else 16-row ones for twice as many.
-  if (chain && K > 0 && N > 0 && in_dtype != TM_DT_F32 && batch <= 65535) {
+  if (chain && K > 0 && N > 0 && batch <= 65535) {
     uintptr_t al, ah, bl, bh, wl, wh, cl, chh;
     const int isz = elem_size(in_dtype);
     extent(A, isz, batch, M, K, st[0], st[1], st[2], &al, &ah);
@@ -158,7 +158,8 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
     if (apart(al, ah) && apart(bl, bh) && apart(wl, wh) && groups <= 0x7fffffffLL) {
       char name[32];
       snprintf(name, sizeof name, "dot_chain%d_%s", b32 ? 32 : 16,
-               is_fp8(in_dtype) ? "fp8" : in_dtype == TM_DT_BF16 ? "bf16" : "f16");
+               is_fp8(in_dtype) ? "fp8" : in_dtype == TM_DT_BF16 ? "bf16"
+               : in_dtype == TM_DT_F32 ? "f32" : "f16");
       return launch(kernel_named(name), dim3((unsigned)groups, (unsigned)batch), dim3(256), 0,
                     stream, p);
     }

@@ -33,7 +33,7 @@
 // the product, which the workgroup keeps in LDS (N <= 8192); it also serves
 // K = 0 and a bias read in place across rows.  With an fp32 output the
 // softmax takes the tile kernels and dot_softmax_rows instead, and chain-dot
-// with 16-bit or FP8 inputs the fused dot_chain kernels.
+// with C apart from its operands the fused dot_chain kernels.
 #include "common.h"
 
 enum { EPI_NONE = 0, EPI_ADD_MATRIX = 1, EPI_ADD_ROWS = 2, EPI_ADD_COLS = 3, EPI_SOFTMAX = 4,
@@ -679,42 +679,48 @@ extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) 
 }
 
 // ----------------------------------------------------------------------------
-// dot_chain{16,32}_<f16|bf16|fp8>: the chain-dot epilogue fused,
+// dot_chain{16,32}_<f16|bf16|fp8|f32>: the chain-dot epilogue fused,
 //   C[b, m, l] = sum_n P[b, m, n] W[n, l],  P = A @ B in fp32, never rounded,
-// for 16-bit and FP8 inputs at any strides.  Grid (ceil(M / BM) * ceil(L /
-// 64), batch), block 256: each workgroup owns a BM x 64 tile of C and walks N
-// in chunks of 64.  For each chunk the P tile [BM][64] is formed over K in
-// steps of 64 on v_mfma_f32_16x16x32 (wave w: columns 16 w .. +15 of the
-// chunk, BM / 16 tiles of 16 rows; FP8 decoded exactly to fp16 through the
-// LDS table, as in dot_tile), written to LDS as fp32 and multiplied into the
-// C tile on v_mfma_f32_16x16x4_f32 (wave w: columns 16 w .. +15 of the C
-// tile) against the chunk's W [64][64] (any input dtype, as fp32).  Every
-// operand is read by element loads whose lane order follows its smaller
-// stride, at addresses clamped into the operand (W: the aligned 4-byte word
-// holding the element, decoded at the LDS store); the LDS store zeroes the
-// elements past the operand.  Loads run two steps ahead in two register sets,
-// since a step holds few MFMAs; every step loads its chunk's W (stored to LDS
-// with the chunk's last k step), so that each step issues the same loads and
-// the waits for the older set stay exact, and the stores mask with integer
-// ANDs rather than selects, which the compiler turns into branches.
-// LDS, halves: A [BM][64 k + 8], B [64 n][64 k + 8] (16-byte operand reads at
-// a 144-byte row pitch: the 16 rows of one read start on distinct 4-bank groups); floats: P [BM][64 + 4] (the 16 rows x 4 k of one
+// at any strides.  Grid (ceil(M / BM) * ceil(L / 64), batch), block 256:
+// each workgroup owns a BM x 64 tile of C and walks N in chunks of 64.  For
+// each chunk the P tile [BM][64] is formed over K in steps of 64 (wave w:
+// columns 16 w .. +15 of the chunk, BM / 16 tiles of 16 rows) on
+// v_mfma_f32_16x16x32 (FP8 decoded exactly to fp16 through the LDS table, as
+// in dot_tile) or, for fp32 inputs, v_mfma_f32_16x16x4_f32; written to LDS as
+// fp32 and multiplied into the C tile on v_mfma_f32_16x16x4_f32 (wave w:
+// columns 16 w .. +15 of the C tile) against the chunk's W [64][64] (any
+// input dtype, as fp32).  Every operand is read by element loads whose lane
+// order follows its smaller stride, at addresses clamped into the operand
+// (W: the aligned 4-byte word holding the element, decoded at the LDS
+// store); the LDS store zeroes the elements past the operand.  Loads run two
+// steps ahead in two register sets, since a step holds few MFMAs; every step
+// issues the same loads (its chunk's W included, stored to LDS with the
+// chunk's last k step; the last step's loads again at the end), since a load
+// under a branch makes the compiler wait for every load at the next use of an
+// older one, and the stores mask with integer ANDs rather than selects, which
+// the compiler turns into branches.
+// LDS: A [BM][64 k + 8], B [64 n][64 k + 8] halves (16-byte operand reads at
+// a 144-byte row pitch: the 16 rows of one read start on distinct 4-bank
+// groups; fp32 inputs: + 4 floats, the 16 rows x 4 k of one read on 64
+// distinct banks); floats: P [BM][64 + 4] (the 16 rows x 4 k of one
 // read on 64 distinct banks), W [2 chunks][64 n][64 + 16].
 // ----------------------------------------------------------------------------
 namespace {
-template <bool BF16, bool FP8, int BM>
+template <bool BF16, bool FP8, int BM, bool F32 = false>
 __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
-  constexpr int BN = 64, BK = 64, BL = 64, LDK = BK + 8, LDP = BN + 4, LDW = BL + 16;
+  constexpr int BN = 64, BK = 64, BL = 64, LDK = BK + (F32 ? 4 : 8), LDP = BN + 4, LDW = BL + 16;
   constexpr int RI = BM / 16;        // MFMA row tiles per wave
   constexpr int AE = BM * BK / 256;  // A elements per thread and step
   constexpr int BE = BN * BK / 256;  // B elements per thread and step
   constexpr int WE = BN * BL / 256;  // W elements per thread and chunk
-  __shared__ __align__(16) uint16_t As[BM * LDK];
-  __shared__ __align__(16) uint16_t Bs[BN * LDK];
+  using lds_t = typename std::conditional<F32, uint32_t, uint16_t>::type;
+  __shared__ __align__(16) lds_t As[BM * LDK];
+  __shared__ __align__(16) lds_t Bs[BN * LDK];
   __shared__ __align__(16) float Ps[BM * LDP];
   __shared__ __align__(16) float Ws[2][BN * LDW];
   __shared__ uint16_t lut[256];
-  using raw_t = typename std::conditional<FP8, uint8_t, uint16_t>::type;
+  using raw_t = typename std::conditional<F32, uint32_t,
+                typename std::conditional<FP8, uint8_t, uint16_t>::type>::type;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
@@ -789,14 +795,14 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
       int r, k;
       a_at(e, r, k);
       const uint32_t v = FP8 ? (uint32_t)lut[ra[e]] : ra[e];
-      As[r * LDK + k] = (uint16_t)(v & (0u - (uint32_t)(m0 + r < p.M && k0 + k < p.K)));
+      As[r * LDK + k] = (lds_t)(v & (0u - (uint32_t)(m0 + r < p.M && k0 + k < p.K)));
     }
 #pragma unroll
     for (int e = 0; e < BE; ++e) {
       int n, k;
       b_at(e, n, k);
       const uint32_t v = FP8 ? (uint32_t)lut[rb[e]] : rb[e];
-      Bs[n * LDK + k] = (uint16_t)(v & (0u - (uint32_t)(n0 + n < p.N && k0 + k < p.K)));
+      Bs[n * LDK + k] = (lds_t)(v & (0u - (uint32_t)(n0 + n < p.N && k0 + k < p.K)));
     }
     if (is_last(s)) {
       float* ws = Ws[c & 1];
@@ -838,13 +844,25 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
                   const uint32_t* rb_p, const uint32_t* rw_p) {
     const bool last = is_last(s);
     load_step(ra_n, rb_n, rw_n, min(s + 2, nsteps - 1));
+    if constexpr (F32) {
+      // fp32 operands: v_mfma_f32_16x16x4_f32, lane l row l % 16, k kk + l / 16
 #pragma unroll
-    for (int kb = 0; kb < BK; kb += 32) {
-      const u4_t bv = *(const u4_t*)(Bs + (16 * wave + r16) * LDK + kb + 8 * q);
+      for (int kk = 0; kk < BK; kk += 4) {
+        const float bv = __uint_as_float(Bs[(16 * wave + r16) * LDK + kk + q]);
 #pragma unroll
-      for (int i = 0; i < RI; ++i) {
-        const u4_t av = *(const u4_t*)(As + (16 * i + r16) * LDK + kb + 8 * q);
-        accp[i] = mfma16<BF16 && !FP8>(av, bv, accp[i]);
+        for (int i = 0; i < RI; ++i)
+          accp[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              __uint_as_float(As[(16 * i + r16) * LDK + kk + q]), bv, accp[i], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < BK; kb += 32) {
+        const u4_t bv = *(const u4_t*)(Bs + (16 * wave + r16) * LDK + kb + 8 * q);
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+          const u4_t av = *(const u4_t*)(As + (16 * i + r16) * LDK + kb + 8 * q);
+          accp[i] = mfma16<BF16 && !FP8>(av, bv, accp[i]);
+        }
       }
     }
     __syncthreads();
@@ -894,16 +912,18 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
 }
 }  // namespace
 
-#define TM_DOT_CHAIN(NAME, BF, F8, BM)                                            \
+#define TM_DOT_CHAIN(NAME, BF, F8, BM, F32)                                       \
   extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {         \
-    dot_chain_body<BF, F8, BM>(p);                                              \
+    dot_chain_body<BF, F8, BM, F32>(p);                                         \
   }
-TM_DOT_CHAIN(dot_chain16_f16, false, false, 16)
-TM_DOT_CHAIN(dot_chain16_bf16, true, false, 16)
-TM_DOT_CHAIN(dot_chain16_fp8, false, true, 16)
-TM_DOT_CHAIN(dot_chain32_f16, false, false, 32)
-TM_DOT_CHAIN(dot_chain32_bf16, true, false, 32)
-TM_DOT_CHAIN(dot_chain32_fp8, false, true, 32)
+TM_DOT_CHAIN(dot_chain16_f16, false, false, 16, false)
+TM_DOT_CHAIN(dot_chain16_bf16, true, false, 16, false)
+TM_DOT_CHAIN(dot_chain16_fp8, false, true, 16, false)
+TM_DOT_CHAIN(dot_chain16_f32, false, false, 16, true)
+TM_DOT_CHAIN(dot_chain32_f16, false, false, 32, false)
+TM_DOT_CHAIN(dot_chain32_bf16, true, false, 32, false)
+TM_DOT_CHAIN(dot_chain32_fp8, false, true, 32, false)
+TM_DOT_CHAIN(dot_chain32_f32, false, false, 32, true)
 
 // ----------------------------------------------------------------------------
 // dot_rows: grid batch * M, block 256.  Columns in groups of 1024 (4 per
