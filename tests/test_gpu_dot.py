@@ -211,8 +211,8 @@ def test_dot_softmax(dev, dt, N):
 @pytest.mark.parametrize("out", [torch.float32, torch.float16])
 def test_dot_softmax_batched(dev, layout, out):
     """Batched softmax: an fp32 output takes the tile kernels and the in-place
-    row softmax (dot_softmax_rows), a 16-bit one dot_rows; both against the
-    softmax of the fp64 product."""
+    row softmax (dot_softmax_rows), a 16-bit one dot_softmax16; both against
+    the softmax of the fp64 product."""
     B, M, N, K = 3, 70, 300, 96
     da, db, a, b = _views(M, N, K, torch.bfloat16, layout, seed=47, batch=B)
     c = torch.empty(B, M, N, dtype=out, device=dev)
@@ -222,6 +222,25 @@ def test_dot_softmax_batched(dev, layout, out):
         np.testing.assert_allclose(c.cpu().numpy(), ref, atol=1e-6, rtol=1e-4)
     else:
         np.testing.assert_allclose(c.float().cpu().numpy(), ref, atol=1e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("N", [40, 700, 2048, 2049])
+@pytest.mark.parametrize("out", [torch.float16, torch.bfloat16])
+def test_dot_softmax_16bit_output(dev, dt, N, out):
+    """softmax into a 16-bit C: rows of N <= 2048 on dot_softmax16 (16 whole
+    fp32 product rows on chip), N = 2049 on dot_rows; against the softmax of
+    the fp64 product, rounded once (half an ulp relative; fp16 subnormals
+    absolute)."""
+    B, M, K = 2, 37, 72
+    da, db, a, b = _views(M, N, K, dt, "trans_b", seed=N + 3, batch=B)
+    da, a = (da.float() * 0.1).to(dt), (a.float() * 0.1).to(dt)
+    c = torch.empty(B, M, N, dtype=out, device=dev)
+    tm.dot(da, db, c, "softmax")
+    ref = oracle.dot(_np(a), _np(b), "softmax")
+    rel = 2.0 ** -11 if out == torch.float16 else 2.0 ** -8
+    err = np.abs(c.double().cpu().numpy() - ref)
+    assert (err <= (1e-4 + rel) * ref + 1e-7).all(), f"max err {err.max():.3e}"
 
 
 @pytest.mark.parametrize("dt", [torch.float16, torch.float32])

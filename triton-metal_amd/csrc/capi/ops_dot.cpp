@@ -1,8 +1,8 @@
 // Typed entry point for tl.dot in general form (strided / transposed
 // operands, a batch dimension, FP8 inputs, epilogues): the dot_tile kernels
 // (MFMA, the none / add-* epilogues, and the product before dot_softmax_rows),
-// dot_chain (chain-dot) or dot_rows (every epilogue, any case the others do
-// not take).  Also the FP8 path of tm_matmul.
+// dot_softmax16 (softmax into other outputs, N <= 2048), dot_chain
+// (chain-dot) or dot_rows (every epilogue, any case the others do not take).  Also the FP8 path of tm_matmul.
 #include <cstring>
 
 #include "runtime.h"
@@ -138,6 +138,24 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
       if (rc) return rc;
       static Kernel ksm("dot_softmax_rows");
       return launch(ksm, dim3((unsigned)((long long)batch * M)), dim3(256), 0, stream, p);
+    }
+  }
+  // softmax into any other C (a 16-bit one: the product must not be rounded
+  // first) with rows of N <= 2048 and C sharing no memory with A or B:
+  // dot_softmax16 keeps 16 whole product rows on chip
+  if (epilogue == TM_EPI_SOFTMAX && K > 0 && N <= 2048 && batch <= 65535) {
+    uintptr_t al, ah, bl, bh, cl, chh;
+    const int isz = elem_size(in_dtype);
+    extent(A, isz, batch, M, K, st[0], st[1], st[2], &al, &ah);
+    extent(B, isz, batch, K, N, st[3], st[4], st[5], &bl, &bh);
+    extent(C, elem_size(out_dtype), batch, M, N, st[6], st[7], st[8], &cl, &chh);
+    if (!(cl < ah && al < chh) && !(cl < bh && bl < chh)) {
+      char name[32];
+      snprintf(name, sizeof name, "dot_softmax16_%s",
+               is_fp8(in_dtype) ? "fp8" : in_dtype == TM_DT_BF16 ? "bf16"
+               : in_dtype == TM_DT_F32 ? "f32" : "f16");
+      return launch(kernel_named(name), dim3((unsigned)((M + 15) / 16), (unsigned)batch),
+                    dim3(256), 0, stream, p);
     }
   }
   // chain-dot with C sharing no memory with A, B or W:

@@ -32,8 +32,9 @@
 // every epilogue.  The softmax and chain-dot epilogues need the whole row of
 // the product, which the workgroup keeps in LDS (N <= 8192); it also serves
 // K = 0 and a bias read in place across rows.  With an fp32 output the
-// softmax takes the tile kernels and dot_softmax_rows instead, and chain-dot
-// with C apart from its operands the fused dot_chain kernels.
+// softmax takes the tile kernels and dot_softmax_rows instead, with another
+// output and N <= 2048 dot_softmax16, and chain-dot with C apart from its
+// operands the fused dot_chain kernels.
 #include "common.h"
 
 enum { EPI_NONE = 0, EPI_ADD_MATRIX = 1, EPI_ADD_ROWS = 2, EPI_ADD_COLS = 3, EPI_SOFTMAX = 4,
@@ -706,9 +707,13 @@ extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) 
 // read on 64 distinct banks), W [2 chunks][64 n][64 + 16].
 // ----------------------------------------------------------------------------
 namespace {
-template <bool BF16, bool FP8, int BM, bool F32 = false>
+template <bool BF16, bool FP8, int BM, bool F32 = false, bool SMX = false>
 __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
-  constexpr int BN = 64, BK = 64, BL = 64, LDK = BK + (F32 ? 4 : 8), LDP = BN + 4, LDW = BL + 16;
+  // SMX: the softmax epilogue instead of chain-dot; P keeps whole rows of up
+  // to SMX_NMAX columns and no W is read
+  constexpr int SMX_NMAX = 2048;
+  constexpr int BN = 64, BK = 64, BL = 64, LDK = BK + (F32 ? 4 : 8);
+  constexpr int LDP = (SMX ? SMX_NMAX : BN) + 4, LDW = BL + 16;
   constexpr int RI = BM / 16;        // MFMA row tiles per wave
   constexpr int AE = BM * BK / 256;  // A elements per thread and step
   constexpr int BE = BN * BK / 256;  // B elements per thread and step
@@ -717,14 +722,14 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
   __shared__ __align__(16) lds_t As[BM * LDK];
   __shared__ __align__(16) lds_t Bs[BN * LDK];
   __shared__ __align__(16) float Ps[BM * LDP];
-  __shared__ __align__(16) float Ws[2][BN * LDW];
+  __shared__ __align__(16) float Ws[2][SMX ? 4 : BN * LDW];
   __shared__ uint16_t lut[256];
   using raw_t = typename std::conditional<F32, uint32_t,
                 typename std::conditional<FP8, uint8_t, uint16_t>::type>::type;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r16 = lane & 15;
-  const int tiles_l = (p.L + BL - 1) / BL;
+  const int tiles_l = SMX ? 1 : (p.L + BL - 1) / BL;
   const int m0 = (int)(blockIdx.x / tiles_l) * BM, l0 = (int)(blockIdx.x % tiles_l) * BL;
   const int b = blockIdx.y;
   if constexpr (FP8) lut[tid] = f32_to_f16_bits(fp8_to_f32((uint32_t)tid, p.in_dt));
@@ -779,7 +784,7 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
       b_at(e, n, k);
       rb[e] = Bb[(long long)min(n0 + n, p.N - 1) * p.sb_n + (long long)min(k0 + k, p.K - 1) * p.sb_k];
     }
-    {
+    if constexpr (!SMX) {
 #pragma unroll
       for (int e = 0; e < WE; ++e) {
         int n, l;
@@ -804,7 +809,7 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
       const uint32_t v = FP8 ? (uint32_t)lut[rb[e]] : rb[e];
       Bs[n * LDK + k] = (lds_t)(v & (0u - (uint32_t)(n0 + n < p.N && k0 + k < p.K)));
     }
-    if (is_last(s)) {
+    if (!SMX && is_last(s)) {
       float* ws = Ws[c & 1];
       // one dtype branch around the whole chunk, so the loop is straight-line
       auto put_w = [&](auto dtc) {
@@ -871,12 +876,14 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
 #pragma unroll
       for (int i = 0; i < RI; ++i) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) Ps[(16 * i + 4 * q + e) * LDP + 16 * wave + r16] = accp[i][e];
+        for (int e = 0; e < 4; ++e)
+          Ps[(16 * i + 4 * q + e) * LDP + (SMX ? (s / ksteps) * BN : 0) + 16 * wave + r16] =
+              accp[i][e];
         accp[i] = f4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
     __syncthreads();
-    if (last) {
+    if (!SMX && last) {
       const float* ws = Ws[(s / ksteps) & 1];
 #pragma unroll 4
       for (int kk = 0; kk < BN; kk += 4) {
@@ -900,6 +907,27 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
   }
 
   const long long cb = (long long)b * p.sc_b;
+  if constexpr (SMX) {
+    // softmax of each row, the arithmetic of dot_rows: exp(x - max) / sum;
+    // wave w takes rows w, w + 4, ..  (the last step's barrier ordered P)
+    for (int r = wave; r < BM; r += 4) {
+      const int m = m0 + r;
+      if (m >= p.M) break;
+      const float* pr = Ps + r * LDP;
+      float mx = -__builtin_inff();
+      for (int n = lane; n < p.N; n += 64) mx = fmaxf(mx, pr[n]);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      float sm = 0.0f;
+      for (int n = lane; n < p.N; n += 64) sm += expf(pr[n] - mx);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) sm += __shfl_xor(sm, o, 64);
+      const long long rb = cb + (long long)m * p.sc_m;
+      for (int n = lane; n < p.N; n += 64)
+        store_elem(p.C, rb + (long long)n * p.sc_n, p.out_dt, expf(pr[n] - mx) / sm);
+    }
+    return;
+  }
   const int l = l0 + 16 * wave + r16;
   if (l >= p.L) return;
 #pragma unroll
@@ -924,6 +952,18 @@ TM_DOT_CHAIN(dot_chain32_f16, false, false, 32, false)
 TM_DOT_CHAIN(dot_chain32_bf16, true, false, 32, false)
 TM_DOT_CHAIN(dot_chain32_fp8, false, true, 32, false)
 TM_DOT_CHAIN(dot_chain32_f32, false, false, 32, true)
+
+// dot_softmax16_<f16|bf16|fp8|f32>: the softmax epilogue for rows of N <=
+// 2048 on the same P pipeline (16-row blocks, grid (ceil(M / 16), batch)):
+// whole fp32 P rows in LDS, then each row's softmax into C in any dtype.
+#define TM_DOT_SOFTMAX(NAME, BF, F8, F32)                                        \
+  extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {         \
+    dot_chain_body<BF, F8, 16, F32, true>(p);                                   \
+  }
+TM_DOT_SOFTMAX(dot_softmax16_f16, false, false, false)
+TM_DOT_SOFTMAX(dot_softmax16_bf16, true, false, false)
+TM_DOT_SOFTMAX(dot_softmax16_fp8, false, true, false)
+TM_DOT_SOFTMAX(dot_softmax16_f32, false, false, true)
 
 // ----------------------------------------------------------------------------
 // dot_rows: grid batch * M, block 256.  Columns in groups of 1024 (4 per
