@@ -2,7 +2,8 @@
 // operands, a batch dimension, FP8 inputs, epilogues): the dot_tile kernels
 // (MFMA, the none / add-* epilogues, and the product before dot_softmax_rows),
 // dot_softmax16 (softmax into other outputs, N <= 2048), dot_chain
-// (chain-dot) or dot_rows (every epilogue, any case the others do not take).  Also the FP8 path of tm_matmul.
+// (chain-dot) or dot_rows (every epilogue, any case the others do not take).
+// Also the FP8 path of tm_matmul.
 #include <cstring>
 
 #include "runtime.h"
