@@ -117,7 +117,7 @@ def dot_general(dev, layout, dt_name, M, N, K, batch=None, epilogue="none"):
     take: "colmajor_a" (A stored [K, M]), "batched" (row-major [batch, M, K] @
     [batch, K, N]) or "trans_b" with an add-matrix epilogue; "row" with the
     chain-dot epilogue: (A @ B) @ W, W [N, L = K] in the input dtype, C [M, L]
-    in fp32."""
+    in fp32; "row" with the softmax epilogue into C in the input dtype."""
     import torch
     import triton_metal_amd as tm
     dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dt_name]
@@ -391,6 +391,8 @@ EXTRA = {"hbm_copy": hbm_copy,
                                                       epilogue="chain-dot"),
          "dot_fp16_chain_4096x1024x128": lambda d: dot_general(d, "row", "fp16", 4096, 1024, 128,
                                                                epilogue="chain-dot"),
+         "dot_fp16_softmax_4096x1024x128": lambda d: dot_general(d, "row", "fp16", 4096, 1024,
+                                                                 128, epilogue="softmax"),
          "dot_fp16_addmatrix_2048": lambda d: dot_general(d, "trans_b", "fp16", 2048, 2048, 2048,
                                                           epilogue="add-matrix"),
          "dot_fp32_colmajor_a_4096": lambda d: dot_general(d, "colmajor_a", "fp32", 4096, 4096, 4096),
