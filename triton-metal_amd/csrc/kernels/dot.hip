@@ -849,6 +849,7 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
                   const uint32_t* rb_p, const uint32_t* rw_p) {
     const bool last = is_last(s);
     load_step(ra_n, rb_n, rw_n, min(s + 2, nsteps - 1));
+    if (s >= nsteps) return;  // the loop's second step past the end: loads only
     if constexpr (F32) {
       // fp32 operands: v_mfma_f32_16x16x4_f32, lane l row l % 16, k kk + l / 16
 #pragma unroll
@@ -903,7 +904,7 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
   __syncthreads();
   for (int s = 0; s < nsteps; s += 2) {
     step(s, ra0, rb0, rw0, ra1, rb1, rw1);
-    if (s + 1 < nsteps) step(s + 1, ra1, rb1, rw1, ra0, rb0, rw0);
+    step(s + 1, ra1, rb1, rw1, ra0, rb0, rw0);
   }
 
   const long long cb = (long long)b * p.sc_b;
