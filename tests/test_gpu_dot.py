@@ -227,13 +227,15 @@ def test_dot_softmax_batched(dev, layout, out):
 @pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("N", [40, 700, 2048, 2049])
 @pytest.mark.parametrize("out", [torch.float16, torch.bfloat16])
-def test_dot_softmax_16bit_output(dev, dt, N, out):
+@pytest.mark.parametrize("layout", ["trans_b", "row"])
+def test_dot_softmax_16bit_output(dev, dt, N, out, layout):
     """softmax into a 16-bit C: rows of N <= 2048 on dot_softmax16 (16 whole
-    fp32 product rows on chip), N = 2049 on dot_rows; against the softmax of
-    the fp64 product, rounded once (half an ulp relative; fp16 subnormals
-    absolute)."""
+    fp32 product rows on chip; a row-major 16-bit B with N % 8 == 0 read in
+    16-byte pieces, N = 40 leaving most of its one chunk past N), N = 2049 on
+    dot_rows; against the softmax of the fp64 product, rounded once (half an
+    ulp relative; fp16 subnormals absolute)."""
     B, M, K = 2, 37, 72
-    da, db, a, b = _views(M, N, K, dt, "trans_b", seed=N + 3, batch=B)
+    da, db, a, b = _views(M, N, K, dt, layout, seed=N + 3, batch=B)
     da, a = (da.float() * 0.1).to(dt), (a.float() * 0.1).to(dt)
     c = torch.empty(B, M, N, dtype=out, device=dev)
     tm.dot(da, db, c, "softmax")

@@ -141,6 +141,11 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
       return launch(ksm, dim3((unsigned)((long long)batch * M)), dim3(256), 0, stream, p);
     }
   }
+  // dot_softmax16 / dot_chain read a 16-bit B that is row-contiguous in
+  // aligned 16-byte pieces (n contiguous) with 16-byte loads (the _vb forms)
+  const auto vec_b = [&]() {
+    return is_half(in_dtype) && fetch_mode(B, st[3], st[5], st[4], batch, 2) == MODE_RC;
+  };
   // softmax into any other C (a 16-bit one: the product must not be rounded
   // first) with rows of N <= 2048 and C sharing no memory with A or B:
   // dot_softmax16 keeps 16 whole product rows on chip
@@ -151,10 +156,10 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
     extent(B, isz, batch, K, N, st[3], st[4], st[5], &bl, &bh);
     extent(C, elem_size(out_dtype), batch, M, N, st[6], st[7], st[8], &cl, &chh);
     if (!(cl < ah && al < chh) && !(cl < bh && bl < chh)) {
-      char name[32];
-      snprintf(name, sizeof name, "dot_softmax16_%s",
+      char name[40];
+      snprintf(name, sizeof name, "dot_softmax16_%s%s",
                is_fp8(in_dtype) ? "fp8" : in_dtype == TM_DT_BF16 ? "bf16"
-               : in_dtype == TM_DT_F32 ? "f32" : "f16");
+               : in_dtype == TM_DT_F32 ? "f32" : "f16", vec_b() ? "_vb" : "");
       return launch(kernel_named(name), dim3((unsigned)((M + 15) / 16), (unsigned)batch),
                     dim3(256), 0, stream, p);
     }
@@ -175,10 +180,10 @@ int dot_impl(const char* op, const void* A, const void* B, void* C, const void* 
     const bool b32 = (long long)((M + 31) / 32) * tl * batch >= cu_count();
     const long long groups = (long long)((M + (b32 ? 31 : 15)) / (b32 ? 32 : 16)) * tl;
     if (apart(al, ah) && apart(bl, bh) && apart(wl, wh) && groups <= 0x7fffffffLL) {
-      char name[32];
-      snprintf(name, sizeof name, "dot_chain%d_%s", b32 ? 32 : 16,
+      char name[40];
+      snprintf(name, sizeof name, "dot_chain%d_%s%s", b32 ? 32 : 16,
                is_fp8(in_dtype) ? "fp8" : in_dtype == TM_DT_BF16 ? "bf16"
-               : in_dtype == TM_DT_F32 ? "f32" : "f16");
+               : in_dtype == TM_DT_F32 ? "f32" : "f16", vec_b() ? "_vb" : "");
       return launch(kernel_named(name), dim3((unsigned)groups, (unsigned)batch), dim3(256), 0,
                     stream, p);
     }

@@ -691,7 +691,8 @@ extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) 
 // fp32 and multiplied into the C tile on v_mfma_f32_16x16x4_f32 (wave w:
 // columns 16 w .. +15 of the C tile) against the chunk's W [64][64] (any
 // input dtype, as fp32).  Every operand is read by element loads whose lane
-// order follows its smaller stride, at addresses clamped into the operand
+// order follows its smaller stride (the _vb forms: a 16-bit B row-contiguous
+// in aligned pieces by 16-byte loads, as dot_tile's RC operands), at addresses clamped into the operand
 // (W: the aligned 4-byte word holding the element, decoded at the LDS
 // store); the LDS store zeroes the elements past the operand.  Loads run two
 // steps ahead in two register sets, since a step holds few MFMAs; every step
@@ -707,8 +708,12 @@ extern "C" __global__ __launch_bounds__(256) void dot_softmax_rows(DotParams p) 
 // read on 64 distinct banks), W [2 chunks][64 n][64 + 16].
 // ----------------------------------------------------------------------------
 namespace {
-template <bool BF16, bool FP8, int BM, bool F32 = false, bool SMX = false>
+template <bool BF16, bool FP8, int BM, bool F32 = false, bool SMX = false, bool VB = false>
 __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
+  // VB: 16-bit B row-contiguous (n) in aligned 16-byte pieces of 8 n at one k,
+  // two per thread and step (piece h: k (tid + 256 h) / 8, n 8 (tid % 8) .. +7),
+  // kept in rb[4 h .. 4 h + 3]
+  static_assert(!VB || (!FP8 && !F32), "B pieces of 8 halves");
   // SMX: the softmax epilogue instead of chain-dot; P keeps whole rows of up
   // to SMX_NMAX columns and no W is read
   constexpr int SMX_NMAX = 2048;
@@ -778,11 +783,21 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
       a_at(e, r, k);
       ra[e] = Ab[(long long)min(m0 + r, p.M - 1) * p.sa_m + (long long)min(k0 + k, p.K - 1) * p.sa_k];
     }
+    if constexpr (VB) {
 #pragma unroll
-    for (int e = 0; e < BE; ++e) {
-      int n, k;
-      b_at(e, n, k);
-      rb[e] = Bb[(long long)min(n0 + n, p.N - 1) * p.sb_n + (long long)min(k0 + k, p.K - 1) * p.sb_k];
+      for (int h = 0; h < 2; ++h) {
+        const int pc = tid + 256 * h, k = pc >> 3, n8 = 8 * (pc & 7);
+        const u4_t w = ldg128(Bb + (long long)min(n0 + n8, (p.N - 1) & ~7) +
+                              (long long)min(k0 + k, p.K - 1) * p.sb_k);
+        rb[4 * h] = w.x; rb[4 * h + 1] = w.y; rb[4 * h + 2] = w.z; rb[4 * h + 3] = w.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < BE; ++e) {
+        int n, k;
+        b_at(e, n, k);
+        rb[e] = Bb[(long long)min(n0 + n, p.N - 1) * p.sb_n + (long long)min(k0 + k, p.K - 1) * p.sb_k];
+      }
     }
     if constexpr (!SMX) {
 #pragma unroll
@@ -802,12 +817,25 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
       const uint32_t v = FP8 ? (uint32_t)lut[ra[e]] : ra[e];
       As[r * LDK + k] = (lds_t)(v & (0u - (uint32_t)(m0 + r < p.M && k0 + k < p.K)));
     }
+    if constexpr (VB) {
 #pragma unroll
-    for (int e = 0; e < BE; ++e) {
-      int n, k;
-      b_at(e, n, k);
-      const uint32_t v = FP8 ? (uint32_t)lut[rb[e]] : rb[e];
-      Bs[n * LDK + k] = (lds_t)(v & (0u - (uint32_t)(n0 + n < p.N && k0 + k < p.K)));
+      for (int h = 0; h < 2; ++h) {
+        const int pc = tid + 256 * h, k = pc >> 3, n8 = 8 * (pc & 7);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t v = rb[4 * h + (e >> 1)] >> (16 * (e & 1));
+          Bs[(n8 + e) * LDK + k] =
+              (lds_t)(v & (0u - (uint32_t)(n0 + n8 + e < p.N && k0 + k < p.K)));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < BE; ++e) {
+        int n, k;
+        b_at(e, n, k);
+        const uint32_t v = FP8 ? (uint32_t)lut[rb[e]] : rb[e];
+        Bs[n * LDK + k] = (lds_t)(v & (0u - (uint32_t)(n0 + n < p.N && k0 + k < p.K)));
+      }
     }
     if (!SMX && is_last(s)) {
       float* ws = Ws[c & 1];
@@ -945,6 +973,17 @@ __device__ __forceinline__ void dot_chain_body(const DotParams& p) {
   extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {         \
     dot_chain_body<BF, F8, BM, F32>(p);                                         \
   }
+// _vb: 16-bit B row-contiguous in aligned 16-byte pieces
+#define TM_DOT_CHAIN_VB(NAME, BF, BM, SMX)                                       \
+  extern "C" __global__ __launch_bounds__(256) void NAME(DotParams p) {         \
+    dot_chain_body<BF, false, BM, false, SMX, true>(p);                         \
+  }
+TM_DOT_CHAIN_VB(dot_chain16_f16_vb, false, 16, false)
+TM_DOT_CHAIN_VB(dot_chain16_bf16_vb, true, 16, false)
+TM_DOT_CHAIN_VB(dot_chain32_f16_vb, false, 32, false)
+TM_DOT_CHAIN_VB(dot_chain32_bf16_vb, true, 32, false)
+TM_DOT_CHAIN_VB(dot_softmax16_f16_vb, false, 16, true)
+TM_DOT_CHAIN_VB(dot_softmax16_bf16_vb, true, 16, true)
 TM_DOT_CHAIN(dot_chain16_f16, false, false, 16, false)
 TM_DOT_CHAIN(dot_chain16_bf16, true, false, 16, false)
 TM_DOT_CHAIN(dot_chain16_fp8, false, true, 16, false)
