@@ -305,6 +305,23 @@ def test_dot_chain_fused_fp8(dev, fmt):
     _chain_check(c, ref.reshape(c.shape), (np.abs(av) @ np.abs(bv)) @ np.abs(_np(w)))
 
 
+@pytest.mark.parametrize("fmt", FP8)
+@pytest.mark.parametrize("wlayout", ["row", "col"])
+def test_dot_chain_fp8_w(dev, fmt, wlayout):
+    """chain-dot with fp16 operands and an FP8 W (codes over the whole format):
+    the fused kernel loads the aligned 4-byte word holding each code and
+    decodes the code at its byte offset (all four occur in both layouts)."""
+    M, N, K, L = 40, 90, 48, 37
+    da, db, a, b = _views(M, N, K, torch.float16, "row", seed=89)
+    w = _fp8_codes((N, L), fmt, 97)
+    dw = w.to(dev) if wlayout == "row" else w.t().contiguous().to(dev).t()
+    c = torch.empty(M, L, dtype=torch.float32, device=dev)
+    tm.dot(da, db, c, "chain-dot", w=dw, fp8_format=fmt)
+    wv = oracle.fp8_decode(w.numpy(), fmt)
+    ref = oracle.dot(_np(a), _np(b), "chain-dot", W=wv)
+    _chain_check(c, ref, (np.abs(_np(a)) @ np.abs(_np(b))) @ np.abs(wv))
+
+
 def _fp8_codes(shape, fmt, seed):
     """Codes over the whole format, NaN / inf codes replaced by 0."""
     c = torch.randint(0, 256, shape, generator=_gen(seed), dtype=torch.uint8)
